@@ -1,0 +1,160 @@
+"""Decode throughput of the random-init Qwen3.5-0.8B-shape hybrid model (Q4)
+on one MI355X at 32K / 64K / 128K context, with the HBM roofline fraction and
+a CPU baseline from the oracle.
+
+A step is one greedy decode token through all 24 layers and the vocab head
+(one replay of the captured decode graph). The KV caches and GDN states are a
+synthetic context (N(0,1) KV rows, N(0,0.1) states) so no prefill runs before
+timing; weights are the seeded random-init model. `value` is decode tok/s at
+the 128K context; 32K and 64K are reported alongside.
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+PKG = os.path.join(ROOT, "enginesmith-qwen35-08b-long-decode-m5max-round005_amd")
+sys.path.insert(0, PKG)
+import esdecode as E  # noqa: E402
+
+N_LAYERS, VOCAB = 24, 248320
+HBM_PEAK = 8.0e12
+GDN_STATE_BYTES = 18 * 2 * 16 * 128 * 128 * 4      # fp32 state read + write
+CONV_HISTORY_BYTES = 18 * 73728                      # history read + write (reference byte model)
+KV_BYTES_PER_POS = 6 * 2 * 2 * 256 * 2               # 6 layers x {K,V} x 2 heads x 256 x bf16
+
+
+def weight_bytes():
+    lay = E.weights_layout(N_LAYERS, VOCAB)
+    return sum(b for _, _, b, _ in lay) + 576        # + the embedding row gathered per token
+
+
+def bytes_per_token(ctx, w):
+    return w + GDN_STATE_BYTES + CONV_HISTORY_BYTES + KV_BYTES_PER_POS * ctx
+
+
+def cpu_baseline(blob, ctx, steps):
+    """Oracle decode steps at context `ctx` on the host cores (bounded sample)."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle as O
+    cores = os.cpu_count() or 1
+    threads = min(cores, 16)
+    O.set_threads(threads)
+    views = E.tensor_views(blob, N_LAYERS, VOCAB)
+    m = O.OracleModel(views, N_LAYERS, VOCAB, capacity=ctx + steps + 1)
+    r = np.random.default_rng(7)
+    tile = O.f32_to_bf16(r.normal(0, 1, 1 << 20).astype(np.float32))
+    for l in m.kcache:
+        for arr in (m.kcache[l], m.vcache[l]):
+            flat = arr.reshape(-1)
+            n = 2 * (ctx + steps + 1) * 256
+            reps = -(-n // tile.size)
+            flat[:] = np.tile(tile, reps)[:n]
+    for l in m.state:
+        m.state[l][...] = r.normal(0, 0.1, m.state[l].shape).astype(np.float32)
+    m.position = ctx
+    tok = 1
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        tok = m.step(tok)
+    dt = time.perf_counter() - t0
+    return dict(value=steps / dt, unit="tok/s", cores=threads, kind="port",
+                sample=f"{steps} oracle decode steps of the 24-layer model at {ctx} context, "
+                       f"{threads} OpenMP threads on {cores} host cores")
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=64)
+    ap.add_argument("--warmup", type=int, default=8)
+    ap.add_argument("--contexts", default="32768,65536,131072")
+    ap.add_argument("--cpu-steps", type=int, default=2)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--attn-reps", type=int, default=20)
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this engine runs on one GPU; multi-GPU decode is not built "
+                                   "(see DESIGN.md for how the path would shard)"}))
+        sys.exit(2)
+    if E.device_count() < 1:
+        print(json.dumps({"error": "no GPU visible"}))
+        sys.exit(1)
+
+    contexts = [int(c) for c in args.contexts.split(",")]
+    seed = 20260101
+    t0 = time.perf_counter()
+    blob = E.random_weights(N_LAYERS, VOCAB, seed, threads=min(os.cpu_count() or 8, 16))
+    gen_s = time.perf_counter() - t0
+    cap = max(contexts) + args.steps + args.warmup + 16
+    eng = E.Engine(blob, N_LAYERS, VOCAB, capacity=cap)
+    w = weight_bytes()
+    per_ctx = {}
+    for ctx in contexts:
+        start = ctx - args.warmup - args.steps // 2
+        eng.fill_synthetic(start, seed=ctx, pending=1)
+        ms = eng.time_decode(args.steps, args.warmup)
+        tps = args.steps / (ms / 1e3)
+        b = bytes_per_token(ctx, w)
+        per_ctx[ctx] = dict(tok_s=round(tps, 1), ms_per_step=round(ms / args.steps, 4),
+                            bytes_per_token=b, achieved_GBs=round(b * tps / 1e9, 1),
+                            roofline_frac=round(b * tps / HBM_PEAK, 4))
+        print(f"# ctx {ctx}: {tps:.1f} tok/s, {ms / args.steps * 1e3:.1f} us/step, "
+              f"{b * tps / 1e9:.0f} GB/s ({b * tps / HBM_PEAK * 100:.1f}% of 8 TB/s)", file=sys.stderr, flush=True)
+    head_ctx = max(contexts)
+    # dominant kernel: split-K attention of one layer at the headline context
+    eng.fill_synthetic(head_ctx - 1, seed=1, pending=1)
+    attn_ms = eng.time_attention(3, args.attn_reps)
+    attn_bytes = KV_BYTES_PER_POS // 6 * head_ctx + 8 * 512 * 2
+    head_ms = eng.time_head(args.attn_reps)
+    eng.close()
+
+    cpu = None
+    if not args.no_cpu:
+        cpu = cpu_baseline(blob, head_ctx, args.cpu_steps)
+
+    main_ctx = per_ctx[head_ctx]
+    line = {
+        "metric": "decode tok/s at 32K/64K/128K ctx on 1 MI355X; % of HBM roofline",
+        "value": main_ctx["tok_s"],
+        "unit": "tok/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": main_ctx["ms_per_step"],
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "q4-affine weights, bf16 activations, fp32 accumulate",
+        "data": "synthetic: seeded random-init weights, N(0,1) KV context, N(0,0.1) GDN states",
+        "config": {
+            "workload": f"batch-1 greedy decode, Qwen3.5-0.8B-shape hybrid (18 GDN + 6 GQA layers, Q4 g64), "
+                        f"{head_ctx} context",
+            "n_layers": N_LAYERS, "vocab": VOCAB, "contexts": contexts,
+            "per_context": {str(k): v for k, v in per_ctx.items()},
+            "step_roofline_frac_8TBs": main_ctx["roofline_frac"],
+            "weight_gen_s": round(gen_s, 1),
+            "head_kernel_us": round(head_ms * 1e3, 2),
+        },
+        "roofline": {
+            "kernel": "k_attn_split (one attention layer, split-K decode)",
+            "bound": "hbm",
+            "achieved": round(attn_bytes / (attn_ms / 1e3) / 1e9, 1),
+            "peak": 8000.0,
+            "unit": "GB/s",
+            "frac": round(attn_bytes / (attn_ms / 1e3) / HBM_PEAK, 4),
+            "traffic": None,
+            "launch_us": round(attn_ms * 1e3, 2),
+            "algorithmic_bytes": attn_bytes,
+        },
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

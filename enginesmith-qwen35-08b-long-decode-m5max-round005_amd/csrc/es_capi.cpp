@@ -1,0 +1,382 @@
+// extern "C" entry points declared in include/es_decode.h.
+#include "../../include/es_decode.h"
+
+#include <hip/hip_runtime.h>
+
+#include <cstring>
+#include <string>
+
+#include "es_engine.hpp"
+#include "es_kernels.hpp"
+#include "es_weights.hpp"
+
+struct es_engine {
+  es::Engine* impl;
+};
+
+namespace {
+
+thread_local std::string g_error;
+
+int fail(int code, const std::string& msg) {
+  g_error = msg;
+  return code;
+}
+
+int hip_status(hipError_t e, const char* what) {
+  if (e == hipSuccess) return ES_OK;
+  if (e == hipErrorInvalidValue) return fail(ES_ERR_INVALID, std::string(what) + ": invalid arguments or shapes");
+  return fail(ES_ERR_DEVICE, std::string(what) + ": " + hipGetErrorString(e));
+}
+
+bool to_q4(const es_q4* in, es::Q4* out) {
+  if (!in) return false;
+  *out = es::Q4{in->codes, in->scales, in->biases, in->n, in->k};
+  return in->codes && in->scales && in->biases && in->n > 0 && in->k > 0;
+}
+
+hipStream_t S(void* s) { return static_cast<hipStream_t>(s); }
+
+int engine_rc(int rc, const std::string& err) {
+  if (rc == 0) return ES_OK;
+  if (rc == 3) return fail(ES_ERR_CANCELLED, err);
+  if (rc == 2) return fail(ES_ERR_DEVICE, err);
+  return fail(ES_ERR_INVALID, err);
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* es_last_error(void) { return g_error.c_str(); }
+
+// ---- plumbing ----
+int es_device_count(int* count) {
+  if (!count) return fail(ES_ERR_INVALID, "null count");
+  int n = 0;
+  hipError_t e = hipGetDeviceCount(&n);
+  if (e != hipSuccess) n = 0;
+  *count = n;
+  return ES_OK;
+}
+int es_device_name(int device, char* buf, int len) {
+  if (!buf || len <= 0) return fail(ES_ERR_INVALID, "null buffer");
+  hipDeviceProp_t p;
+  if (int rc = hip_status(hipGetDeviceProperties(&p, device), "hipGetDeviceProperties")) return rc;
+  std::snprintf(buf, len, "%s (%s, %d CUs)", p.name, p.gcnArchName, p.multiProcessorCount);
+  return ES_OK;
+}
+int es_set_device(int device) { return hip_status(hipSetDevice(device), "hipSetDevice"); }
+int es_malloc(void** ptr, size_t bytes) {
+  if (!ptr) return fail(ES_ERR_INVALID, "null ptr");
+  return hip_status(hipMalloc(ptr, bytes ? bytes : 1), "hipMalloc");
+}
+int es_free(void* ptr) { return hip_status(hipFree(ptr), "hipFree"); }
+int es_memcpy_htod(void* dst, const void* src, size_t bytes) {
+  return hip_status(hipMemcpy(dst, src, bytes, hipMemcpyHostToDevice), "hipMemcpy H2D");
+}
+int es_memcpy_dtoh(void* dst, const void* src, size_t bytes) {
+  return hip_status(hipMemcpy(dst, src, bytes, hipMemcpyDeviceToHost), "hipMemcpy D2H");
+}
+int es_memset(void* dst, int value, size_t bytes) {
+  return hip_status(hipMemset(dst, value, bytes), "hipMemset");
+}
+int es_synchronize(void) { return hip_status(hipDeviceSynchronize(), "hipDeviceSynchronize"); }
+int es_stream_create(void** stream) {
+  if (!stream) return fail(ES_ERR_INVALID, "null stream");
+  hipStream_t s;
+  if (int rc = hip_status(hipStreamCreateWithFlags(&s, hipStreamNonBlocking), "hipStreamCreate"))
+    return rc;
+  *stream = s;
+  return ES_OK;
+}
+int es_stream_destroy(void* stream) { return hip_status(hipStreamDestroy(S(stream)), "hipStreamDestroy"); }
+int es_stream_synchronize(void* stream) {
+  return hip_status(hipStreamSynchronize(S(stream)), "hipStreamSynchronize");
+}
+
+// ---- LINEAR ----
+int es_embedding_q4(const es_q4* table, const uint32_t* token, uint16_t* out, void* stream) {
+  es::Q4 t;
+  if (!to_q4(table, &t) || t.k != 1024) return fail(ES_ERR_INVALID, "es_embedding_q4: table must be [n,1024] Q4");
+  return hip_status(es::launch_embedding(t, token, out, S(stream)), "es_embedding_q4");
+}
+
+int es_q4_matvec(const es_q4* w, const uint16_t* x, uint16_t* y, float* y_f32, void* stream) {
+  es::Q4 m;
+  if (!to_q4(w, &m)) return fail(ES_ERR_INVALID, "es_q4_matvec: null weight");
+  return hip_status(es::launch_qmv(m, x, nullptr, y, y_f32, S(stream)), "es_q4_matvec");
+}
+
+int es_q4_matvec_add(const es_q4* w, const uint16_t* x, const uint16_t* residual, uint16_t* y,
+                     void* stream) {
+  es::Q4 m;
+  if (!to_q4(w, &m) || !residual) return fail(ES_ERR_INVALID, "es_q4_matvec_add: null argument");
+  if (x == y) return fail(ES_ERR_INVALID, "es_q4_matvec_add: x must not alias y");
+  return hip_status(es::launch_qmv(m, x, residual, y, nullptr, S(stream)), "es_q4_matvec_add");
+}
+
+int es_q4_rmsnorm_matvec_multi(const es_q4* w, int count, const uint16_t* x, const uint16_t* gain,
+                               uint16_t* norm_out, uint16_t* const* y, void* stream) {
+  if (count < 1 || count > 4 || !w || !y || !x) return fail(ES_ERR_INVALID, "es_q4_rmsnorm_matvec_multi: bad count/pointers");
+  es::NormMultiArgs a{};
+  a.count = count;
+  for (int i = 0; i < count; ++i) {
+    if (!to_q4(&w[i], &a.m[i])) return fail(ES_ERR_INVALID, "es_q4_rmsnorm_matvec_multi: null weight");
+    a.y[i] = y[i];
+  }
+  a.x = x;
+  a.gain = gain;
+  a.norm_out = norm_out;
+  return hip_status(es::launch_norm_multi(a, S(stream)), "es_q4_rmsnorm_matvec_multi");
+}
+
+int es_q4_rmsnorm_gate_up_swiglu(const es_q4* gate, const es_q4* up, const uint16_t* x,
+                                 const uint16_t* gain, uint16_t* norm_out, uint16_t* act,
+                                 void* stream) {
+  es::Q4 g, u;
+  if (!to_q4(gate, &g) || !to_q4(up, &u)) return fail(ES_ERR_INVALID, "es_q4_rmsnorm_gate_up_swiglu: null weight");
+  return hip_status(es::launch_norm_gate_up(g, u, x, gain, norm_out, act, S(stream)),
+                    "es_q4_rmsnorm_gate_up_swiglu");
+}
+
+// ---- GDN ----
+int es_gdn_in_proj(const es_q4* qkv, const es_q4* z, const es_q4* a, const es_q4* b,
+                   const uint16_t* x, const uint16_t* gain, uint16_t* norm_out, uint16_t* ring,
+                   int position, uint16_t* z_out, uint16_t* ab_out, void* stream) {
+  es::NormMultiArgs n{};
+  n.count = 4;
+  if (!to_q4(qkv, &n.m[0]) || !to_q4(z, &n.m[1]) || !to_q4(a, &n.m[2]) || !to_q4(b, &n.m[3]))
+    return fail(ES_ERR_INVALID, "es_gdn_in_proj: null weight");
+  if (n.m[0].n != 6144 || n.m[1].n != 2048 || n.m[2].n != 16 || n.m[3].n != 16)
+    return fail(ES_ERR_INVALID, "es_gdn_in_proj: expected qkv 6144, z 2048, a 16, b 16 rows");
+  if (position < 0 || !ring || !z_out || !ab_out) return fail(ES_ERR_INVALID, "es_gdn_in_proj: bad position/pointers");
+  n.y[0] = ring;
+  n.y[1] = z_out;
+  n.y[2] = ab_out;
+  n.y[3] = ab_out + 16;
+  n.ring0 = 1;
+  n.pos_val = position;
+  n.x = x;
+  n.gain = gain;
+  n.norm_out = norm_out;
+  return hip_status(es::launch_norm_multi(n, S(stream)), "es_gdn_in_proj");
+}
+
+int es_gdn_recur_step(const uint16_t* ring, int position, const uint16_t* conv_w,
+                      const uint16_t* ab, const float* a_log, const uint16_t* dt_bias,
+                      float* state, uint16_t* y, uint16_t* qkv_out, float* g_out,
+                      uint16_t* beta_out, void* stream) {
+  if (position < 0) return fail(ES_ERR_INVALID, "es_gdn_recur_step: negative position");
+  es::GdnRecurArgs g{};
+  g.ring = ring;
+  g.conv_w = conv_w;
+  g.ab = ab;
+  g.a_log = a_log;
+  g.dt_bias = dt_bias;
+  g.state = state;
+  g.y = y;
+  g.qkv_out = qkv_out;
+  g.g_out = g_out;
+  g.beta_out = beta_out;
+  g.pos_val = position;
+  return hip_status(es::launch_gdn_recur(g, S(stream)), "es_gdn_recur_step");
+}
+
+int es_gdn_gate_out_proj(const es_q4* out_proj, const uint16_t* y, const uint16_t* z,
+                         const uint16_t* norm_w, uint16_t* h, uint16_t* gated_out, void* stream) {
+  es::Q4 m;
+  if (!to_q4(out_proj, &m)) return fail(ES_ERR_INVALID, "es_gdn_gate_out_proj: null weight");
+  return hip_status(es::launch_gdn_gate_out(m, y, z, norm_w, h, gated_out, S(stream)),
+                    "es_gdn_gate_out_proj");
+}
+
+// ---- attention ----
+int es_rope_inv_freq(float* host_out32) {
+  if (!host_out32) return fail(ES_ERR_INVALID, "null output");
+  for (int i = 0; i < 32; ++i) host_out32[i] = es::rope_inv_freq_host(i);
+  return ES_OK;
+}
+
+size_t es_attn_scratch_bytes(int splits) {
+  if (splits < 1 || splits > 1024) return 0;
+  return es::attn_scratch_bytes(splits);
+}
+
+int es_attn_decode(const uint16_t* q_proj, const uint16_t* k_proj, const uint16_t* v_proj,
+                   const uint16_t* q_gain, const uint16_t* k_gain, uint16_t* kcache,
+                   uint16_t* vcache, int capacity, int position, const float* inv_freq,
+                   int splits, void* scratch, size_t scratch_bytes, uint16_t* gated,
+                   uint16_t* query_out, void* stream) {
+  if (splits < 1 || splits > 1024) return fail(ES_ERR_INVALID, "es_attn_decode: splits must be 1..1024");
+  if (position < 0 || position >= capacity) return fail(ES_ERR_INVALID, "es_attn_decode: position outside capacity");
+  if (!scratch || scratch_bytes < es::attn_scratch_bytes(splits))
+    return fail(ES_ERR_INVALID, "es_attn_decode: scratch too small");
+  es::AttnArgs a{};
+  a.q_proj = q_proj;
+  a.k_proj = k_proj;
+  a.v_proj = v_proj;
+  a.q_gain = q_gain;
+  a.k_gain = k_gain;
+  a.kcache = kcache;
+  a.vcache = vcache;
+  a.capacity = capacity;
+  a.inv_freq = inv_freq;
+  a.part_o = static_cast<float*>(scratch);
+  a.part_ml = a.part_o + (size_t)8 * splits * 256;
+  a.splits = splits;
+  a.gated = gated;
+  a.query_out = query_out;
+  a.pos_val = position;
+  if (int rc = hip_status(es::launch_attn_split(a, S(stream)), "es_attn_decode split")) return rc;
+  return hip_status(es::launch_attn_merge(a, S(stream)), "es_attn_decode merge");
+}
+
+// ---- head ----
+size_t es_head_scratch_bytes(int vocab) {
+  if (vocab < 1) return 0;
+  return es::head_scratch_bytes(vocab);
+}
+
+int es_head_greedy(const es_q4* embed, const uint16_t* h, const uint16_t* gain,
+                   uint16_t* norm_out, uint16_t* logits, void* scratch, size_t scratch_bytes,
+                   uint32_t* token, float* lse, void* stream) {
+  es::HeadArgs a{};
+  if (!to_q4(embed, &a.embed) || a.embed.k != 1024) return fail(ES_ERR_INVALID, "es_head_greedy: table must be [vocab,1024] Q4");
+  if (!scratch || scratch_bytes < es::head_scratch_bytes(a.embed.n))
+    return fail(ES_ERR_INVALID, "es_head_greedy: scratch too small");
+  a.h = h;
+  a.gain = gain;
+  a.norm_out = norm_out;
+  a.logits = logits;
+  a.part = static_cast<float*>(scratch);
+  a.token_out = token;
+  a.lse_out = lse;
+  return hip_status(es::launch_head(a, S(stream)), "es_head_greedy");
+}
+
+// ---- weights ----
+size_t es_weights_total_bytes(int n_layers, int vocab) {
+  if (n_layers < 1 || vocab < 1) return 0;
+  uint64_t total = 0;
+  es::weight_layout({n_layers, vocab}, &total);
+  return total;
+}
+
+int es_weights_tensor_count(int n_layers) {
+  if (n_layers < 1) return 0;
+  return (int)es::weight_layout({n_layers, 1}, nullptr).size();
+}
+
+int es_weights_tensor_info(int n_layers, int vocab, int index, char* name, int name_len,
+                           uint64_t* offset, uint64_t* bytes, int* dtype) {
+  if (n_layers < 1 || vocab < 1) return fail(ES_ERR_INVALID, "bad model shape");
+  const auto t = es::weight_layout({n_layers, vocab}, nullptr);
+  if (index < 0 || index >= (int)t.size()) return fail(ES_ERR_INVALID, "tensor index out of range");
+  if (name && name_len > 0) {
+    std::strncpy(name, t[index].name.c_str(), name_len - 1);
+    name[name_len - 1] = 0;
+  }
+  if (offset) *offset = t[index].offset;
+  if (bytes) *bytes = t[index].bytes;
+  if (dtype) *dtype = (int)t[index].dtype;
+  return ES_OK;
+}
+
+int es_weights_random(int n_layers, int vocab, uint64_t seed, void* blob, size_t bytes,
+                      int threads) {
+  if (n_layers < 1 || vocab < 1) return fail(ES_ERR_INVALID, "bad model shape");
+  if (!es::weights_random({n_layers, vocab}, seed, blob, bytes, threads))
+    return fail(ES_ERR_INVALID, "es_weights_random: blob too small");
+  return ES_OK;
+}
+
+// ---- engine ----
+es_engine* es_engine_create(const void* blob, size_t bytes, int n_layers, int vocab,
+                            int capacity) {
+  std::string err;
+  es::Engine* e = es::Engine::create(blob, bytes, n_layers, vocab, capacity, &err);
+  if (!e) {
+    fail(ES_ERR_INVALID, err);
+    return nullptr;
+  }
+  return new es_engine{e};
+}
+
+void es_engine_destroy(es_engine* e) {
+  if (!e) return;
+  delete e->impl;
+  delete e;
+}
+
+int es_engine_generate(es_engine* e, const uint32_t* prompt, int len, int max_tokens, int reset,
+                       uint32_t* out) {
+  if (!e || !out) return fail(ES_ERR_INVALID, "null engine/output");
+  std::string err;
+  return engine_rc(e->impl->generate(prompt, len, max_tokens, reset != 0, out, &err), err);
+}
+
+void es_engine_cancel(es_engine* e) {
+  if (e) e->impl->cancel();
+}
+void es_engine_clear_cancel(es_engine* e) {
+  if (e) e->impl->clear_cancel();
+}
+int es_engine_position(const es_engine* e) { return e ? e->impl->position() : -1; }
+
+int es_engine_forced_decode(es_engine* e, const uint32_t* tokens, int n, uint32_t* argmax,
+                            uint16_t* logits) {
+  if (!e) return fail(ES_ERR_INVALID, "null engine");
+  std::string err;
+  return engine_rc(e->impl->forced_decode(tokens, n, argmax, logits, &err), err);
+}
+
+int es_engine_read_kv(es_engine* e, int layer, int which, int pos0, int count, void* host) {
+  if (!e) return fail(ES_ERR_INVALID, "null engine");
+  std::string err;
+  return engine_rc(e->impl->read_kv(layer, which, pos0, count, host, &err), err);
+}
+int es_engine_write_kv(es_engine* e, int layer, int which, int pos0, int count,
+                       const void* host) {
+  if (!e) return fail(ES_ERR_INVALID, "null engine");
+  std::string err;
+  return engine_rc(e->impl->write_kv(layer, which, pos0, count, host, &err), err);
+}
+int es_engine_read_gdn(es_engine* e, int layer, void* ring, void* state) {
+  if (!e) return fail(ES_ERR_INVALID, "null engine");
+  std::string err;
+  return engine_rc(e->impl->read_gdn(layer, ring, state, &err), err);
+}
+int es_engine_write_gdn(es_engine* e, int layer, const void* ring, const void* state) {
+  if (!e) return fail(ES_ERR_INVALID, "null engine");
+  std::string err;
+  return engine_rc(e->impl->write_gdn(layer, ring, state, &err), err);
+}
+int es_engine_set_position(es_engine* e, int position, uint32_t pending) {
+  if (!e) return fail(ES_ERR_INVALID, "null engine");
+  std::string err;
+  return engine_rc(e->impl->set_position(position, pending, &err), err);
+}
+int es_engine_fill_synthetic(es_engine* e, int length, uint64_t seed, uint32_t pending) {
+  if (!e) return fail(ES_ERR_INVALID, "null engine");
+  std::string err;
+  return engine_rc(e->impl->fill_synthetic(length, seed, pending, &err), err);
+}
+int es_engine_time_decode(es_engine* e, int steps, int warmup, double* ms_total) {
+  if (!e || !ms_total) return fail(ES_ERR_INVALID, "null engine/output");
+  std::string err;
+  return engine_rc(e->impl->time_decode(steps, warmup, ms_total, &err), err);
+}
+int es_engine_time_attention(es_engine* e, int layer, int reps, double* ms_avg) {
+  if (!e || !ms_avg) return fail(ES_ERR_INVALID, "null engine/output");
+  std::string err;
+  return engine_rc(e->impl->time_attention(layer, reps, ms_avg, &err), err);
+}
+int es_engine_time_head(es_engine* e, int reps, double* ms_avg) {
+  if (!e || !ms_avg) return fail(ES_ERR_INVALID, "null engine/output");
+  std::string err;
+  return engine_rc(e->impl->time_head(reps, ms_avg, &err), err);
+}
+int es_engine_splits_for(int length) { return es::Engine::splits_for(length); }
+
+}  // extern "C"

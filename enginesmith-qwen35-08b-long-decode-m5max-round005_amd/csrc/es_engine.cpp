@@ -1,0 +1,625 @@
+// Decode engine implementation (see es_engine.hpp).
+#include "es_engine.hpp"
+
+#include <algorithm>
+#include <cstring>
+#include <map>
+
+namespace es {
+
+namespace {
+
+constexpr int kKindDecode = 0;  // layers + vocab head (advances via the head)
+constexpr int kKindPrompt = 1;  // layers + advance (prompt consumption)
+
+#define ES_HIP(expr, what)                                                 \
+  do {                                                                     \
+    hipError_t e_ = (expr);                                                \
+    if (e_ != hipSuccess) {                                                \
+      if (err) *err = std::string(what) + ": " + hipGetErrorString(e_);    \
+      return 2;                                                            \
+    }                                                                      \
+  } while (0)
+
+}  // namespace
+
+int Engine::splits_for(int length) { return length < 8192 ? 32 : 256; }
+
+Engine* Engine::create(const void* blob, uint64_t bytes, int n_layers, int vocab, int capacity,
+                       std::string* err) {
+  if (n_layers < 1 || n_layers > 64 || vocab < 1 || vocab > (1 << 24) || capacity < 4 ||
+      capacity > (1 << 22)) {
+    if (err) *err = "invalid engine configuration";
+    return nullptr;
+  }
+  Engine* e = new Engine();
+  e->shape_ = {n_layers, vocab};
+  e->capacity_ = capacity;
+  if (e->init(blob, bytes, err) != 0) {
+    delete e;
+    return nullptr;
+  }
+  return e;
+}
+
+Engine::~Engine() {
+  if (stream_) (void)hipStreamSynchronize(stream_);
+  for (auto& g : graphs_) {
+    (void)hipGraphExecDestroy(g.exec);
+    (void)hipGraphDestroy(g.g);
+  }
+  for (void* p : allocations_) (void)hipFree(p);
+  if (stream_) (void)hipStreamDestroy(stream_);
+}
+
+int Engine::init(const void* blob, uint64_t bytes, std::string* err) {
+  uint64_t total = 0;
+  const auto layout = weight_layout(shape_, &total);
+  if (!blob || bytes < total) {
+    if (err) *err = "weight blob too small for the model shape";
+    return 1;
+  }
+  ES_HIP(hipStreamCreateWithFlags(&stream_, hipStreamNonBlocking), "hipStreamCreate");
+  auto alloc = [&](size_t n) -> void* {
+    void* p = nullptr;
+    if (hipMalloc(&p, std::max<size_t>(n, 256)) != hipSuccess) return nullptr;
+    allocations_.push_back(p);
+    return p;
+  };
+  d_weights_ = static_cast<uint8_t*>(alloc(total));
+  if (!d_weights_) {
+    if (err) *err = "device allocation of weights failed";
+    return 2;
+  }
+  ES_HIP(hipMemcpy(d_weights_, blob, total, hipMemcpyHostToDevice), "weight upload");
+
+  std::map<std::string, const TensorDesc*> by_name;
+  for (const auto& d : layout) by_name[d.name] = &d;
+  auto ptr = [&](const std::string& n) -> void* { return d_weights_ + by_name.at(n)->offset; };
+  auto q4 = [&](const std::string& n, int rows, int k) {
+    return Q4{static_cast<const uint32_t*>(ptr(n + ".weight")),
+              static_cast<const uint16_t*>(ptr(n + ".scales")),
+              static_cast<const uint16_t*>(ptr(n + ".biases")), rows, k};
+  };
+  embed_ = q4("embed_tokens", shape_.vocab, 1024);
+  final_norm_ = static_cast<const uint16_t*>(ptr("norm.weight"));
+  layers_.resize(shape_.n_layers);
+  for (int l = 0; l < shape_.n_layers; ++l) {
+    LayerDev& L = layers_[l];
+    const std::string p = "layers." + std::to_string(l);
+    L.attention = shape_.is_attention(l);
+    L.input_norm = static_cast<const uint16_t*>(ptr(p + ".input_layernorm.weight"));
+    L.post_norm = static_cast<const uint16_t*>(ptr(p + ".post_attention_layernorm.weight"));
+    L.gate = q4(p + ".mlp.gate_proj", 3584, 1024);
+    L.up = q4(p + ".mlp.up_proj", 3584, 1024);
+    L.down = q4(p + ".mlp.down_proj", 1024, 3584);
+    if (L.attention) {
+      const std::string a = p + ".self_attn";
+      L.q = q4(a + ".q_proj", 4096, 1024);
+      L.k = q4(a + ".k_proj", 512, 1024);
+      L.v = q4(a + ".v_proj", 512, 1024);
+      L.o = q4(a + ".o_proj", 1024, 2048);
+      L.q_norm = static_cast<const uint16_t*>(ptr(a + ".q_norm.weight"));
+      L.k_norm = static_cast<const uint16_t*>(ptr(a + ".k_norm.weight"));
+      const size_t cache = (size_t)2 * capacity_ * 256 * sizeof(uint16_t);
+      L.kcache = static_cast<uint16_t*>(alloc(cache));
+      L.vcache = static_cast<uint16_t*>(alloc(cache));
+      if (!L.kcache || !L.vcache) {
+        if (err) *err = "device allocation of KV caches failed";
+        return 2;
+      }
+    } else {
+      const std::string g = p + ".linear_attn";
+      L.qkv = q4(g + ".in_proj_qkv", 6144, 1024);
+      L.z = q4(g + ".in_proj_z", 2048, 1024);
+      L.a = q4(g + ".in_proj_a", 16, 1024);
+      L.b = q4(g + ".in_proj_b", 16, 1024);
+      L.out = q4(g + ".out_proj", 1024, 2048);
+      L.conv_w = static_cast<const uint16_t*>(ptr(g + ".conv1d.weight"));
+      L.gdn_norm = static_cast<const uint16_t*>(ptr(g + ".norm.weight"));
+      L.dt_bias = static_cast<const uint16_t*>(ptr(g + ".dt_bias"));
+      L.a_log = static_cast<const float*>(ptr(g + ".A_log"));
+      L.ring = static_cast<uint16_t*>(alloc((size_t)4 * kConv * sizeof(uint16_t)));
+      L.state = static_cast<float*>(alloc((size_t)16 * 128 * 128 * sizeof(float)));
+      if (!L.ring || !L.state) {
+        if (err) *err = "device allocation of GDN state failed";
+        return 2;
+      }
+    }
+  }
+  h_ = static_cast<uint16_t*>(alloc(1024 * 2));
+  z_ = static_cast<uint16_t*>(alloc(2048 * 2));
+  ab_ = static_cast<uint16_t*>(alloc(32 * 2));
+  y_ = static_cast<uint16_t*>(alloc(2048 * 2));
+  q_ = static_cast<uint16_t*>(alloc(4096 * 2));
+  k_ = static_cast<uint16_t*>(alloc(512 * 2));
+  v_ = static_cast<uint16_t*>(alloc(512 * 2));
+  act_ = static_cast<uint16_t*>(alloc(3584 * 2));
+  logits_ = static_cast<uint16_t*>(alloc((size_t)shape_.vocab * 2));
+  head_part_ = static_cast<float*>(alloc((size_t)head_blocks(shape_.vocab) * 2 * sizeof(float)));
+  part_o_ = static_cast<float*>(alloc((size_t)8 * 256 * 256 * sizeof(float)));
+  part_ml_ = static_cast<float*>(alloc((size_t)8 * 256 * 2 * sizeof(float)));
+  inv_freq_ = static_cast<float*>(alloc(32 * sizeof(float)));
+  st_ = static_cast<StepState*>(alloc(sizeof(StepState)));
+  prompt_ = static_cast<uint32_t*>(alloc((size_t)capacity_ * 4));
+  out_ = static_cast<uint32_t*>(alloc((size_t)capacity_ * 4));
+  forced_ = static_cast<uint32_t*>(alloc((size_t)capacity_ * 4));
+  for (void* p : {(void*)h_, (void*)z_, (void*)ab_, (void*)y_, (void*)q_, (void*)k_, (void*)v_,
+                  (void*)act_, (void*)logits_, (void*)head_part_,
+                  (void*)part_o_, (void*)part_ml_, (void*)inv_freq_, (void*)st_, (void*)prompt_,
+                  (void*)out_, (void*)forced_}) {
+    if (!p) {
+      if (err) *err = "device allocation of scratch failed";
+      return 2;
+    }
+  }
+  float inv_freq[32];
+  for (int i = 0; i < 32; ++i) inv_freq[i] = rope_inv_freq_host(i);
+  ES_HIP(hipMemcpy(inv_freq_, inv_freq, sizeof(inv_freq), hipMemcpyHostToDevice), "inv_freq");
+  ES_HIP(hipMemset(h_, 0, 1024 * 2), "memset");
+  for (auto& L : layers_)
+    if (L.attention) {
+      const size_t cache = (size_t)2 * capacity_ * 256 * sizeof(uint16_t);
+      ES_HIP(hipMemset(L.kcache, 0, cache), "memset kv");
+      ES_HIP(hipMemset(L.vcache, 0, cache), "memset kv");
+    }
+  reset_state();
+  ES_HIP(hipStreamSynchronize(stream_), "init sync");
+  return 0;
+}
+
+// model.rs:93-96: position 0, no pending token, zeroed GDN history and state.
+void Engine::reset_state() {
+  position_ = 0;
+  has_pending_ = false;
+  pending_ = 0;
+  for (auto& L : layers_)
+    if (!L.attention) {
+      (void)hipMemsetAsync(L.ring, 0, (size_t)4 * kConv * 2, stream_);
+      (void)hipMemsetAsync(L.state, 0, (size_t)16 * 128 * 128 * 4, stream_);
+    }
+}
+
+AttnArgs Engine::attn_args(const LayerDev& L, int splits) {
+  AttnArgs a{};
+  a.q_proj = q_;
+  a.k_proj = k_;
+  a.v_proj = v_;
+  a.q_gain = L.q_norm;
+  a.k_gain = L.k_norm;
+  a.kcache = L.kcache;
+  a.vcache = L.vcache;
+  a.capacity = capacity_;
+  a.inv_freq = inv_freq_;
+  a.part_o = part_o_;
+  a.part_ml = part_ml_;
+  a.splits = splits;
+  a.gated = y_;
+  a.query_out = nullptr;
+  a.st = st_;
+  a.pos_val = 0;
+  return a;
+}
+
+// Kernel order of encode_forward with rows == 1 (model.rs:228-307): per GDN
+// layer 5 launches, per attention layer 6, embedding fused into layer 0.
+hipError_t Engine::enqueue_layers(hipStream_t s, int splits) {
+  hipError_t e;
+  for (int l = 0; l < shape_.n_layers; ++l) {
+    const LayerDev& L = layers_[l];
+    NormMultiArgs nm{};
+    nm.x = h_;
+    nm.gain = L.input_norm;
+    nm.st = st_;
+    if (l == 0) {
+      nm.embed = embed_;
+      nm.h_out = h_;
+    }
+    if (!L.attention) {
+      nm.count = 4;
+      nm.m[0] = L.qkv; nm.y[0] = L.ring;
+      nm.m[1] = L.z;   nm.y[1] = z_;
+      nm.m[2] = L.a;   nm.y[2] = ab_;
+      nm.m[3] = L.b;   nm.y[3] = ab_ + 16;
+      nm.ring0 = 1;
+      if ((e = launch_norm_multi(nm, s)) != hipSuccess) return e;
+      GdnRecurArgs g{};
+      g.ring = L.ring;
+      g.conv_w = L.conv_w;
+      g.ab = ab_;
+      g.a_log = L.a_log;
+      g.dt_bias = L.dt_bias;
+      g.state = L.state;
+      g.y = y_;
+      g.st = st_;
+      if ((e = launch_gdn_recur(g, s)) != hipSuccess) return e;
+      if ((e = launch_gdn_gate_out(L.out, y_, z_, L.gdn_norm, h_, nullptr, s)) != hipSuccess)
+        return e;
+    } else {
+      nm.count = 3;
+      nm.m[0] = L.q; nm.y[0] = q_;
+      nm.m[1] = L.k; nm.y[1] = k_;
+      nm.m[2] = L.v; nm.y[2] = v_;
+      if ((e = launch_norm_multi(nm, s)) != hipSuccess) return e;
+      const AttnArgs a = attn_args(L, splits);
+      if ((e = launch_attn_split(a, s)) != hipSuccess) return e;
+      if ((e = launch_attn_merge(a, s)) != hipSuccess) return e;
+      if ((e = launch_qmv(L.o, y_, h_, h_, nullptr, s)) != hipSuccess) return e;
+    }
+    if ((e = launch_norm_gate_up(L.gate, L.up, h_, L.post_norm, nullptr, act_, s)) != hipSuccess)
+      return e;
+    if ((e = launch_qmv(L.down, act_, h_, h_, nullptr, s)) != hipSuccess) return e;
+  }
+  return hipSuccess;
+}
+
+hipError_t Engine::enqueue_step(hipStream_t s, int splits, bool with_head) {
+  hipError_t e = enqueue_layers(s, splits);
+  if (e != hipSuccess) return e;
+  if (with_head) {
+    HeadArgs h{};
+    h.embed = embed_;
+    h.h = h_;
+    h.gain = final_norm_;
+    h.logits = logits_;
+    h.part = head_part_;
+    h.st = st_;
+    h.out_tokens = out_;
+    return launch_head(h, s);
+  }
+  return launch_advance(st_, prompt_, s);
+}
+
+hipGraphExec_t Engine::graph(int kind, int splits, std::string* err) {
+  for (auto& g : graphs_)
+    if (g.kind == kind && g.splits == splits) return g.exec;
+  GraphEntry ge{kind, splits, nullptr, nullptr};
+  if (hipStreamBeginCapture(stream_, hipStreamCaptureModeThreadLocal) != hipSuccess) {
+    if (err) *err = "hipStreamBeginCapture failed";
+    return nullptr;
+  }
+  const hipError_t qe = enqueue_step(stream_, splits, kind == kKindDecode);
+  const hipError_t ce = hipStreamEndCapture(stream_, &ge.g);
+  if (qe != hipSuccess || ce != hipSuccess) {
+    if (err) *err = std::string("graph capture failed: ") + hipGetErrorString(qe != hipSuccess ? qe : ce);
+    if (ge.g) (void)hipGraphDestroy(ge.g);
+    return nullptr;
+  }
+  if (hipGraphInstantiate(&ge.exec, ge.g, nullptr, nullptr, 0) != hipSuccess) {
+    if (err) *err = "hipGraphInstantiate failed";
+    (void)hipGraphDestroy(ge.g);
+    return nullptr;
+  }
+  graphs_.push_back(ge);
+  return ge.exec;
+}
+
+int Engine::upload_state(int pos, int step, uint32_t token, std::string* err) {
+  StepState hs{pos, step, token, 0u};
+  ES_HIP(hipMemcpyAsync(st_, &hs, sizeof(hs), hipMemcpyHostToDevice, stream_), "state upload");
+  ES_HIP(hipStreamSynchronize(stream_), "state upload sync");
+  return 0;
+}
+
+// Launch `count` steps of one kind starting at absolute position first_pos.
+// At most kAhead steps are in flight between cancellation checks
+// (model.rs:127-139 keeps 16 outstanding).
+int Engine::run_steps(int kind, int first_pos, int count, const uint32_t* forced_dev,
+                      uint16_t* logits_out, std::string* err) {
+  constexpr int kAhead = 16;
+  int launched = 0;
+  while (launched < count) {
+    if (cancelled_.load()) {
+      (void)hipStreamSynchronize(stream_);
+      if (err) *err = "input disconnected";
+      return 3;
+    }
+    const int batch = std::min(kAhead, count - launched);
+    for (int i = 0; i < batch; ++i) {
+      const int pos = first_pos + launched + i;
+      hipGraphExec_t ex = graph(kind, splits_for(pos + 1), err);
+      if (!ex) return 2;
+      if (forced_dev) {
+        ES_HIP(launch_set_token(st_, forced_dev + launched + i, stream_), "set token");
+      }
+      ES_HIP(hipGraphLaunch(ex, stream_), "hipGraphLaunch");
+      if (logits_out) {
+        ES_HIP(hipMemcpyAsync(logits_out + (size_t)(launched + i) * shape_.vocab, logits_,
+                              (size_t)shape_.vocab * 2, hipMemcpyDeviceToHost, stream_),
+               "logits copy");
+        ES_HIP(hipStreamSynchronize(stream_), "logits sync");
+      }
+    }
+    launched += batch;
+    ES_HIP(hipStreamSynchronize(stream_), "step sync");
+  }
+  return 0;
+}
+
+int Engine::generate(const uint32_t* prompt, int len, int count, bool reset, uint32_t* out,
+                     std::string* err) {
+  if (count <= 0 || count > capacity_) {
+    if (err) *err = "invalid output length";
+    return 1;
+  }
+  int first;
+  if (reset) {
+    if (len <= 0 || !prompt) {
+      if (err) *err = "reset needs nonempty prompt";
+      return 1;
+    }
+    if ((int64_t)len + count - 1 > capacity_) {
+      if (err) *err = "context capacity exceeded";
+      return 1;
+    }
+    for (int i = 0; i < len; ++i)
+      if (prompt[i] >= (uint32_t)shape_.vocab) {
+        if (err) *err = "token outside vocabulary";
+        return 1;
+      }
+    reset_state();
+    ES_HIP(hipMemcpyAsync(prompt_, prompt, (size_t)len * 4, hipMemcpyHostToDevice, stream_),
+           "prompt upload");
+    if (int rc = upload_state(0, 0, prompt[0], err)) return rc;
+    if (len > 1) {
+      if (int rc = run_steps(kKindPrompt, 0, len - 1, nullptr, nullptr, err)) {
+        reset_state();
+        return rc;
+      }
+    }
+    position_ = len - 1;
+    first = position_;
+    // token for the first decode step is prompt[len-1], already in the state
+  } else {
+    if (len != 0) {
+      if (err) *err = "continuation prompt must be empty";
+      return 1;
+    }
+    if ((int64_t)position_ + count > capacity_) {
+      if (err) *err = "context capacity exceeded";
+      return 1;
+    }
+    if (!has_pending_) {
+      if (err) *err = "no continuation state";
+      return 1;
+    }
+    if (int rc = upload_state(position_, 0, pending_, err)) return rc;
+    first = position_;
+  }
+  if (int rc = run_steps(kKindDecode, first, count, nullptr, nullptr, err)) {
+    reset_state();
+    return rc;
+  }
+  ES_HIP(hipMemcpy(out, out_, (size_t)count * 4, hipMemcpyDeviceToHost), "token readback");
+  position_ = first + count;
+  pending_ = out[count - 1];
+  has_pending_ = true;
+  return 0;
+}
+
+int Engine::forced_decode(const uint32_t* tokens, int n, uint32_t* argmax_out,
+                          uint16_t* logits_out, std::string* err) {
+  if (n <= 0 || !tokens || !argmax_out) {
+    if (err) *err = "invalid forced decode request";
+    return 1;
+  }
+  if ((int64_t)position_ + n > capacity_) {
+    if (err) *err = "context capacity exceeded";
+    return 1;
+  }
+  for (int i = 0; i < n; ++i)
+    if (tokens[i] >= (uint32_t)shape_.vocab) {
+      if (err) *err = "token outside vocabulary";
+      return 1;
+    }
+  ES_HIP(hipMemcpyAsync(forced_, tokens, (size_t)n * 4, hipMemcpyHostToDevice, stream_),
+         "forced upload");
+  if (int rc = upload_state(position_, 0, tokens[0], err)) return rc;
+  if (int rc = run_steps(kKindDecode, position_, n, forced_, logits_out, err)) {
+    reset_state();
+    return rc;
+  }
+  ES_HIP(hipMemcpy(argmax_out, out_, (size_t)n * 4, hipMemcpyDeviceToHost), "argmax readback");
+  position_ += n;
+  pending_ = argmax_out[n - 1];
+  has_pending_ = true;
+  return 0;
+}
+
+int Engine::read_kv(int layer, int which, int pos0, int count, void* host, std::string* err) {
+  if (layer < 0 || layer >= shape_.n_layers || !layers_[layer].attention || which < 0 ||
+      which > 1 || pos0 < 0 || count < 0 || pos0 + count > capacity_ || !host) {
+    if (err) *err = "invalid KV read";
+    return 1;
+  }
+  const uint16_t* base = which == 0 ? layers_[layer].kcache : layers_[layer].vcache;
+  for (int h = 0; h < 2; ++h)
+    ES_HIP(hipMemcpy(static_cast<uint16_t*>(host) + (size_t)h * count * 256,
+                     base + ((size_t)h * capacity_ + pos0) * 256, (size_t)count * 256 * 2,
+                     hipMemcpyDeviceToHost),
+           "kv read");
+  return 0;
+}
+
+int Engine::write_kv(int layer, int which, int pos0, int count, const void* host,
+                     std::string* err) {
+  if (layer < 0 || layer >= shape_.n_layers || !layers_[layer].attention || which < 0 ||
+      which > 1 || pos0 < 0 || count < 0 || pos0 + count > capacity_ || !host) {
+    if (err) *err = "invalid KV write";
+    return 1;
+  }
+  uint16_t* base = which == 0 ? layers_[layer].kcache : layers_[layer].vcache;
+  for (int h = 0; h < 2; ++h)
+    ES_HIP(hipMemcpy(base + ((size_t)h * capacity_ + pos0) * 256,
+                     static_cast<const uint16_t*>(host) + (size_t)h * count * 256,
+                     (size_t)count * 256 * 2, hipMemcpyHostToDevice),
+           "kv write");
+  return 0;
+}
+
+int Engine::read_gdn(int layer, void* ring_host, void* state_host, std::string* err) {
+  if (layer < 0 || layer >= shape_.n_layers || layers_[layer].attention) {
+    if (err) *err = "invalid GDN read";
+    return 1;
+  }
+  ES_HIP(hipStreamSynchronize(stream_), "sync");
+  if (ring_host)
+    ES_HIP(hipMemcpy(ring_host, layers_[layer].ring, (size_t)4 * kConv * 2, hipMemcpyDeviceToHost),
+           "ring read");
+  if (state_host)
+    ES_HIP(hipMemcpy(state_host, layers_[layer].state, (size_t)16 * 128 * 128 * 4,
+                     hipMemcpyDeviceToHost),
+           "state read");
+  return 0;
+}
+
+int Engine::write_gdn(int layer, const void* ring_host, const void* state_host,
+                      std::string* err) {
+  if (layer < 0 || layer >= shape_.n_layers || layers_[layer].attention) {
+    if (err) *err = "invalid GDN write";
+    return 1;
+  }
+  ES_HIP(hipStreamSynchronize(stream_), "sync");
+  if (ring_host)
+    ES_HIP(hipMemcpy(layers_[layer].ring, ring_host, (size_t)4 * kConv * 2, hipMemcpyHostToDevice),
+           "ring write");
+  if (state_host)
+    ES_HIP(hipMemcpy(layers_[layer].state, state_host, (size_t)16 * 128 * 128 * 4,
+                     hipMemcpyHostToDevice),
+           "state write");
+  return 0;
+}
+
+int Engine::fill_synthetic(int length, uint64_t seed, uint32_t token, std::string* err) {
+  if (length < 0 || length >= capacity_ || token >= (uint32_t)shape_.vocab) {
+    if (err) *err = "invalid synthetic context";
+    return 1;
+  }
+  uint64_t s = seed * 0x9E3779B97F4A7C15ull + 1;
+  for (auto& L : layers_) {
+    if (L.attention) {
+      for (int h = 0; h < 2; ++h) {
+        ES_HIP(launch_fill_normal_bf16(L.kcache + (size_t)h * capacity_ * 256,
+                                       (size_t)length * 256, 1.0f, s++, stream_),
+               "fill k");
+        ES_HIP(launch_fill_normal_bf16(L.vcache + (size_t)h * capacity_ * 256,
+                                       (size_t)length * 256, 1.0f, s++, stream_),
+               "fill v");
+      }
+    } else {
+      ES_HIP(launch_fill_normal_bf16(L.ring, (size_t)4 * kConv, 1.0f, s++, stream_), "fill ring");
+      ES_HIP(launch_fill_normal_f32(L.state, (size_t)16 * 128 * 128, 0.1f, s++, stream_),
+             "fill state");
+    }
+  }
+  ES_HIP(hipStreamSynchronize(stream_), "fill sync");
+  position_ = length;
+  pending_ = token;
+  has_pending_ = true;
+  return 0;
+}
+
+int Engine::set_position(int position, uint32_t pending, std::string* err) {
+  if (position < 0 || position >= capacity_ || pending >= (uint32_t)shape_.vocab) {
+    if (err) *err = "invalid position";
+    return 1;
+  }
+  position_ = position;
+  pending_ = pending;
+  has_pending_ = true;
+  return 0;
+}
+
+int Engine::time_decode(int steps, int warmup, double* ms_total, std::string* err) {
+  if (steps <= 0 || warmup < 0 || !has_pending_ ||
+      (int64_t)position_ + steps + warmup > capacity_) {
+    if (err) *err = "invalid timing request";
+    return 1;
+  }
+  if (int rc = upload_state(position_, 0, pending_, err)) return rc;
+  for (int i = 0; i < warmup; ++i) {
+    hipGraphExec_t ex = graph(kKindDecode, splits_for(position_ + i + 1), err);
+    if (!ex) return 2;
+    ES_HIP(hipGraphLaunch(ex, stream_), "launch");
+  }
+  // capture every graph the timed steps need before the clock starts
+  for (int i = 0; i < steps; ++i)
+    if (!graph(kKindDecode, splits_for(position_ + warmup + i + 1), err)) return 2;
+  ES_HIP(hipStreamSynchronize(stream_), "warmup sync");
+  hipEvent_t e0, e1;
+  ES_HIP(hipEventCreate(&e0), "event");
+  ES_HIP(hipEventCreate(&e1), "event");
+  ES_HIP(hipEventRecord(e0, stream_), "record");
+  for (int i = 0; i < steps; ++i) {
+    hipGraphExec_t ex = graph(kKindDecode, splits_for(position_ + warmup + i + 1), err);
+    ES_HIP(hipGraphLaunch(ex, stream_), "launch");
+  }
+  ES_HIP(hipEventRecord(e1, stream_), "record");
+  ES_HIP(hipEventSynchronize(e1), "event sync");
+  float ms = 0.0f;
+  ES_HIP(hipEventElapsedTime(&ms, e0, e1), "elapsed");
+  (void)hipEventDestroy(e0);
+  (void)hipEventDestroy(e1);
+  *ms_total = ms;
+  uint32_t last = 0;
+  ES_HIP(hipMemcpy(&last, out_ + (steps + warmup - 1), 4, hipMemcpyDeviceToHost), "readback");
+  position_ += steps + warmup;
+  pending_ = last;
+  return 0;
+}
+
+int Engine::time_attention(int layer, int reps, double* ms_avg, std::string* err) {
+  if (layer < 0 || layer >= shape_.n_layers || !layers_[layer].attention || reps <= 0) {
+    if (err) *err = "invalid attention timing request";
+    return 1;
+  }
+  if (int rc = upload_state(position_, 0, pending_, err)) return rc;
+  const AttnArgs a = attn_args(layers_[layer], splits_for(position_ + 1));
+  ES_HIP(launch_attn_split(a, stream_), "attn warmup");
+  ES_HIP(hipStreamSynchronize(stream_), "sync");
+  hipEvent_t e0, e1;
+  ES_HIP(hipEventCreate(&e0), "event");
+  ES_HIP(hipEventCreate(&e1), "event");
+  ES_HIP(hipEventRecord(e0, stream_), "record");
+  for (int i = 0; i < reps; ++i) ES_HIP(launch_attn_split(a, stream_), "attn");
+  ES_HIP(hipEventRecord(e1, stream_), "record");
+  ES_HIP(hipEventSynchronize(e1), "sync");
+  float ms = 0.0f;
+  ES_HIP(hipEventElapsedTime(&ms, e0, e1), "elapsed");
+  (void)hipEventDestroy(e0);
+  (void)hipEventDestroy(e1);
+  *ms_avg = ms / reps;
+  return 0;
+}
+
+int Engine::time_head(int reps, double* ms_avg, std::string* err) {
+  if (reps <= 0) {
+    if (err) *err = "invalid head timing request";
+    return 1;
+  }
+  HeadArgs h{};
+  h.embed = embed_;
+  h.h = h_;
+  h.gain = final_norm_;
+  h.logits = logits_;
+  h.part = head_part_;
+  uint32_t* tok = forced_;
+  h.token_out = tok;
+  ES_HIP(launch_head(h, stream_), "head warmup");
+  ES_HIP(hipStreamSynchronize(stream_), "sync");
+  hipEvent_t e0, e1;
+  ES_HIP(hipEventCreate(&e0), "event");
+  ES_HIP(hipEventCreate(&e1), "event");
+  ES_HIP(hipEventRecord(e0, stream_), "record");
+  for (int i = 0; i < reps; ++i) ES_HIP(launch_head(h, stream_), "head");
+  ES_HIP(hipEventRecord(e1, stream_), "record");
+  ES_HIP(hipEventSynchronize(e1), "sync");
+  float ms = 0.0f;
+  ES_HIP(hipEventElapsedTime(&ms, e0, e1), "elapsed");
+  (void)hipEventDestroy(e0);
+  (void)hipEventDestroy(e1);
+  *ms_avg = ms / reps;
+  return 0;
+}
+
+}  // namespace es

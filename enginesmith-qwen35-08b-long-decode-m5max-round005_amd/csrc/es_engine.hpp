@@ -1,0 +1,136 @@
+// Decode engine: the MI355X counterpart of the reference's Model
+// (model.rs:28-180). It owns the weights, the persistent decode state (GDN
+// conv rings and fp32 states, bf16 KV caches), the scratch buffers, and one
+// hipGraph per step kind and attention split count. A step's position and
+// token live in device memory (StepState), so the same graph replays for
+// every token and the vocab head feeds its argmax to the next step's
+// embedding without a host round trip.
+#pragma once
+#include <hip/hip_runtime.h>
+
+#include <atomic>
+#include <cstdint>
+#include <string>
+#include <vector>
+
+#include "es_kernels.hpp"
+#include "es_weights.hpp"
+
+namespace es {
+
+struct LayerDev {
+  bool attention;
+  const uint16_t* input_norm;
+  const uint16_t* post_norm;
+  Q4 gate, up, down;
+  // GDN
+  Q4 qkv, z, a, b, out;
+  const uint16_t* conv_w;
+  const uint16_t* gdn_norm;
+  const uint16_t* dt_bias;
+  const float* a_log;
+  uint16_t* ring;   // [4, 6144]
+  float* state;     // [16, 128, 128]
+  // attention
+  Q4 q, k, v, o;
+  const uint16_t* q_norm;
+  const uint16_t* k_norm;
+  uint16_t* kcache; // [2, capacity, 256]
+  uint16_t* vcache;
+};
+
+class Engine {
+ public:
+  static Engine* create(const void* blob, uint64_t bytes, int n_layers, int vocab, int capacity,
+                        std::string* err);
+  ~Engine();
+
+  // Model::generate (model.rs:97-122). Returns 0 or an error (message in err).
+  int generate(const uint32_t* prompt, int len, int count, bool reset, uint32_t* out,
+               std::string* err);
+  // Teacher-forced decode: step i consumes tokens[i]; argmax_out[i] is the
+  // greedy pick after it. logits_out (optional, host) receives [n, vocab] bf16.
+  int forced_decode(const uint32_t* tokens, int n, uint32_t* argmax_out, uint16_t* logits_out,
+                    std::string* err);
+  void cancel() { cancelled_.store(true); }
+  void clear_cancel() { cancelled_.store(false); }
+  int position() const { return position_; }
+  bool has_pending() const { return has_pending_; }
+  uint32_t pending() const { return pending_; }
+
+  // State handoff (host copies). which: 0 = K cache, 1 = V cache.
+  int read_kv(int layer, int which, int pos0, int count, void* host, std::string* err);
+  int write_kv(int layer, int which, int pos0, int count, const void* host, std::string* err);
+  // ring [4,6144] bf16 and state [16,128,128] f32 of a GDN layer
+  int read_gdn(int layer, void* ring_host, void* state_host, std::string* err);
+  int write_gdn(int layer, const void* ring_host, const void* state_host, std::string* err);
+  // Synthetic context of `length` consumed tokens: N(0,1) KV rows, N(0,0.1)
+  // GDN states, N(0,1) rings; the pending token is `token`.
+  int fill_synthetic(int length, uint64_t seed, uint32_t token, std::string* err);
+  int set_position(int position, uint32_t pending, std::string* err);
+
+  // Timing (HIP events on the engine stream).
+  int time_decode(int steps, int warmup, double* ms_total, std::string* err);
+  int time_attention(int layer, int reps, double* ms_avg, std::string* err);
+  int time_head(int reps, double* ms_avg, std::string* err);
+
+  int n_layers() const { return shape_.n_layers; }
+  int vocab() const { return shape_.vocab; }
+  int capacity() const { return capacity_; }
+  static int splits_for(int length);
+
+ private:
+  Engine() = default;
+  int init(const void* blob, uint64_t bytes, std::string* err);
+  void reset_state();
+  hipError_t enqueue_layers(hipStream_t s, int splits);
+  hipError_t enqueue_step(hipStream_t s, int splits, bool with_head);
+  hipGraphExec_t graph(int kind, int splits, std::string* err);
+  int run_steps(int kind, int first_pos, int count, const uint32_t* forced_dev,
+                uint16_t* logits_out, std::string* err);
+  int upload_state(int pos, int step, uint32_t token, std::string* err);
+  AttnArgs attn_args(const LayerDev& L, int splits);
+
+  ModelShape shape_{};
+  int capacity_ = 0;
+  hipStream_t stream_ = nullptr;
+  uint8_t* d_weights_ = nullptr;
+  std::vector<LayerDev> layers_;
+  Q4 embed_{};
+  const uint16_t* final_norm_ = nullptr;
+  std::vector<void*> allocations_;
+
+  // scratch
+  uint16_t* h_ = nullptr;       // residual stream [1024]
+  uint16_t* z_ = nullptr;       // [2048]
+  uint16_t* ab_ = nullptr;      // [32]
+  uint16_t* y_ = nullptr;       // [2048] GDN readout / attention gated output
+  uint16_t* q_ = nullptr;       // [4096]
+  uint16_t* k_ = nullptr;       // [512]
+  uint16_t* v_ = nullptr;       // [512]
+  uint16_t* act_ = nullptr;     // [3584]
+  uint16_t* logits_ = nullptr;  // [vocab]
+  float* head_part_ = nullptr;
+  float* part_o_ = nullptr;
+  float* part_ml_ = nullptr;
+  float* inv_freq_ = nullptr;
+  StepState* st_ = nullptr;
+  uint32_t* prompt_ = nullptr;  // [capacity]
+  uint32_t* out_ = nullptr;     // [capacity]
+  uint32_t* forced_ = nullptr;  // [capacity]
+
+  struct GraphEntry {
+    int kind;
+    int splits;
+    hipGraph_t g;
+    hipGraphExec_t exec;
+  };
+  std::vector<GraphEntry> graphs_;
+
+  int position_ = 0;
+  bool has_pending_ = false;
+  uint32_t pending_ = 0;
+  std::atomic<bool> cancelled_{false};
+};
+
+}  // namespace es

@@ -1,0 +1,121 @@
+// Host-side launchers for the decode kernels. Every launcher checks the
+// shapes its kernel assumes and returns hipErrorInvalidValue (without
+// launching) when they do not hold; device pointers are caller-owned.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include "es_device.hpp"
+
+namespace es {
+
+// ---- linear (Q4 affine group 64), k_linear.hip ----
+// RMSNorm(x)*gain (K=1024) followed by up to four projections sharing the
+// normalised input. When embed.w is set, x is instead the bf16 embedding row
+// of the token in st->token (or token_val when st is null); block 0 writes
+// that row to h_out. With ring0 set, output 0 is a 4-slot ring [4, n0] and the
+// slot (pos & 3) is written.
+struct NormMultiArgs {
+  Q4 m[4];
+  uint16_t* y[4];
+  int count;
+  int ring0;
+  const uint16_t* x;
+  const uint16_t* gain;
+  uint16_t* norm_out;
+  Q4 embed;
+  uint16_t* h_out;
+  uint32_t token_val;
+  const StepState* st;
+  int pos_val;
+};
+hipError_t launch_norm_multi(const NormMultiArgs& a, hipStream_t s);
+
+// RMSNorm(x)*gain then act = SwiGLU(gate u, up u) (K=1024).
+hipError_t launch_norm_gate_up(const Q4& gate, const Q4& up, const uint16_t* x,
+                               const uint16_t* gain, uint16_t* norm_out, uint16_t* act,
+                               hipStream_t s);
+
+// y = bf16(W x) or, with residual, y = bf16(residual + bf16(W x)). x bf16[K].
+// K == 1024 or 1024 < K <= 4096 with K % 64 == 0. y may alias residual.
+hipError_t launch_qmv(const Q4& w, const uint16_t* x, const uint16_t* residual, uint16_t* y,
+                      float* y_f32, hipStream_t s);
+
+// Embedding row: out = bf16(scale*q + bias) for token *token_dev.
+hipError_t launch_embedding(const Q4& table, const uint32_t* token_dev, uint16_t* out,
+                            hipStream_t s);
+
+// ---- Gated DeltaNet, k_gdn.hip ----
+struct GdnRecurArgs {
+  const uint16_t* ring;     // [4, 6144] raw projected qkv, slot = position & 3
+  const uint16_t* conv_w;   // [6144, 4]
+  const uint16_t* ab;       // a[16] then b[16] raw projections
+  const float* a_log;       // [16]
+  const uint16_t* dt_bias;  // [16]
+  float* state;             // [16, 128 v, 128 k] in place
+  uint16_t* y;              // [2048]
+  uint16_t* qkv_out;        // optional [6144]: normalised q|k and activated v
+  float* g_out;             // optional [16]
+  uint16_t* beta_out;       // optional [16]
+  const StepState* st;
+  int pos_val;
+};
+hipError_t launch_gdn_recur(const GdnRecurArgs& a, hipStream_t s);
+
+// Gated RMSNorm of y by z (per 128-wide head) feeding out_proj (K=2048) with
+// the residual add: h = bf16(h + bf16(W gated)). gated_out (optional) receives
+// the gated vector from block 0.
+hipError_t launch_gdn_gate_out(const Q4& w, const uint16_t* y, const uint16_t* z,
+                               const uint16_t* norm_w, uint16_t* h, uint16_t* gated_out,
+                               hipStream_t s);
+
+// ---- attention, k_attention.hip ----
+struct AttnArgs {
+  const uint16_t* q_proj;   // [8, 512] query|gate per head
+  const uint16_t* k_proj;   // [2, 256]
+  const uint16_t* v_proj;   // [2, 256]
+  const uint16_t* q_gain;   // [256]
+  const uint16_t* k_gain;   // [256]
+  uint16_t* kcache;         // [2, capacity, 256]
+  uint16_t* vcache;         // [2, capacity, 256]
+  int capacity;
+  const float* inv_freq;    // [32] rotary inverse frequencies
+  float* part_o;            // [8, splits, 256]
+  float* part_ml;           // [8, splits, 2]
+  int splits;
+  uint16_t* gated;          // [8, 256]
+  uint16_t* query_out;      // optional [8, 256] roped queries
+  const StepState* st;
+  int pos_val;
+};
+size_t attn_scratch_bytes(int splits);
+hipError_t launch_attn_split(const AttnArgs& a, hipStream_t s);
+hipError_t launch_attn_merge(const AttnArgs& a, hipStream_t s);
+
+// ---- vocab head, k_head.hip ----
+struct HeadArgs {
+  Q4 embed;                 // tied table [vocab, 1024]
+  const uint16_t* h;        // [1024]
+  const uint16_t* gain;     // final norm [1024]
+  uint16_t* norm_out;       // optional
+  uint16_t* logits;         // [vocab] bf16
+  float* part;              // [blocks, 2] (max, sumexp)
+  uint32_t* token_out;      // written by the tail (may be null)
+  float* lse_out;           // optional
+  StepState* st;            // optional: advances pos/step, stores token, out_tokens[step]
+  uint32_t* out_tokens;     // optional with st
+};
+int head_blocks(int vocab);
+size_t head_scratch_bytes(int vocab);
+hipError_t launch_head(const HeadArgs& a, hipStream_t s);
+
+// Prompt step epilogue: pos += 1, token = prompt[pos].
+hipError_t launch_advance(StepState* st, const uint32_t* prompt, hipStream_t s);
+// st->token = *src (teacher forcing from a device token list).
+hipError_t launch_set_token(StepState* st, const uint32_t* src, hipStream_t s);
+// Fill with N(0, sigma) bf16 / fp32 values from a counter-based generator.
+hipError_t launch_fill_normal_bf16(uint16_t* dst, size_t n, float sigma, uint64_t seed,
+                                   hipStream_t s);
+hipError_t launch_fill_normal_f32(float* dst, size_t n, float sigma, uint64_t seed,
+                                  hipStream_t s);
+
+}  // namespace es

@@ -1,0 +1,146 @@
+// Gated DeltaNet decode step on gfx950: causal conv1d (4 taps) + SiLU, Q/K
+// L2 normalisation, decay/beta gates and the delta-rule state update with
+// readout, fused in one launch.
+//
+// Grid: 8 row-blocks x 16 heads, 256 threads. A block owns 16 value rows of
+// one head; its fp32 state slice (16 x 128 = 8 KiB) is read once into
+// registers, updated and written back, 16 lanes per row and 8 keys per lane
+// (one DPP row per value row). Every block of a head recomputes the head's
+// 256 Q/K conv channels (cheap) so no cross-block dependency exists.
+//
+// Convolution history is a 4-slot ring of raw projections, slot = position&3:
+// the projection kernel writes slot pos&3, this kernel reads slots pos-3..pos,
+// and nothing is shifted. Slots for positions < 0 are zero after reset, which
+// matches the reference's zeroed [3,6144] history (gdn.metal:141-153).
+//
+// Arithmetic follows gdn.metal:121-171 (conv/prepare: fma over taps, bf16 at
+// conv and SiLU, rsqrt(ss/128 + 1e-6/128), q x 1/128, k x bf16(128^-1/2),
+// g = exp(-exp(A_log) * softplus_bf(bf16(a+dt))), beta = sigmoid_bf(b)) and
+// gdn.metal:192-226 (decay, memory, delta, update, readout; fp32 state).
+#include "es_kernels.hpp"
+
+namespace es {
+namespace {
+
+// Raw values of channel c in all four ring slots, loaded before the position
+// is known; conv_silu then orders them as taps (pos-3 .. pos).
+struct RingTaps {
+  uint32_t v[4];
+  uint2 w;
+};
+
+__device__ __forceinline__ void ring_load(const uint16_t* ring, const uint16_t* conv_w, int c,
+                                          RingTaps& r) {
+#pragma unroll
+  for (int s = 0; s < 4; ++s) r.v[s] = ring[(size_t)s * kConv + c];
+  r.w = *reinterpret_cast<const uint2*>(conv_w + (size_t)c * 4);
+}
+
+__device__ __forceinline__ float conv_silu(const RingTaps& r, int pos) {
+  const int sh = pos + 1;  // slot of tap t is (pos - 3 + t) & 3 = (pos + 1 + t) & 3
+  uint32_t x[4];
+#pragma unroll
+  for (int t = 0; t < 4; ++t) {
+    const int slot = (sh + t) & 3;
+    x[t] = slot == 0 ? r.v[0] : slot == 1 ? r.v[1] : slot == 2 ? r.v[2] : r.v[3];
+  }
+  float acc = 0.0f;
+  acc = fmaf(bf2f(x[0]), bf_lo(r.w.x), acc);
+  acc = fmaf(bf2f(x[1]), bf_hi(r.w.x), acc);
+  acc = fmaf(bf2f(x[2]), bf_lo(r.w.y), acc);
+  acc = fmaf(bf2f(x[3]), bf_hi(r.w.y), acc);
+  const float xv = rbf(acc);
+  return rbf(xv * sigmoid_bf(xv));
+}
+
+__global__ __launch_bounds__(256) void k_gdn_recur(GdnRecurArgs a) {
+  __shared__ float qk[256];
+  __shared__ float vv[16];
+  __shared__ float red[4];
+  __shared__ float gates[2];
+  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+  const int h = blockIdx.y, r0 = blockIdx.x * 16;
+  const int row = r0 + (t >> 4), j = t & 15;
+
+  // State slice first: its latency overlaps the convolution below.
+  float* sp = a.state + ((size_t)(h * 128 + row)) * 128 + 8 * j;
+  const float4 s_lo = reinterpret_cast<const float4*>(sp)[0];
+  const float4 s_hi = reinterpret_cast<const float4*>(sp)[1];
+
+  // Q (threads 0..127) and K (128..255) channels of head h; threads 0..15
+  // also own the V channels of this block's rows.
+  const int c = t < 128 ? h * 128 + t : 2048 + h * 128 + (t - 128);
+  RingTaps rt, rv;
+  ring_load(a.ring, a.conv_w, c, rt);
+  const int cv = 4096 + h * 128 + r0 + (t & 15);
+  if (t < 16) ring_load(a.ring, a.conv_w, cv, rv);
+  const int pos = load_pos(a.st, a.pos_val);
+  const float v = conv_silu(rt, pos);
+  float ss = wave_sum(v * v);
+  if (lane == 0) red[wave] = ss;
+  if (t < 16) {
+    const float vval = conv_silu(rv, pos);
+    vv[t] = vval;
+    if (a.qkv_out) a.qkv_out[cv] = (uint16_t)f2bf(vval);
+  }
+  if (t == 64) {
+    const float ax = rbf(bf2f(a.ab[h]) + bf2f(a.dt_bias[h]));
+    const float g = expf(-expf(a.a_log[h]) * softplus_bf(ax));
+    const float beta = sigmoid_bf(bf2f(a.ab[16 + h]));
+    gates[0] = g;
+    gates[1] = beta;
+    if (blockIdx.x == 0) {
+      if (a.g_out) a.g_out[h] = g;
+      if (a.beta_out) a.beta_out[h] = (uint16_t)f2bf(beta);
+    }
+  }
+  __syncthreads();
+  {
+    const float tot = t < 128 ? red[0] + red[1] : red[2] + red[3];
+    const float inv = 1.0f / sqrtf(tot / 128.0f + 1.0e-6f / 128.0f);
+    const float scale = t < 128 ? 0.0078125f : rbf(0.08838834764831845f);
+    const float qkv = rbf(rbf(v * inv) * scale);
+    qk[t] = qkv;
+    if (a.qkv_out && blockIdx.x == 0) a.qkv_out[c] = (uint16_t)f2bf(qkv);
+  }
+  __syncthreads();
+
+  const float g = gates[0], beta = gates[1];
+  float S[8] = {s_lo.x, s_lo.y, s_lo.z, s_lo.w, s_hi.x, s_hi.y, s_hi.z, s_hi.w};
+  float kk[8], qq[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    kk[i] = qk[128 + 8 * j + i];
+    qq[i] = qk[8 * j + i];
+  }
+  float mem = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    S[i] = S[i] * g;
+    mem = fmaf(S[i], kk[i], mem);
+  }
+  mem = row16_sum(mem);
+  const float delta = (vv[t >> 4] - mem) * beta;
+  float out = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    S[i] = fmaf(kk[i], delta, S[i]);
+    out = fmaf(S[i], qq[i], out);
+  }
+  out = row16_sum(out);
+  if (j == 0) a.y[h * 128 + row] = (uint16_t)f2bf(out);
+  reinterpret_cast<float4*>(sp)[0] = make_float4(S[0], S[1], S[2], S[3]);
+  reinterpret_cast<float4*>(sp)[1] = make_float4(S[4], S[5], S[6], S[7]);
+}
+
+}  // namespace
+
+hipError_t launch_gdn_recur(const GdnRecurArgs& a, hipStream_t s) {
+  if (!a.ring || !a.conv_w || !a.ab || !a.a_log || !a.dt_bias || !a.state || !a.y)
+    return hipErrorInvalidValue;
+  if (!a.st && a.pos_val < 0) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(k_gdn_recur, dim3(8, kGdnHeads), dim3(256), 0, s, a);
+  return hipGetLastError();
+}
+
+}  // namespace es

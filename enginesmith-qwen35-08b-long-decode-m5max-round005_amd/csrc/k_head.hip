@@ -1,0 +1,256 @@
+// Final RMSNorm + tied Q4 vocab head + log-sum-exp + greedy pick.
+//
+// k_head: each block of 256 threads computes 256 consecutive logits (a wave
+// owns 64 rows, two per pass, loads double-buffered four passes at a time),
+// rounds them to bf16 (head_lse.metal:53) and writes its own (max, sum exp)
+// over those bf16 logits.
+// k_head_tail (one block) merges the partials into
+//   lse = bf16(log(sum) + max)                         (head_lse.metal:81)
+// and selects the lowest index whose bf16(logit - lse) equals the maximum
+// (head_lse.metal:83-97, docs/protocol.md:44). Rounding is monotone, so the
+// maximum is bf16(maxlogit - lse), and the lowest block whose own maximum
+// reaches it holds the answer. The tail also advances the device cursor.
+#include "es_kernels.hpp"
+
+namespace es {
+namespace {
+
+constexpr int kRowsPerBlock = 256;
+constexpr int kPassBatch = 4;  // passes (2 rows each) whose loads are in flight together
+constexpr int kBatches = 64 / (2 * kPassBatch);
+
+__device__ __forceinline__ unsigned int wave_umin(unsigned int v) {
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) {
+    const unsigned int o = (unsigned int)__shfl_xor((int)v, off, 64);
+    v = o < v ? o : v;
+  }
+  return v;
+}
+
+struct HeadBatch {
+  u32x4 c[kPassBatch];
+  uint32_t s[kPassBatch], b[kPassBatch];
+};
+
+__device__ __forceinline__ void head_load(const Q4& e, int row0, int it, int half, int sl, int vocab,
+                                          HeadBatch& hb) {
+#pragma unroll
+  for (int p = 0; p < kPassBatch; ++p) {
+    const int r = row0 + it * 2 * kPassBatch + 2 * p + half;
+    const size_t rl = r < vocab ? r : 0;
+    hb.c[p] = *reinterpret_cast<const u32x4*>(e.w + rl * 128 + sl * 4);
+    hb.s[p] = e.s[rl * 16 + sl / 2];
+    hb.b[p] = e.b[rl * 16 + sl / 2];
+  }
+}
+
+__global__ __launch_bounds__(256) void k_head(HeadArgs a) {
+  __shared__ float lg[kRowsPerBlock];
+  __shared__ float wred[4];
+  __shared__ float wred2[4];
+  const int t = threadIdx.x, lane = t & 63, wave = t >> 6, half = lane >> 5, sl = lane & 31;
+  const int vocab = a.embed.n;
+  const int row0 = blockIdx.x * kRowsPerBlock + wave * 64;
+
+  HeadBatch cur, nxt;
+  head_load(a.embed, row0, 0, half, sl, vocab, cur);
+
+  // normalised input slice (rms_norm_bf16 with the final norm gain)
+  float xv[32], xn[32], xr[32];
+  load_bf16x32(a.h + sl * 32, xv);
+  {
+    float ss = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 32; ++i) ss += xv[i] * xv[i];
+    ss = half_sum(ss);
+    const float inv = 1.0f / sqrtf(ss / 1024.0f + 1e-6f);
+    float gv[32];
+    load_bf16x32(a.gain + sl * 32, gv);
+#pragma unroll
+    for (int i = 0; i < 32; ++i) xn[i] = rbf(rbf(xv[i] * inv) * gv[i]);
+  }
+  if (a.norm_out && blockIdx.x == 0 && t < 32) {
+#pragma unroll
+    for (int i = 0; i < 32; ++i) a.norm_out[sl * 32 + i] = (uint16_t)f2bf(xn[i]);
+  }
+  const float xs = prep_slice(xn, xr);
+
+#pragma unroll
+  for (int it = 0; it < kBatches; ++it) {
+    if (it + 1 < kBatches) head_load(a.embed, row0, it + 1, half, sl, vocab, nxt);
+#pragma unroll
+    for (int p = 0; p < kPassBatch; ++p) {
+      const int local = wave * 64 + it * 2 * kPassBatch + 2 * p + half;
+      const int r = blockIdx.x * kRowsPerBlock + local;
+      float part = bf2f(cur.s[p]) * q4_dot32(cur.c[p], xr) + xs * bf2f(cur.b[p]);
+      part = half_sum(part);
+      if (sl == 0) {
+        const uint32_t b = f2bf(part);
+        lg[local] = r < vocab ? bf2f(b) : -INFINITY;
+        if (r < vocab) a.logits[r] = (uint16_t)b;
+      }
+    }
+    if (it + 1 < kBatches) cur = nxt;
+  }
+  __syncthreads();
+
+  // block (max, sum exp) over its bf16 logits
+  const float v = lg[t];
+  float bm = wave_max(v);
+  if (lane == 0) wred[wave] = bm;
+  __syncthreads();
+  bm = fmaxf(fmaxf(wred[0], wred[1]), fmaxf(wred[2], wred[3]));
+  const float se = wave_sum(v == -INFINITY ? 0.0f : expf(v - bm));
+  if (lane == 0) wred2[wave] = se;
+  __syncthreads();
+  if (t == 0) {
+    a.part[2 * blockIdx.x] = bm;
+    a.part[2 * blockIdx.x + 1] = (wred2[0] + wred2[1]) + (wred2[2] + wred2[3]);
+  }
+}
+
+__global__ __launch_bounds__(256) void k_head_tail(HeadArgs a, int nb) {
+  __shared__ float wred[4];
+  __shared__ float wred2[4];
+  __shared__ unsigned int wmin[4];
+  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+  const int vocab = a.embed.n;
+  float gm = -3.402823466e38f;
+  for (int b = t; b < nb; b += 256) gm = fmaxf(gm, a.part[2 * b]);
+  gm = wave_max(gm);
+  if (lane == 0) wred[wave] = gm;
+  __syncthreads();
+  gm = fmaxf(fmaxf(wred[0], wred[1]), fmaxf(wred[2], wred[3]));
+  float gs = 0.0f;
+  for (int b = t; b < nb; b += 256) gs += a.part[2 * b + 1] * expf(a.part[2 * b] - gm);
+  gs = wave_sum(gs);
+  if (lane == 0) wred2[wave] = gs;
+  __syncthreads();
+  gs = (wred2[0] + wred2[1]) + (wred2[2] + wred2[3]);
+  const float lse = rbf(logf(gs) + gm);
+  const float target = rbf(gm - lse);
+  unsigned int first = 0xffffffffu;
+  for (int b = t; b < nb; b += 256)
+    if (rbf(a.part[2 * b] - lse) == target && (unsigned int)b < first) first = (unsigned int)b;
+  first = wave_umin(first);
+  if (lane == 0) wmin[wave] = first;
+  __syncthreads();
+  first = wmin[0];
+  for (int w = 1; w < 4; ++w) first = wmin[w] < first ? wmin[w] : first;
+  __syncthreads();
+  unsigned int best = 0xffffffffu;
+  if (first < (unsigned int)nb) {
+    const int r = (int)first * kRowsPerBlock + t;
+    if (r < vocab && rbf(bf2f(a.logits[r]) - lse) == target) best = (unsigned int)r;
+  }
+  best = wave_umin(best);
+  if (lane == 0) wmin[wave] = best;
+  __syncthreads();
+  if (t == 0) {
+    unsigned int tok = wmin[0];
+    for (int w = 1; w < 4; ++w) tok = wmin[w] < tok ? wmin[w] : tok;
+    if (tok >= (unsigned int)vocab) tok = 0;  // unreachable unless logits are NaN
+    if (a.token_out) *a.token_out = tok;
+    if (a.lse_out) *a.lse_out = lse;
+    if (a.st) {
+      const int step = a.st->step;
+      if (a.out_tokens) a.out_tokens[step] = tok;
+      a.st->token = tok;
+      a.st->step = step + 1;
+      a.st->pos = a.st->pos + 1;
+    }
+  }
+}
+
+__global__ void k_advance(StepState* st, const uint32_t* prompt) {
+  const int p = st->pos + 1;
+  st->pos = p;
+  st->token = prompt[p];
+}
+
+__global__ void k_set_token(StepState* st, const uint32_t* src) { st->token = *src; }
+
+__device__ __forceinline__ uint64_t splitmix64(uint64_t x) {
+  x += 0x9E3779B97F4A7C15ull;
+  x = (x ^ (x >> 30)) * 0xBF58476D1CE4E5B9ull;
+  x = (x ^ (x >> 27)) * 0x94D049BB133111EBull;
+  return x ^ (x >> 31);
+}
+
+__device__ __forceinline__ float2 normal_pair(uint64_t seed, uint64_t i) {
+  const uint64_t r = splitmix64(seed ^ (i * 0xD1B54A32D192ED03ull));
+  const float u1 = ((float)(uint32_t)(r >> 40) + 0.5f) * (1.0f / 16777216.0f);
+  const float u2 = ((float)(uint32_t)(r & 0xFFFFFFu)) * (1.0f / 16777216.0f);
+  const float rad = sqrtf(-2.0f * logf(u1));
+  return make_float2(rad * cosf(6.283185307179586f * u2), rad * sinf(6.283185307179586f * u2));
+}
+
+__global__ void k_fill_normal_bf16(uint16_t* dst, size_t n, float sigma, uint64_t seed) {
+  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; 2 * i < n;
+       i += (size_t)gridDim.x * blockDim.x) {
+    const float2 z = normal_pair(seed, i);
+    dst[2 * i] = (uint16_t)f2bf(z.x * sigma);
+    if (2 * i + 1 < n) dst[2 * i + 1] = (uint16_t)f2bf(z.y * sigma);
+  }
+}
+
+__global__ void k_fill_normal_f32(float* dst, size_t n, float sigma, uint64_t seed) {
+  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; 2 * i < n;
+       i += (size_t)gridDim.x * blockDim.x) {
+    const float2 z = normal_pair(seed, i);
+    dst[2 * i] = z.x * sigma;
+    if (2 * i + 1 < n) dst[2 * i + 1] = z.y * sigma;
+  }
+}
+
+}  // namespace
+
+int head_blocks(int vocab) { return (vocab + kRowsPerBlock - 1) / kRowsPerBlock; }
+size_t head_scratch_bytes(int vocab) { return (size_t)head_blocks(vocab) * 2 * sizeof(float); }
+
+hipError_t launch_head(const HeadArgs& a, hipStream_t s) {
+  if (!a.embed.w || !a.embed.s || !a.embed.b || a.embed.k != kHidden || a.embed.n <= 0 || !a.h ||
+      !a.gain || !a.logits || !a.part)
+    return hipErrorInvalidValue;
+  const int nb = head_blocks(a.embed.n);
+  hipLaunchKernelGGL(k_head, dim3(nb), dim3(256), 0, s, a);
+  hipLaunchKernelGGL(k_head_tail, dim3(1), dim3(256), 0, s, a, nb);
+  return hipGetLastError();
+}
+
+hipError_t launch_advance(StepState* st, const uint32_t* prompt, hipStream_t s) {
+  if (!st || !prompt) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(k_advance, dim3(1), dim3(1), 0, s, st, prompt);
+  return hipGetLastError();
+}
+
+hipError_t launch_set_token(StepState* st, const uint32_t* src, hipStream_t s) {
+  if (!st || !src) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(k_set_token, dim3(1), dim3(1), 0, s, st, src);
+  return hipGetLastError();
+}
+
+hipError_t launch_fill_normal_bf16(uint16_t* dst, size_t n, float sigma, uint64_t seed,
+                                   hipStream_t s) {
+  if (!dst) return hipErrorInvalidValue;
+  if (n == 0) return hipSuccess;
+  size_t pairs = (n + 1) / 2;
+  int blocks = (int)((pairs + 255) / 256);
+  if (blocks > 16384) blocks = 16384;
+  hipLaunchKernelGGL(k_fill_normal_bf16, dim3(blocks), dim3(256), 0, s, dst, n, sigma, seed);
+  return hipGetLastError();
+}
+
+hipError_t launch_fill_normal_f32(float* dst, size_t n, float sigma, uint64_t seed,
+                                  hipStream_t s) {
+  if (!dst) return hipErrorInvalidValue;
+  if (n == 0) return hipSuccess;
+  size_t pairs = (n + 1) / 2;
+  int blocks = (int)((pairs + 255) / 256);
+  if (blocks > 16384) blocks = 16384;
+  hipLaunchKernelGGL(k_fill_normal_f32, dim3(blocks), dim3(256), 0, s, dst, n, sigma, seed);
+  return hipGetLastError();
+}
+
+}  // namespace es

@@ -1,0 +1,451 @@
+// Q4 affine (group 64) dequant-matvec kernels for batch-1 decode on gfx950.
+//
+// Layout is the reference's (weights.rs:50-52): codes u32 [N, K/8] with 8
+// nibbles per word (nibble j of word w = column 8w+j), bf16 scale and bias per
+// 64 columns. A lane owns one 32-column slice of a row (one 16-byte code load,
+// half a group); a K=1024 row is one half-wave, wider rows loop over slices.
+// Each lane keeps its slice of x in registers, so the only per-row traffic is
+// the 16-byte code load plus one scale and one bias. Accumulation is fp32 and
+// the result is rounded to bf16 once (linear.metal:41-72); the residual
+// epilogue rounds the projection before the add (linear.metal:121).
+#include "es_kernels.hpp"
+
+namespace es {
+namespace {
+
+__device__ __forceinline__ void store_bf16x32(uint16_t* p, const float* v) {
+  u32x4* q = reinterpret_cast<u32x4*>(p);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    u32x4 o;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) o[j] = f2bf(v[8 * i + 2 * j]) | (f2bf(v[8 * i + 2 * j + 1]) << 16);
+    q[i] = o;
+  }
+}
+
+// RMSNorm of a K=1024 vector whose 32-element slice `sl` this lane holds; the
+// 32 lanes of a half-wave cover the vector once (rms_norm_bf16 arithmetic,
+// linear.metal:311-329: fp32 sum of squares, bf16(bf16(x*inv)*gain)).
+__device__ __forceinline__ void norm_slice_1024(const float* xv, const uint16_t* gain, int sl,
+                                                float* xn) {
+  float ss = 0.0f;
+#pragma unroll
+  for (int j = 0; j < 32; ++j) ss += xv[j] * xv[j];
+  ss = half_sum(ss);
+  const float inv = 1.0f / sqrtf(ss / 1024.0f + 1e-6f);
+  float gv[32];
+  load_bf16x32(gain + sl * 32, gv);
+#pragma unroll
+  for (int j = 0; j < 32; ++j) xn[j] = rbf(rbf(xv[j] * inv) * gv[j]);
+}
+
+// Dequantised embedding slice (embedding_q4, linear.metal:20-23).
+__device__ __forceinline__ void embed_slice(const Q4& e, uint32_t tok, int sl, float* xv) {
+  if (tok >= (uint32_t)e.n) tok = 0;  // ids come from validated prompts or the head's argmax
+  const u32x4 c = *reinterpret_cast<const u32x4*>(e.w + (size_t)tok * 128 + sl * 4);
+  const float sc = bf2f(e.s[(size_t)tok * 16 + sl / 2]);
+  const float bi = bf2f(e.b[(size_t)tok * 16 + sl / 2]);
+#pragma unroll
+  for (int w = 0; w < 4; ++w)
+#pragma unroll
+    for (int j = 0; j < 8; ++j) xv[8 * w + j] = rbf(sc * (float)((c[w] >> (4 * j)) & 15u) + bi);
+}
+
+struct MultiDev {
+  Q4 m[4];
+  uint16_t* y[4];
+  int count;
+  int total;
+  int ring0;
+  const uint16_t* x;
+  const uint16_t* gain;
+  uint16_t* norm_out;
+  Q4 embed;
+  uint16_t* h_out;
+  uint32_t token_val;
+  const StepState* st;
+  int pos_val;
+};
+
+template <int P>
+__global__ __launch_bounds__(256) void k_norm_multi(MultiDev a) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, half = lane >> 5, sl = lane & 31;
+  // Weight loads first: they do not depend on the input, so their latency
+  // overlaps the input load and the normalisation below.
+  const int base = (blockIdx.x * 4 + wave) * (2 * P);
+  u32x4 c[P];
+  uint32_t sv[P], bv[P];
+  int mi[P], lr[P];
+#pragma unroll
+  for (int p = 0; p < P; ++p) {
+    const int r = base + 2 * p + half;
+    int local = r < a.total ? r : 0;
+    int m = 0;
+    const uint32_t* w = a.m[0].w;
+    const uint16_t* s = a.m[0].s;
+    const uint16_t* b = a.m[0].b;
+    if (a.count > 1 && local >= a.m[0].n) {
+      local -= a.m[0].n; m = 1;
+      w = a.m[1].w; s = a.m[1].s; b = a.m[1].b;
+      if (a.count > 2 && local >= a.m[1].n) {
+        local -= a.m[1].n; m = 2;
+        w = a.m[2].w; s = a.m[2].s; b = a.m[2].b;
+        if (a.count > 3 && local >= a.m[2].n) {
+          local -= a.m[2].n; m = 3;
+          w = a.m[3].w; s = a.m[3].s; b = a.m[3].b;
+        }
+      }
+    }
+    mi[p] = r < a.total ? m : -1;
+    lr[p] = local;
+    c[p] = *reinterpret_cast<const u32x4*>(w + (size_t)local * 128 + sl * 4);
+    sv[p] = s[(size_t)local * 16 + sl / 2];
+    bv[p] = b[(size_t)local * 16 + sl / 2];
+  }
+
+  float xv[32];
+  if (a.embed.w) {
+    const uint32_t tok = a.st ? a.st->token : a.token_val;
+    embed_slice(a.embed, tok, sl, xv);
+    if (a.h_out && blockIdx.x == 0 && threadIdx.x < 32) store_bf16x32(a.h_out + sl * 32, xv);
+  } else {
+    load_bf16x32(a.x + sl * 32, xv);
+  }
+  float xn[32];
+  norm_slice_1024(xv, a.gain, sl, xn);
+  if (a.norm_out && blockIdx.x == 0 && threadIdx.x < 32) store_bf16x32(a.norm_out + sl * 32, xn);
+  float xr[32];
+  const float xs = prep_slice(xn, xr);
+
+  uint16_t* y0 = a.y[0];
+  if (a.ring0) y0 += (size_t)(load_pos(a.st, a.pos_val) & 3) * a.m[0].n;
+#pragma unroll
+  for (int p = 0; p < P; ++p) {
+    float part = bf2f(sv[p]) * q4_dot32(c[p], xr) + xs * bf2f(bv[p]);
+    part = half_sum(part);
+    if (sl == 0 && mi[p] >= 0) {
+      uint16_t* y = mi[p] == 0 ? y0 : mi[p] == 1 ? a.y[1] : mi[p] == 2 ? a.y[2] : a.y[3];
+      y[lr[p]] = (uint16_t)f2bf(part);
+    }
+  }
+}
+
+// RMSNorm + gate/up projections + SwiGLU with the MLX bf16 graph boundaries
+// (linear_norm.metal:214-222). A wave owns 2*NP output rows; lane 0 of each
+// half holds a row's gate and up sums and applies the activation in place.
+template <int NP>
+__global__ __launch_bounds__(256) void k_norm_gate_up(Q4 gate, Q4 up, const uint16_t* x,
+                                                      const uint16_t* gain, uint16_t* norm_out,
+                                                      uint16_t* act) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, half = lane >> 5, sl = lane & 31;
+  const int base = (blockIdx.x * 4 + wave) * (2 * NP);
+  u32x4 cg[NP], cu[NP];
+  uint32_t sg[NP], bg[NP], su[NP], bu[NP];
+  int rr[NP];
+#pragma unroll
+  for (int p = 0; p < NP; ++p) {
+    const int r = base + 2 * p + half;
+    rr[p] = r;
+    const int rl = r < gate.n ? r : 0;
+    cg[p] = *reinterpret_cast<const u32x4*>(gate.w + (size_t)rl * 128 + sl * 4);
+    cu[p] = *reinterpret_cast<const u32x4*>(up.w + (size_t)rl * 128 + sl * 4);
+    sg[p] = gate.s[(size_t)rl * 16 + sl / 2];
+    bg[p] = gate.b[(size_t)rl * 16 + sl / 2];
+    su[p] = up.s[(size_t)rl * 16 + sl / 2];
+    bu[p] = up.b[(size_t)rl * 16 + sl / 2];
+  }
+  float xv[32];
+  load_bf16x32(x + sl * 32, xv);
+  float xn[32];
+  norm_slice_1024(xv, gain, sl, xn);
+  if (norm_out && blockIdx.x == 0 && threadIdx.x < 32) store_bf16x32(norm_out + sl * 32, xn);
+  float xr[32];
+  const float xs = prep_slice(xn, xr);
+#pragma unroll
+  for (int p = 0; p < NP; ++p) {
+    float g = bf2f(sg[p]) * q4_dot32(cg[p], xr) + xs * bf2f(bg[p]);
+    float u = bf2f(su[p]) * q4_dot32(cu[p], xr) + xs * bf2f(bu[p]);
+    g = half_sum(g);
+    u = half_sum(u);
+    if (sl == 0 && rr[p] < gate.n) {
+      const float gb = rbf(g), ub = rbf(u);
+      const float silu = rbf(gb * sigmoid_bf(gb));
+      act[rr[p]] = (uint16_t)f2bf(silu * ub);
+    }
+  }
+}
+
+// Plain / residual QMV for K == 1024 (half-wave rows).
+template <int P, bool ADD>
+__global__ __launch_bounds__(256) void k_qmv_narrow(Q4 m, const uint16_t* x,
+                                                    const uint16_t* residual, uint16_t* y,
+                                                    float* y_f32) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, half = lane >> 5, sl = lane & 31;
+  const int base = (blockIdx.x * 4 + wave) * (2 * P);
+  u32x4 c[P];
+  uint32_t sv[P], bv[P];
+#pragma unroll
+  for (int p = 0; p < P; ++p) {
+    const int r = base + 2 * p + half;
+    const int rl = r < m.n ? r : 0;
+    c[p] = *reinterpret_cast<const u32x4*>(m.w + (size_t)rl * 128 + sl * 4);
+    sv[p] = m.s[(size_t)rl * 16 + sl / 2];
+    bv[p] = m.b[(size_t)rl * 16 + sl / 2];
+  }
+  float xv[32], xr[32];
+  load_bf16x32(x + sl * 32, xv);
+  const float xs = prep_slice(xv, xr);
+#pragma unroll
+  for (int p = 0; p < P; ++p) {
+    const int r = base + 2 * p + half;
+    float part = bf2f(sv[p]) * q4_dot32(c[p], xr) + xs * bf2f(bv[p]);
+    part = half_sum(part);
+    if (sl == 0 && r < m.n) {
+      if (y_f32) y_f32[r] = part;
+      if (ADD) y[r] = (uint16_t)f2bf(bf2f(residual[r]) + rbf(part));
+      else y[r] = (uint16_t)f2bf(part);
+    }
+  }
+}
+
+// Wide rows (1024 < K <= 4096): a whole wave per row, lane slices l and l+64.
+template <int P, bool ADD>
+__global__ __launch_bounds__(256) void k_qmv_wide(Q4 m, const uint16_t* x,
+                                                  const uint16_t* residual, uint16_t* y,
+                                                  float* y_f32) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int ns = m.k >> 5;
+  const bool v1 = lane < ns, v2 = lane + 64 < ns;
+  const int wpr = m.k >> 3, gpr = m.k >> 6;
+  const int s1 = v1 ? lane : 0, s2 = v2 ? lane + 64 : 0;
+  const int base = (blockIdx.x * 4 + wave) * P;
+  u32x4 c1[P], c2[P];
+  uint32_t sa[P], ba[P], sb[P], bb[P];
+#pragma unroll
+  for (int p = 0; p < P; ++p) {
+    const int r = base + p;
+    const size_t rl = r < m.n ? r : 0;
+    c1[p] = *reinterpret_cast<const u32x4*>(m.w + rl * wpr + s1 * 4);
+    sa[p] = m.s[rl * gpr + s1 / 2];
+    ba[p] = m.b[rl * gpr + s1 / 2];
+    if (v2) {
+      c2[p] = *reinterpret_cast<const u32x4*>(m.w + rl * wpr + s2 * 4);
+      sb[p] = m.s[rl * gpr + s2 / 2];
+      bb[p] = m.b[rl * gpr + s2 / 2];
+    } else {
+      c2[p] = u32x4{0u, 0u, 0u, 0u};
+      sb[p] = 0u;
+      bb[p] = 0u;
+    }
+  }
+  float xv[32], xr1[32], xr2[32];
+  float xs1 = 0.0f, xs2 = 0.0f;
+  if (v1) {
+    load_bf16x32(x + lane * 32, xv);
+    xs1 = prep_slice(xv, xr1);
+  } else {
+#pragma unroll
+    for (int j = 0; j < 32; ++j) xr1[j] = 0.0f;
+  }
+  if (v2) {
+    load_bf16x32(x + (lane + 64) * 32, xv);
+    xs2 = prep_slice(xv, xr2);
+  } else {
+#pragma unroll
+    for (int j = 0; j < 32; ++j) xr2[j] = 0.0f;
+  }
+#pragma unroll
+  for (int p = 0; p < P; ++p) {
+    const int r = base + p;
+    float part = 0.0f;
+    if (v1) part = bf2f(sa[p]) * q4_dot32(c1[p], xr1) + xs1 * bf2f(ba[p]);
+    if (v2) part += bf2f(sb[p]) * q4_dot32(c2[p], xr2) + xs2 * bf2f(bb[p]);
+    part = wave_sum(part);
+    if (lane == 0 && r < m.n) {
+      if (y_f32) y_f32[r] = part;
+      if (ADD) y[r] = (uint16_t)f2bf(bf2f(residual[r]) + rbf(part));
+      else y[r] = (uint16_t)f2bf(part);
+    }
+  }
+}
+
+// Gated RMSNorm (gdn.metal:238-254) computed once per block into LDS, then
+// out_proj (K=2048) with residual. Element k lives at xg[k + k/32] so each
+// lane's 32-element slice reads without bank conflicts.
+template <int P>
+__global__ __launch_bounds__(256) void k_gdn_gate_out(Q4 m, const uint16_t* y, const uint16_t* z,
+                                                      const uint16_t* norm_w, uint16_t* h,
+                                                      uint16_t* gated_out) {
+  __shared__ float xg[2048 + 64];
+  const int t = threadIdx.x;
+  const int lane = t & 63, wave = t >> 6;
+  const int base = (blockIdx.x * 4 + wave) * P;
+  u32x4 c[P];
+  uint32_t sv[P], bv[P];
+#pragma unroll
+  for (int p = 0; p < P; ++p) {
+    const int r = base + p;
+    const size_t rl = r < m.n ? r : 0;
+    c[p] = *reinterpret_cast<const u32x4*>(m.w + rl * 256 + lane * 4);
+    sv[p] = m.s[rl * 32 + lane / 2];
+    bv[p] = m.b[rl * 32 + lane / 2];
+  }
+  {
+    const int e0 = (t >> 4) * 128 + (t & 15) * 8;  // head t/16, eight channels
+    const u32x4 yv = *reinterpret_cast<const u32x4*>(y + e0);
+    const u32x4 zv = *reinterpret_cast<const u32x4*>(z + e0);
+    const u32x4 wv = *reinterpret_cast<const u32x4*>(norm_w + (t & 15) * 8);
+    float yf[8], zf[8], wf[8];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      yf[2 * j] = bf_lo(yv[j]); yf[2 * j + 1] = bf_hi(yv[j]);
+      zf[2 * j] = bf_lo(zv[j]); zf[2 * j + 1] = bf_hi(zv[j]);
+      wf[2 * j] = bf_lo(wv[j]); wf[2 * j + 1] = bf_hi(wv[j]);
+    }
+    float ss = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) ss += yf[i] * yf[i];
+    ss = row16_sum(ss);
+    const float inv = 1.0f / sqrtf(ss / 128.0f + 1e-6f);
+    uint32_t packed[4];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const float norm = rbf(rbf(yf[i] * inv) * wf[i]);
+      const float gz = zf[i];
+      const float sy = 1.0f / (1.0f + expf(fabsf(gz)));
+      const float sig = gz < 0.0f ? sy : 1.0f - sy;
+      const float g = rbf((gz * sig) * norm);
+      const int e = e0 + i;
+      xg[e + (e >> 5)] = g;
+      if (i & 1) packed[i >> 1] |= f2bf(g) << 16;
+      else packed[i >> 1] = f2bf(g);
+    }
+    if (gated_out && blockIdx.x == 0)
+      *reinterpret_cast<u32x4*>(gated_out + e0) = u32x4{packed[0], packed[1], packed[2], packed[3]};
+  }
+  __syncthreads();
+  float xv[32], xr[32];
+#pragma unroll
+  for (int j = 0; j < 32; ++j) xv[j] = xg[lane * 33 + j];
+  const float xs = prep_slice(xv, xr);
+#pragma unroll
+  for (int p = 0; p < P; ++p) {
+    const int r = base + p;
+    float part = bf2f(sv[p]) * q4_dot32(c[p], xr) + xs * bf2f(bv[p]);
+    part = wave_sum(part);
+    if (lane == 0 && r < m.n) h[r] = (uint16_t)f2bf(bf2f(h[r]) + rbf(part));
+  }
+}
+
+__global__ __launch_bounds__(256) void k_embedding(Q4 e, const uint32_t* token, uint16_t* out) {
+  uint32_t tok = *token;
+  if (tok >= (uint32_t)e.n) tok = 0;
+  for (int k = threadIdx.x; k < e.k; k += blockDim.x) {
+    const uint32_t q = (e.w[(size_t)tok * (e.k / 8) + k / 8] >> (4 * (k % 8))) & 15u;
+    const size_t g = (size_t)tok * (e.k / 64) + k / 64;
+    out[k] = (uint16_t)f2bf(bf2f(e.s[g]) * (float)q + bf2f(e.b[g]));
+  }
+}
+
+bool q4_ok(const Q4& m) { return m.w && m.s && m.b && m.n > 0 && m.k > 0 && m.k % 64 == 0; }
+
+}  // namespace
+
+constexpr int kMultiP = 4;     // passes per wave: 8 rows per wave, 32 per block
+constexpr int kGateUpNP = 2;   // 4 output rows per wave, 16 per block
+constexpr int kNarrowP = 2;    // 4 rows per wave
+constexpr int kWideP = 1;      // 1 row per wave
+constexpr int kGateOutP = 2;   // 2 rows per wave, 8 per block
+
+hipError_t launch_norm_multi(const NormMultiArgs& a, hipStream_t s) {
+  if (a.count < 1 || a.count > 4 || !a.gain || (!a.x && !a.embed.w)) return hipErrorInvalidValue;
+  MultiDev d{};
+  int total = 0;
+  for (int i = 0; i < a.count; ++i) {
+    if (!q4_ok(a.m[i]) || a.m[i].k != kHidden || !a.y[i]) return hipErrorInvalidValue;
+    d.m[i] = a.m[i];
+    d.y[i] = a.y[i];
+    total += a.m[i].n;
+  }
+  if (a.embed.w && a.embed.k != kHidden) return hipErrorInvalidValue;
+  if (a.ring0 && !a.st) {
+    if (a.pos_val < 0) return hipErrorInvalidValue;
+  }
+  d.count = a.count;
+  d.total = total;
+  d.ring0 = a.ring0;
+  d.x = a.x;
+  d.gain = a.gain;
+  d.norm_out = a.norm_out;
+  d.embed = a.embed;
+  d.h_out = a.h_out;
+  d.token_val = a.token_val;
+  d.st = a.st;
+  d.pos_val = a.pos_val;
+  const int rows_per_block = 4 * 2 * kMultiP;
+  const int blocks = (total + rows_per_block - 1) / rows_per_block;
+  hipLaunchKernelGGL(k_norm_multi<kMultiP>, dim3(blocks), dim3(256), 0, s, d);
+  return hipGetLastError();
+}
+
+hipError_t launch_norm_gate_up(const Q4& gate, const Q4& up, const uint16_t* x,
+                               const uint16_t* gain, uint16_t* norm_out, uint16_t* act,
+                               hipStream_t s) {
+  if (!q4_ok(gate) || !q4_ok(up) || gate.k != kHidden || up.k != kHidden || gate.n != up.n ||
+      !x || !gain || !act)
+    return hipErrorInvalidValue;
+  const int rows_per_block = 4 * 2 * kGateUpNP;
+  const int blocks = (gate.n + rows_per_block - 1) / rows_per_block;
+  hipLaunchKernelGGL(k_norm_gate_up<kGateUpNP>, dim3(blocks), dim3(256), 0, s, gate, up, x, gain,
+                     norm_out, act);
+  return hipGetLastError();
+}
+
+hipError_t launch_qmv(const Q4& w, const uint16_t* x, const uint16_t* residual, uint16_t* y,
+                      float* y_f32, hipStream_t s) {
+  if (!q4_ok(w) || !x || !y) return hipErrorInvalidValue;
+  if (w.k == kHidden) {
+    const int rpb = 4 * 2 * kNarrowP;
+    const int blocks = (w.n + rpb - 1) / rpb;
+    if (residual)
+      hipLaunchKernelGGL((k_qmv_narrow<kNarrowP, true>), dim3(blocks), dim3(256), 0, s, w, x,
+                         residual, y, y_f32);
+    else
+      hipLaunchKernelGGL((k_qmv_narrow<kNarrowP, false>), dim3(blocks), dim3(256), 0, s, w, x,
+                         residual, y, y_f32);
+  } else if (w.k > kHidden && w.k <= 4096) {
+    const int rpb = 4 * kWideP;
+    const int blocks = (w.n + rpb - 1) / rpb;
+    if (residual)
+      hipLaunchKernelGGL((k_qmv_wide<kWideP, true>), dim3(blocks), dim3(256), 0, s, w, x,
+                         residual, y, y_f32);
+    else
+      hipLaunchKernelGGL((k_qmv_wide<kWideP, false>), dim3(blocks), dim3(256), 0, s, w, x,
+                         residual, y, y_f32);
+  } else {
+    return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
+hipError_t launch_gdn_gate_out(const Q4& w, const uint16_t* y, const uint16_t* z,
+                               const uint16_t* norm_w, uint16_t* h, uint16_t* gated_out,
+                               hipStream_t s) {
+  if (!q4_ok(w) || w.k != 2048 || w.n != kHidden || !y || !z || !norm_w || !h)
+    return hipErrorInvalidValue;
+  const int rpb = 4 * kGateOutP;
+  const int blocks = (w.n + rpb - 1) / rpb;
+  hipLaunchKernelGGL(k_gdn_gate_out<kGateOutP>, dim3(blocks), dim3(256), 0, s, w, y, z, norm_w, h,
+                     gated_out);
+  return hipGetLastError();
+}
+
+hipError_t launch_embedding(const Q4& table, const uint32_t* token_dev, uint16_t* out,
+                            hipStream_t s) {
+  if (!q4_ok(table) || !token_dev || !out) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(k_embedding, dim3(1), dim3(256), 0, s, table, token_dev, out);
+  return hipGetLastError();
+}
+
+}  // namespace es

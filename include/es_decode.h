@@ -1,0 +1,235 @@
+/*
+ * es_decode.h -- C ABI of the MI355X decode engine (libesdecode.so).
+ *
+ * Two boundaries of the reference are kept:
+ *  1. the kernel/operator boundary: the LINEAR, GDN and ATTENTION kernel
+ *     interfaces (source/LINEAR_INTERFACE.md, source/GDN_INTERFACE.md,
+ *     source/ATTENTION_INTERFACE.md) that the reference reaches through
+ *     Gpu::dispatch (source/src/gpu.rs:177-187);
+ *  2. the engine boundary: Model::load / Model::generate / cancelled
+ *     (source/src/model.rs:28-122), which the EngineSmith protocol server
+ *     (source/src/main.rs:10-53, docs/protocol.md) drives.
+ *
+ * Conventions (as in the reference): tensors are positional, row-major, bf16
+ * values are raw uint16_t, Q4 weights are the MLX affine 4-bit group-64
+ * triple. Operator pointers are DEVICE pointers owned by the caller; no
+ * operator allocates. `stream` is a hipStream_t (NULL = default stream); ops
+ * are asynchronous on it. Every function returns 0 (ES_OK) or an error code,
+ * with a message from es_last_error() (thread-local). Launch failures are
+ * reported when detected; asynchronous device faults surface at the next
+ * synchronising call, as Gpu::wait reports them (gpu.rs:169-173).
+ * An engine instance is not thread-safe, except es_engine_cancel.
+ */
+#ifndef ES_DECODE_H
+#define ES_DECODE_H
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define ES_OK 0
+#define ES_ERR_INVALID 1   /* bad argument or request (reference `ensure!`) */
+#define ES_ERR_DEVICE 2    /* HIP runtime / launch failure */
+#define ES_ERR_CANCELLED 3 /* input disconnected (model.rs:133) */
+
+/* Text of the last error on this thread ("" if none). */
+const char* es_last_error(void);
+
+/* Q4 affine group-64 weight: codes u32 [n, k/8] (nibble j of word w is column
+ * 8w+j), bf16 scales and biases [n, k/64]. Replaces `Linear` (weights.rs:8,
+ * 104-106). */
+typedef struct es_q4 {
+  const uint32_t* codes;
+  const uint16_t* scales;
+  const uint16_t* biases;
+  int32_t n;
+  int32_t k;
+} es_q4;
+
+/* ------------------------------------------------------------------ */
+/* Device plumbing (stands in for Gpu::new/buffer/zero/finish,         */
+/* gpu.rs:126-176)                                                     */
+/* ------------------------------------------------------------------ */
+int es_device_count(int* count);
+int es_device_name(int device, char* buf, int len);
+int es_set_device(int device);
+int es_malloc(void** ptr, size_t bytes);
+int es_free(void* ptr);
+int es_memcpy_htod(void* dst, const void* src, size_t bytes);
+int es_memcpy_dtoh(void* dst, const void* src, size_t bytes);
+int es_memset(void* dst, int value, size_t bytes);
+int es_synchronize(void);
+int es_stream_create(void** stream);
+int es_stream_destroy(void* stream);
+int es_stream_synchronize(void* stream);
+
+/* ------------------------------------------------------------------ */
+/* LINEAR interface (LINEAR_INTERFACE.md:16-25)                        */
+/* ------------------------------------------------------------------ */
+/* embedding_q4 (linear.metal:11-24): out[1024] = bf16(scale*q + bias) of
+ * row *token (token is a device pointer, as the reference's ids buffer). */
+int es_embedding_q4(const es_q4* table, const uint32_t* token, uint16_t* out, void* stream);
+
+/* qmv_q4 (linear.metal:28-73), M=1: y[n] = bf16(W x). k == 1024, or
+ * 1024 < k <= 4096 with k % 64 == 0. y_f32 (optional) gets the fp32 sums. */
+int es_q4_matvec(const es_q4* w, const uint16_t* x, uint16_t* y, float* y_f32, void* stream);
+
+/* qmv_add_q4 (linear.metal:77-123): y = bf16(residual + bf16(W x)).
+ * y may alias residual; x must not alias y (LINEAR_INTERFACE.md:35-36). */
+int es_q4_matvec_add(const es_q4* w, const uint16_t* x, const uint16_t* residual, uint16_t* y,
+                     void* stream);
+
+/* qmv_multi_g8_norm (linear_input_norm.metal:13-119) with the rms_norm_bf16
+ * arithmetic (linear.metal:300-331): u = bf16(bf16(x*rsqrt(mean(x^2)+1e-6))*gain)
+ * over 1024 columns, then y[i] = bf16(W_i u) for count (1..4) matrices of
+ * k = 1024. norm_out (optional) receives u. */
+int es_q4_rmsnorm_matvec_multi(const es_q4* w, int count, const uint16_t* x, const uint16_t* gain,
+                               uint16_t* norm_out, uint16_t* const* y, void* stream);
+
+/* qmv_mlp_g8_norm (linear_norm.metal:10-104): u = RMSNorm(x)*gain, then
+ * act = bf16(bf16(g*sigmoid_bf(g)) * up) with g = bf16(Wg u), up = bf16(Wu u). */
+int es_q4_rmsnorm_gate_up_swiglu(const es_q4* gate, const es_q4* up, const uint16_t* x,
+                                 const uint16_t* gain, uint16_t* norm_out, uint16_t* act,
+                                 void* stream);
+
+/* ------------------------------------------------------------------ */
+/* GDN interface (GDN_INTERFACE.md:12-18; decode fusion gdn_input.metal) */
+/* ------------------------------------------------------------------ */
+/* Convolution history is kept as a ring of the last four raw qkv projections,
+ * ring [4, 6144] bf16, slot = position & 3. The reference's history [3, 6144]
+ * (oldest first) maps to ring slots (position-3)&3, (position-2)&3,
+ * (position-1)&3; nothing is shifted. A reset ring is all zeros, as the
+ * reference's reset history (model.rs:95). */
+
+/* Projection half of gdn_input_g16 (gdn_input.metal:109-155): u = RMSNorm(x)*gain
+ * (1024), raw qkv = W_qkv u written to ring slot (position & 3), z = W_z u
+ * [2048], ab = [W_a u (16) | W_b u (16)]. */
+int es_gdn_in_proj(const es_q4* qkv, const es_q4* z, const es_q4* a, const es_q4* b,
+                   const uint16_t* x, const uint16_t* gain, uint16_t* norm_out, uint16_t* ring,
+                   int position, uint16_t* z_out, uint16_t* ab_out, void* stream);
+
+/* Convolution/preparation half of gdn_input_g16 (gdn_input.metal:157-205,
+ * == gdn_conv_prepare_decode, gdn.metal:121-171) fused with gdn_recur
+ * (gdn.metal:176-228), T=1: conv over ring slots position-3..position, SiLU,
+ * Q/K L2 norm, g/beta gates, delta-rule update of state [16,128v,128k] fp32 in
+ * place, y [2048] bf16. Optional debug outputs: qkv_out [6144] (normalised
+ * q|k, activated v), g_out [16] fp32, beta_out [16] bf16. */
+int es_gdn_recur_step(const uint16_t* ring, int position, const uint16_t* conv_w,
+                      const uint16_t* ab, const float* a_log, const uint16_t* dt_bias,
+                      float* state, uint16_t* y, uint16_t* qkv_out, float* g_out,
+                      uint16_t* beta_out, void* stream);
+
+/* gdn_norm_gate (gdn.metal:230-255) feeding out_proj with the residual
+ * (qmv_add_q4, model.rs:265): h = bf16(h + bf16(W_out gated)) in place.
+ * gated_out (optional) receives the gated vector [2048]. */
+int es_gdn_gate_out_proj(const es_q4* out_proj, const uint16_t* y, const uint16_t* z,
+                         const uint16_t* norm_w, uint16_t* h, uint16_t* gated_out, void* stream);
+
+/* ------------------------------------------------------------------ */
+/* ATTENTION interface (ATTENTION_INTERFACE.md:13-29, 75-105)          */
+/* ------------------------------------------------------------------ */
+/* Rotary inverse frequencies (attention.metal:62-63), 32 fp32 values on the
+ * host; the attention op reads them from a device copy. */
+int es_rope_inv_freq(float* host_out32);
+
+/* Scratch bytes es_attn_decode needs for `splits` KV splits (1..1024). */
+size_t es_attn_scratch_bytes(int splits);
+
+/* attn_prepare_qkv_decode (attention.metal:262-313) + decode attention with
+ * the output gate: attn_decode/attn_gate for short contexts and
+ * attn_decode_split1 + attn_decode_split2_gate for long ones
+ * (attention_decode.metal:51-431, 830-891; model.rs:318-347), as one split-K
+ * flash decode. q_proj [8,512] (query|gate), k_proj/v_proj [2,256]; writes
+ * K/V row `position` of kcache/vcache [2, capacity, 256] and
+ * gated [8,256] = bf16(bf16(attn) * sigmoid_bf(gate)). Attends to positions
+ * 0..position. query_out (optional) receives the roped queries [8,256]. */
+int es_attn_decode(const uint16_t* q_proj, const uint16_t* k_proj, const uint16_t* v_proj,
+                   const uint16_t* q_gain, const uint16_t* k_gain, uint16_t* kcache,
+                   uint16_t* vcache, int capacity, int position, const float* inv_freq,
+                   int splits, void* scratch, size_t scratch_bytes, uint16_t* gated,
+                   uint16_t* query_out, void* stream);
+
+/* ------------------------------------------------------------------ */
+/* Vocab head (head_lse.metal:11-98 with rms_norm_bf16, model.rs:290-300) */
+/* ------------------------------------------------------------------ */
+/* Scratch for es_head_greedy: per-block (max, sum exp) partials. */
+size_t es_head_scratch_bytes(int vocab);
+
+/* u = RMSNorm(h)*gain; logits[vocab] = bf16(E u) over the tied table;
+ * lse = bf16(log(sum exp) + max) over the bf16 logits; *token = lowest index
+ * of max bf16(logit - lse) (docs/protocol.md:44). token/lse are device
+ * pointers; norm_out and lse are optional. */
+int es_head_greedy(const es_q4* embed, const uint16_t* h, const uint16_t* gain,
+                   uint16_t* norm_out, uint16_t* logits, void* scratch, size_t scratch_bytes,
+                   uint32_t* token, float* lse, void* stream);
+
+/* ------------------------------------------------------------------ */
+/* Model weights (weights.rs:11-44 checks; model.rs:41-78 names)        */
+/* ------------------------------------------------------------------ */
+/* The host weight blob holds every tensor at a 256-byte aligned offset, named
+ * as the checkpoint's language_model.model.* tensors. dtype: 0 u32, 1 bf16,
+ * 2 f32. Layer l is full attention when l % 4 == 3 (model.rs:51). */
+size_t es_weights_total_bytes(int n_layers, int vocab);
+int es_weights_tensor_count(int n_layers);
+int es_weights_tensor_info(int n_layers, int vocab, int index, char* name, int name_len,
+                           uint64_t* offset, uint64_t* bytes, int* dtype);
+/* Seeded random-init model (Q4 of N(0,0.02) weights, see es_weights.hpp). */
+int es_weights_random(int n_layers, int vocab, uint64_t seed, void* blob, size_t bytes,
+                      int threads);
+
+/* ------------------------------------------------------------------ */
+/* Engine (Model::load / generate / cancelled, model.rs:28-180)        */
+/* ------------------------------------------------------------------ */
+typedef struct es_engine es_engine;
+
+/* Model::load (model.rs:37-92) from a host blob; capacity = KV positions
+ * (reference CAPACITY 262144, model.rs:8). NULL on failure. */
+es_engine* es_engine_create(const void* blob, size_t bytes, int n_layers, int vocab,
+                            int capacity);
+void es_engine_destroy(es_engine* e);
+
+/* Model::generate (model.rs:97-122): reset=1 consumes prompt[len] (len>0)
+ * and emits max_tokens greedy ids; reset=0 requires len==0 and first consumes
+ * the last emitted token. out[max_tokens] is host memory. On error the request
+ * is rejected with the reference's messages; after a device error or a
+ * cancellation the state is reset (model.rs:175-178). */
+int es_engine_generate(es_engine* e, const uint32_t* prompt, int len, int max_tokens, int reset,
+                       uint32_t* out);
+
+/* cancelled.store(true) (main.rs:24): the running request stops at its next
+ * step boundary, drains, resets and fails with ES_ERR_CANCELLED. */
+void es_engine_cancel(es_engine* e);
+void es_engine_clear_cancel(es_engine* e);
+int es_engine_position(const es_engine* e);
+
+/* Teacher forcing (docs/protocol.md:61-63): step i consumes tokens[i]; the
+ * greedy pick after it goes to argmax[i]; logits (optional host [n, vocab]). */
+int es_engine_forced_decode(es_engine* e, const uint32_t* tokens, int n, uint32_t* argmax,
+                            uint16_t* logits);
+
+/* State handoff to/from host memory. which: 0 K cache, 1 V cache; KV data is
+ * [2 heads, count, 256] bf16 for positions pos0..pos0+count-1. */
+int es_engine_read_kv(es_engine* e, int layer, int which, int pos0, int count, void* host);
+int es_engine_write_kv(es_engine* e, int layer, int which, int pos0, int count,
+                       const void* host);
+/* GDN layer ring [4,6144] bf16 and state [16,128,128] fp32; NULL skips one. */
+int es_engine_read_gdn(es_engine* e, int layer, void* ring, void* state);
+int es_engine_write_gdn(es_engine* e, int layer, const void* ring, const void* state);
+/* Declare that `position` tokens are consumed and `pending` is next. */
+int es_engine_set_position(es_engine* e, int position, uint32_t pending);
+/* Synthetic context of `length` consumed tokens (benchmarks). */
+int es_engine_fill_synthetic(es_engine* e, int length, uint64_t seed, uint32_t pending);
+
+/* Timing with HIP events on the engine stream. */
+int es_engine_time_decode(es_engine* e, int steps, int warmup, double* ms_total);
+int es_engine_time_attention(es_engine* e, int layer, int reps, double* ms_avg);
+int es_engine_time_head(es_engine* e, int reps, double* ms_avg);
+/* KV splits the engine uses at attention length `length`. */
+int es_engine_splits_for(int length);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

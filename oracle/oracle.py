@@ -1,0 +1,304 @@
+"""ctypes binding of the CPU oracle (libesoracle.so).
+
+TEST INFRASTRUCTURE ONLY: used by tests/, __graft_entry__.smoke() and
+bench.py's cpu_baseline leg as the parity checker / timed CPU baseline.
+The engine never imports this module.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import subprocess
+from ctypes import POINTER, c_float, c_int, c_uint16, c_uint32, c_void_p
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libesoracle.so")
+
+
+def build() -> None:
+    subprocess.run(["make", "-B", "-C", HERE], check=True, stdout=subprocess.DEVNULL)
+
+
+class Linear(ctypes.Structure):
+    _fields_ = [("w", c_void_p), ("s", c_void_p), ("b", c_void_p), ("n", c_int), ("k", c_int)]
+
+
+class Layer(ctypes.Structure):
+    _fields_ = [("is_attention", c_int), ("input_norm", c_void_p), ("post_norm", c_void_p),
+                ("gate", Linear), ("up", Linear), ("down", Linear),
+                ("qkv", Linear), ("z", Linear), ("a", Linear), ("b", Linear), ("out", Linear),
+                ("conv_w", c_void_p), ("gdn_norm", c_void_p), ("dt_bias", c_void_p), ("a_log", c_void_p),
+                ("q", Linear), ("k", Linear), ("v", Linear), ("o", Linear),
+                ("q_norm", c_void_p), ("k_norm", c_void_p)]
+
+
+class Model(ctypes.Structure):
+    _fields_ = [("n_layers", c_int), ("vocab", c_int), ("embed", Linear), ("final_norm", c_void_p),
+                ("layers", Layer * 64)]
+
+
+class State(ctypes.Structure):
+    _fields_ = [("capacity", c_int), ("history", c_void_p * 64), ("state", c_void_p * 64),
+                ("kcache", c_void_p * 64), ("vcache", c_void_p * 64)]
+
+
+_lib = None
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise FileNotFoundError(f"{LIB_PATH} missing: run make -C oracle")
+        L = ctypes.CDLL(LIB_PATH)
+        vp = c_void_p
+        sig = {
+            "eo_bf16_to_f32": (c_float, [c_uint16]),
+            "eo_f32_to_bf16": (c_uint16, [c_float]),
+            "eo_round_bf16": (c_float, [c_float]),
+            "eo_f32_to_bf16_array": (None, [vp, vp, ctypes.c_size_t]),
+            "eo_sigmoid_bf": (c_float, [c_float]),
+            "eo_softplus_bf": (c_float, [c_float]),
+            "eo_rope_inv_freq": (c_float, [c_int]),
+            "eo_embedding": (None, [vp, vp, vp, c_int, c_uint32, vp]),
+            "eo_q4_matvec": (None, [vp, vp, vp, c_int, c_int, vp, vp, vp]),
+            "eo_q4_matvec_add": (None, [vp, vp, vp, c_int, c_int, vp, vp, vp]),
+            "eo_rms_norm": (None, [vp, vp, c_int, c_float, vp]),
+            "eo_swiglu": (None, [vp, vp, c_int, vp]),
+            "eo_gdn_conv_prepare": (None, [vp, vp, vp, vp, vp, vp, vp, vp, vp, vp]),
+            "eo_gdn_recur": (None, [vp, vp, vp, vp, vp]),
+            "eo_gdn_norm_gate": (None, [vp, vp, vp, vp]),
+            "eo_attn_prepare": (None, [vp, vp, vp, vp, vp, vp, vp, vp, c_int, c_int]),
+            "eo_attn_decode_single": (None, [vp, vp, vp, c_int, c_int, vp]),
+            "eo_attn_decode_split": (None, [vp, vp, vp, c_int, c_int, vp, vp, vp]),
+            "eo_attn_split_merge_gate": (None, [vp, vp, vp, vp, vp]),
+            "eo_attn_gate": (None, [vp, vp, vp]),
+            "eo_attn_decode_gated": (None, [vp, vp, vp, c_int, c_int, vp, vp]),
+            "eo_greedy": (c_uint32, [vp, c_int, POINTER(c_float)]),
+            "eo_model_step": (c_uint32, [POINTER(Model), POINTER(State), c_uint32, c_int, c_int, vp, vp]),
+            "eo_num_threads": (c_int, []),
+            "eo_set_num_threads": (None, [c_int]),
+        }
+        for name, (res, args) in sig.items():
+            fn = getattr(L, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = L
+    return _lib
+
+
+def P(a: np.ndarray | None):
+    return None if a is None else a.ctypes.data
+
+
+# ---- numerics helpers (numpy, independent of the C code) ----
+def bf16_to_f32(a: np.ndarray) -> np.ndarray:
+    return (np.asarray(a, dtype=np.uint16).astype(np.uint32) << 16).view(np.float32)
+
+
+def f32_to_bf16(a: np.ndarray) -> np.ndarray:
+    a = np.ascontiguousarray(a, dtype=np.float32)
+    out = np.empty(a.shape, dtype=np.uint16)
+    lib().eo_f32_to_bf16_array(P(a), P(out), a.size)
+    return out
+
+
+# ---- op wrappers ----
+def q4_matvec(codes, scales, biases, x, want_f32=False):
+    n, k8 = codes.shape
+    y = np.empty(n, dtype=np.uint16)
+    yf = np.empty(n, dtype=np.float32)
+    lib().eo_q4_matvec(P(codes), P(scales), P(biases), n, k8 * 8, P(x), P(y), P(yf))
+    return (y, yf) if want_f32 else y
+
+
+def q4_matvec_add(codes, scales, biases, x, residual):
+    n, k8 = codes.shape
+    y = np.empty(n, dtype=np.uint16)
+    lib().eo_q4_matvec_add(P(codes), P(scales), P(biases), n, k8 * 8, P(x), P(residual), P(y))
+    return y
+
+
+def embedding(codes, scales, biases, token):
+    out = np.empty(1024, dtype=np.uint16)
+    lib().eo_embedding(P(codes), P(scales), P(biases), 1024, int(token), P(out))
+    return out
+
+
+def rms_norm(x, gain, eps=1e-6):
+    out = np.empty(x.size, dtype=np.uint16)
+    lib().eo_rms_norm(P(x), P(gain), x.size, eps, P(out))
+    return out
+
+
+def swiglu(gate, up):
+    out = np.empty(gate.size, dtype=np.uint16)
+    lib().eo_swiglu(P(gate), P(up), gate.size, P(out))
+    return out
+
+
+def gdn_conv_prepare(raw, history, conv_w, a, b, a_log, dt_bias):
+    """history [3,6144] is updated in place; returns conv_out, g, beta."""
+    conv = np.empty(6144, dtype=np.uint16)
+    g = np.empty(16, dtype=np.float32)
+    beta = np.empty(16, dtype=np.uint16)
+    lib().eo_gdn_conv_prepare(P(raw), P(history), P(conv_w), P(a), P(b), P(a_log), P(dt_bias), P(conv), P(g),
+                              P(beta))
+    return conv, g, beta
+
+
+def gdn_recur(conv, g, beta, state):
+    """state [16,128,128] fp32 updated in place; returns y [2048]."""
+    y = np.empty(2048, dtype=np.uint16)
+    lib().eo_gdn_recur(P(conv), P(g), P(beta), P(state), P(y))
+    return y
+
+
+def gdn_norm_gate(y, z, w):
+    out = np.empty(2048, dtype=np.uint16)
+    lib().eo_gdn_norm_gate(P(y), P(z), P(w), P(out))
+    return out
+
+
+def attn_prepare(q_proj, k, v, q_gain, k_gain, kcache, vcache, position, capacity):
+    query = np.empty(2048, dtype=np.uint16)
+    lib().eo_attn_prepare(P(q_proj), P(k), P(v), P(q_gain), P(k_gain), P(query), P(kcache), P(vcache), position,
+                          capacity)
+    return query
+
+
+def attn_decode_single(query, kcache, vcache, length, capacity):
+    out = np.empty(2048, dtype=np.uint16)
+    lib().eo_attn_decode_single(P(query), P(kcache), P(vcache), length, capacity, P(out))
+    return out
+
+
+def attn_decode_split(query, kcache, vcache, length, capacity):
+    partials = np.empty((8, 64, 256), dtype=np.uint16)
+    sums = np.empty((8, 64), dtype=np.float32)
+    maxs = np.empty((8, 64), dtype=np.float32)
+    lib().eo_attn_decode_split(P(query), P(kcache), P(vcache), length, capacity, P(partials), P(sums), P(maxs))
+    return partials, sums, maxs
+
+
+def attn_split_merge_gate(partials, sums, maxs, q_proj):
+    out = np.empty(2048, dtype=np.uint16)
+    lib().eo_attn_split_merge_gate(P(partials), P(sums), P(maxs), P(q_proj), P(out))
+    return out
+
+
+def attn_gate(o, q_proj):
+    out = np.empty(2048, dtype=np.uint16)
+    lib().eo_attn_gate(P(o), P(q_proj), P(out))
+    return out
+
+
+def attn_decode_gated(query, kcache, vcache, length, capacity, q_proj):
+    out = np.empty(2048, dtype=np.uint16)
+    lib().eo_attn_decode_gated(P(query), P(kcache), P(vcache), length, capacity, P(q_proj), P(out))
+    return out
+
+
+def greedy(logits):
+    lse = c_float()
+    tok = lib().eo_greedy(P(logits), logits.size, ctypes.byref(lse))
+    return int(tok), float(lse.value)
+
+
+# ---- full model ----
+class OracleModel:
+    """Oracle model over a weight blob (host views), plus its decode state."""
+
+    def __init__(self, views: dict, n_layers: int, vocab: int, capacity: int):
+        self.views = views  # keep arrays alive
+        self.n_layers, self.vocab, self.capacity = n_layers, vocab, capacity
+        m = Model()
+        m.n_layers, m.vocab = n_layers, vocab
+
+        def lin(name, n, k):
+            return Linear(P(views[name + ".weight"]), P(views[name + ".scales"]), P(views[name + ".biases"]), n, k)
+
+        m.embed = lin("embed_tokens", vocab, 1024)
+        m.final_norm = P(views["norm.weight"])
+        self.history, self.state, self.kcache, self.vcache = {}, {}, {}, {}
+        st = State()
+        st.capacity = capacity
+        for l in range(n_layers):
+            p = f"layers.{l}"
+            L = m.layers[l]
+            L.is_attention = 1 if l % 4 == 3 else 0
+            L.input_norm = P(views[p + ".input_layernorm.weight"])
+            L.post_norm = P(views[p + ".post_attention_layernorm.weight"])
+            L.gate = lin(p + ".mlp.gate_proj", 3584, 1024)
+            L.up = lin(p + ".mlp.up_proj", 3584, 1024)
+            L.down = lin(p + ".mlp.down_proj", 1024, 3584)
+            if L.is_attention:
+                a = p + ".self_attn"
+                L.q = lin(a + ".q_proj", 4096, 1024)
+                L.k = lin(a + ".k_proj", 512, 1024)
+                L.v = lin(a + ".v_proj", 512, 1024)
+                L.o = lin(a + ".o_proj", 1024, 2048)
+                L.q_norm = P(views[a + ".q_norm.weight"])
+                L.k_norm = P(views[a + ".k_norm.weight"])
+                self.kcache[l] = np.zeros((2, capacity, 256), dtype=np.uint16)
+                self.vcache[l] = np.zeros((2, capacity, 256), dtype=np.uint16)
+                st.kcache[l] = P(self.kcache[l])
+                st.vcache[l] = P(self.vcache[l])
+            else:
+                g = p + ".linear_attn"
+                L.qkv = lin(g + ".in_proj_qkv", 6144, 1024)
+                L.z = lin(g + ".in_proj_z", 2048, 1024)
+                L.a = lin(g + ".in_proj_a", 16, 1024)
+                L.b = lin(g + ".in_proj_b", 16, 1024)
+                L.out = lin(g + ".out_proj", 1024, 2048)
+                L.conv_w = P(views[g + ".conv1d.weight"])
+                L.gdn_norm = P(views[g + ".norm.weight"])
+                L.dt_bias = P(views[g + ".dt_bias"])
+                L.a_log = P(views[g + ".A_log"])
+                self.history[l] = np.zeros((3, 6144), dtype=np.uint16)
+                self.state[l] = np.zeros((16, 128, 128), dtype=np.float32)
+                st.history[l] = P(self.history[l])
+                st.state[l] = P(self.state[l])
+        self.m, self.st = m, st
+        self.position = 0
+
+    def reset(self):
+        for a in self.history.values():
+            a[...] = 0
+        for a in self.state.values():
+            a[...] = 0
+        self.position = 0
+
+    def step(self, token: int, want_head: bool = True, want_logits: bool = False):
+        logits = np.empty(self.vocab, dtype=np.uint16) if want_logits else None
+        tok = lib().eo_model_step(ctypes.byref(self.m), ctypes.byref(self.st), int(token), self.position,
+                                  1 if want_head else 0, P(logits), None)
+        self.position += 1
+        return (int(tok), logits) if want_logits else int(tok)
+
+    def generate(self, prompt, count: int):
+        """Reference generate(reset=True): consume prompt, emit count greedy ids."""
+        self.reset()
+        for t in prompt[:-1]:
+            self.step(t, want_head=False)
+        out = []
+        tok = prompt[-1]
+        for _ in range(count):
+            tok = self.step(tok)
+            out.append(tok)
+        return out
+
+    def load_ring(self, layer: int, ring: np.ndarray, position: int):
+        """Engine ring [4,6144] -> reference history [3,6144] at `position`."""
+        for i in range(3):
+            self.history[layer][i] = ring[(position - 3 + i) & 3]
+
+
+def set_threads(n: int) -> None:
+    lib().eo_set_num_threads(int(n))
+
+
+def num_threads() -> int:
+    return int(lib().eo_num_threads())

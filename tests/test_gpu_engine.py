@@ -1,0 +1,166 @@
+"""GPU engine: full decode steps against the oracle model, request semantics
+of Model::generate (model.rs:97-180) and the protocol server (main.rs,
+docs/protocol.md).
+
+Agreement is judged teacher-forced (docs/protocol.md:61-63): the GPU's stream
+is replayed through the oracle; a step is a mismatch when the GPU token is
+not the oracle's greedy choice.
+"""
+import json
+import os
+import subprocess
+import tempfile
+
+import numpy as np
+import pytest
+
+import esdecode as E
+import oracle as O
+from helpers import rng
+
+pytestmark = pytest.mark.gpu
+
+SMALL = dict(n_layers=4, vocab=8192)
+
+
+@pytest.fixture(scope="module")
+def small():
+    blob = E.random_weights(SMALL["n_layers"], SMALL["vocab"], seed=5)
+    views = E.tensor_views(blob, **SMALL)
+    eng = E.Engine(blob, SMALL["n_layers"], SMALL["vocab"], capacity=4096)
+    orc = O.OracleModel(views, SMALL["n_layers"], SMALL["vocab"], capacity=4096)
+    yield eng, orc, blob
+    eng.close()
+
+
+def teacher_forced_mismatches(orc, prompt, gpu_tokens):
+    orc.reset()
+    for t in prompt[:-1]:
+        orc.step(t, want_head=False)
+    mism = 0
+    inp = prompt[-1]
+    for t in gpu_tokens:
+        if orc.step(inp) != t:
+            mism += 1
+        inp = t
+    return mism
+
+
+def test_generate_matches_oracle(small):
+    eng, orc, _ = small
+    r = rng(41)
+    prompt = r.integers(0, SMALL["vocab"], 40).tolist()
+    gpu = eng.generate(prompt, 24, reset=True)
+    assert eng.position == len(prompt) - 1 + 24
+    assert all(0 <= t < SMALL["vocab"] for t in gpu)
+    mism = teacher_forced_mismatches(orc, prompt, gpu)
+    assert mism <= 1, f"{mism} teacher-forced mismatches in 24 steps"
+
+
+def test_forced_decode_logits_close(small):
+    eng, orc, _ = small
+    r = rng(42)
+    prompt = r.integers(0, SMALL["vocab"], 17).tolist()
+    first = eng.generate(prompt, 1, reset=True)
+    forced = [first[0]] + r.integers(0, SMALL["vocab"], 7).tolist()
+    am, lg = eng.forced_decode(forced, want_logits=True)
+    orc.reset()
+    for t in prompt[:-1]:
+        orc.step(t, want_head=False)
+    orc.step(prompt[-1])
+    from helpers import f32
+    for i, t in enumerate(forced):
+        tok, logits = orc.step(t, want_logits=True)
+        d = np.abs(f32(lg[i]) - f32(logits))
+        assert d.max() <= 0.05 * np.abs(f32(logits)).max(), f"step {i}: logits diverged"
+        if tok != am[i]:
+            srt = np.sort(f32(logits))[::-1]
+            assert srt[0] - srt[1] <= 0.07, f"step {i}: mismatch without a near tie"
+
+
+def test_continuation_equals_monolithic(small):
+    """generate(P, a) + generate([], b) == generate(P, a+b) (model.rs:111-116)."""
+    eng, _, _ = small
+    r = rng(43)
+    prompt = r.integers(0, SMALL["vocab"], 33).tolist()
+    whole = eng.generate(prompt, 17, reset=True)
+    parts = eng.generate(prompt, 1, reset=True)
+    for n in (2, 4, 5, 5):
+        parts += eng.generate([], n, reset=False)
+    assert parts == whole
+
+
+def test_reset_isolation(small):
+    eng, _, _ = small
+    r = rng(44)
+    p1 = r.integers(0, SMALL["vocab"], 20).tolist()
+    p2 = r.integers(0, SMALL["vocab"], 20).tolist()
+    a = eng.generate(p1, 8, reset=True)
+    eng.generate(p2, 8, reset=True)
+    assert eng.generate(p1, 8, reset=True) == a
+
+
+def test_request_validation(small):
+    eng, _, _ = small
+    with pytest.raises(E.EsError, match="invalid output length"):
+        eng.generate([1, 2], 0, reset=True)
+    with pytest.raises(E.EsError, match="reset needs nonempty prompt"):
+        eng.generate([], 1, reset=True)
+    with pytest.raises(E.EsError, match="token outside vocabulary"):
+        eng.generate([SMALL["vocab"]], 1, reset=True)
+    with pytest.raises(E.EsError, match="context capacity exceeded"):
+        eng.generate([1] * 4000, 200, reset=True)
+    eng.generate([1, 2, 3], 2, reset=True)
+    with pytest.raises(E.EsError, match="continuation prompt must be empty"):
+        eng.generate([1], 1, reset=False)
+    # rejected requests keep the prior state (model.rs:98-103 run before reset)
+    assert eng.position == 4
+    eng.generate([], 1, reset=False)
+
+
+def test_cancel_fails_request_and_resets(small):
+    eng, _, _ = small
+    eng.generate([5, 6, 7], 2, reset=True)
+    eng.cancel()
+    with pytest.raises(E.EsError, match="input disconnected"):
+        eng.generate([], 3, reset=False)
+    eng.clear_cancel()
+    with pytest.raises(E.EsError, match="no continuation state"):
+        eng.generate([], 1, reset=False)
+
+
+def test_protocol_server(small, tmp_path):
+    """Requests go one at a time; each reply is read before the next request
+    (docs/protocol.md:14-17). Closing stdin ends the server."""
+    d = tmp_path / "model"
+    d.mkdir()
+    (d / "es_model.json").write_text(json.dumps(dict(seed=5, capacity=4096, **SMALL)))
+    eng, _, _ = small
+    prompt = [11, 22, 33, 44, 55]
+    expect = eng.generate(prompt, 6, reset=True)
+    p = subprocess.Popen([E.SERVER_PATH, "--model", str(d)], stdin=subprocess.PIPE, stdout=subprocess.PIPE,
+                         stderr=subprocess.PIPE, text=True)
+    try:
+        def ask(req):
+            p.stdin.write(json.dumps(req) + "\n")
+            p.stdin.flush()
+            return p.stdout.readline()
+
+        assert ask({"id": 1, "op": "hello"}) == '{"id":1,"ok":true,"protocol":1}\n'
+        assert json.loads(ask({"id": 2, "op": "generate", "prompt": prompt, "max_tokens": 2, "reset": True})) == \
+            {"id": 2, "ok": True, "tokens": expect[:2]}
+        assert json.loads(ask({"id": "x", "op": "generate", "prompt": [], "max_tokens": 4, "reset": False})) == \
+            {"id": "x", "ok": True, "tokens": expect[2:6]}
+        assert json.loads(ask({"id": 4, "op": "generate", "prompt": [], "max_tokens": 0, "reset": False})) == \
+            {"id": 4, "ok": False, "error": "invalid output length"}
+        assert json.loads(ask({"id": 5, "op": "bogus"})) == {"id": 5, "ok": False, "error": "unknown operation bogus"}
+        assert json.loads(ask({"id": 6, "op": "generate", "prompt": [1, -2], "max_tokens": 1, "reset": True})) == \
+            {"id": 6, "ok": False, "error": "invalid token"}
+        assert json.loads(ask({"op": "generate", "prompt": [1], "max_tokens": 1})) == \
+            {"id": None, "ok": False, "error": "missing reset"}
+        p.stdin.close()
+        assert p.wait(timeout=60) == 0
+    finally:
+        if p.poll() is None:
+            p.kill()
+            p.wait()
