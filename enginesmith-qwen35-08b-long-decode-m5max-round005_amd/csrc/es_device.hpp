@@ -1,9 +1,12 @@
 // Device-side helpers shared by the decode kernels (gfx950, wave64).
 //
-// bf16 values travel as raw uint16_t. f2bf is round-to-nearest-even, the
-// rounding every "bfloat(x)" in the reference kernels performs. The MLX
-// stepwise sigmoid and softplus keep the reference's bf16 boundaries
-// (linear.metal:389-395, gdn.metal:10-29).
+// Arithmetic contract. Every kernel computes in fp32 with the bf16 rounding
+// points of the reference (bf16 = round-to-nearest-even, v_cvt_pk_bf16_f32),
+// and with one fixed evaluation order: fused multiply-adds only where fmaf is
+// written (the library is built with -ffp-contract=off), sequential chains as
+// written, and cross-lane sums as pairwise trees in lane order (tree_n below).
+// exp, log and sin/cos are this file's own series evaluations, so results are
+// reproducible bit for bit by a host implementation of the same steps.
 #pragma once
 #include <hip/hip_runtime.h>
 #include <stdint.h>
@@ -24,39 +27,114 @@ constexpr int kKvProj = 512;      // 2 x 256
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
 
+// ---- bf16 ----
 __device__ __forceinline__ float bf2f(uint32_t b) { return __uint_as_float(b << 16); }
 __device__ __forceinline__ float bf_lo(uint32_t pair) { return __uint_as_float(pair << 16); }
 __device__ __forceinline__ float bf_hi(uint32_t pair) { return __uint_as_float(pair & 0xffff0000u); }
-
 __device__ __forceinline__ uint32_t f2bf(float f) {
-  uint32_t u = __float_as_uint(f);
-  if ((u & 0x7fffffffu) > 0x7f800000u) return (u >> 16) | 0x40u;
-  u += 0x7fffu + ((u >> 16) & 1u);
-  return u >> 16;
+  return (uint32_t)__builtin_bit_cast(uint16_t, (__bf16)f);
 }
-__device__ __forceinline__ float rbf(float f) { return bf2f(f2bf(f)); }
+__device__ __forceinline__ float rbf(float f) { return (float)(__bf16)f; }
+// Two values -> packed bf16 pair (lo in bits 0..15).
+__device__ __forceinline__ uint32_t pack_bf2(float lo, float hi) {
+  const bf16x2_t v = {(__bf16)lo, (__bf16)hi};
+  return __builtin_bit_cast(uint32_t, v);
+}
 
-// MLX unary sigmoid in bf16: round after exp, add, reciprocal, subtraction.
+// ---- series math (bit-reproducible on the host) ----
+// exp: x = n ln2 + r, |r| <= ln2/2, degree-7 Taylor polynomial of e^r, scaled
+// by 2^n. Inputs <= -86 give 0 (keeps every result a normal number).
+__device__ __forceinline__ float es_exp(float x) {
+  if (!(x > -86.0f)) return 0.0f;
+  if (x > 88.72f) return __builtin_inff();
+  const float n = rintf(x * 1.44269504088896341f);
+  float r = fmaf(n, -0.693145751953125f, x);
+  r = fmaf(n, -1.42860682030941723212e-6f, r);
+  float p = 1.0f / 5040.0f;
+  p = fmaf(p, r, 1.0f / 720.0f);
+  p = fmaf(p, r, 1.0f / 120.0f);
+  p = fmaf(p, r, 1.0f / 24.0f);
+  p = fmaf(p, r, 1.0f / 6.0f);
+  p = fmaf(p, r, 0.5f);
+  p = fmaf(p, r, 1.0f);
+  p = fmaf(p, r, 1.0f);
+  return ldexpf(p, (int)n);
+}
+
+// log for positive normal x: x = m 2^e with m in [sqrt(1/2), sqrt(2)),
+// log m = 2 atanh(s), s = (m-1)/(m+1), series to s^9.
+__device__ __forceinline__ float es_log(float x) {
+  int e;
+  float m = frexpf(x, &e);
+  if (m < 0.70710678118654752f) {
+    m = m + m;
+    e = e - 1;
+  }
+  const float f = m - 1.0f;
+  const float s = f / (2.0f + f);
+  const float z = s * s;
+  float p = 2.0f / 9.0f;
+  p = fmaf(p, z, 2.0f / 7.0f);
+  p = fmaf(p, z, 2.0f / 5.0f);
+  p = fmaf(p, z, 2.0f / 3.0f);
+  p = fmaf(p, z, 2.0f);
+  const float lm = s * p;
+  const float ef = (float)e;
+  return fmaf(ef, 0.693145751953125f, fmaf(ef, 1.42860682030941723212e-6f, lm));
+}
+
+// sin and cos of an fp32 angle: quadrant reduction in double precision, then
+// Taylor polynomials on |r| <= pi/4.
+__device__ __forceinline__ void es_sincos(float x, float* sn, float* cs) {
+  const double xd = (double)x;
+  const double kd = rint(xd * 0.63661977236758134308);
+  double rd = fma(-kd, 1.5707963267948966192, xd);
+  rd = fma(-kd, 6.123233995736766036e-17, rd);
+  const float r = (float)rd;
+  const float z = r * r;
+  float sp = 1.0f / 362880.0f;
+  sp = fmaf(sp, z, -1.0f / 5040.0f);
+  sp = fmaf(sp, z, 1.0f / 120.0f);
+  sp = fmaf(sp, z, -1.0f / 6.0f);
+  const float sr = fmaf(sp * z, r, r);
+  float cp = -1.0f / 3628800.0f;
+  cp = fmaf(cp, z, 1.0f / 40320.0f);
+  cp = fmaf(cp, z, -1.0f / 720.0f);
+  cp = fmaf(cp, z, 1.0f / 24.0f);
+  cp = fmaf(cp, z, -0.5f);
+  const float cr = fmaf(cp, z, 1.0f);
+  const int q = (int)((long long)kd & 3);
+  *sn = q == 0 ? sr : q == 1 ? cr : q == 2 ? -sr : -cr;
+  *cs = q == 0 ? cr : q == 1 ? -sr : q == 2 ? -cr : sr;
+}
+
+// MLX unary sigmoid in bf16: round after exp, add, reciprocal, subtraction
+// (linear.metal:389-395, gdn.metal:10-15).
 __device__ __forceinline__ float sigmoid_bf(float x) {
-  float e = rbf(expf(fabsf(x)));
-  float d = rbf(1.0f + e);
-  float p = rbf(1.0f / d);
+  const float e = rbf(es_exp(fabsf(x)));
+  const float d = rbf(1.0f + e);
+  const float p = rbf(1.0f / d);
   return rbf(x < 0.0f ? p : 1.0f - p);
 }
 
-// MLX log1p specialised to [0,1] (utils.h), then bf16 softplus.
+// MLX log1p specialised to [0,1] (utils.h, gdn.metal:19-23), bf16 softplus
+// (gdn.metal:25-29).
 __device__ __forceinline__ float mlx_log1p(float x) {
-  float xp1 = 1.0f + x;
+  const float xp1 = 1.0f + x;
   if (xp1 == 1.0f) return x;
-  return x * (logf(xp1) / (xp1 - 1.0f));
+  return x * (es_log(xp1) / (xp1 - 1.0f));
 }
 __device__ __forceinline__ float softplus_bf(float x) {
-  float e = rbf(expf(-fabsf(x)));
-  float l = rbf(mlx_log1p(e));
+  const float e = rbf(es_exp(-fabsf(x)));
+  const float l = rbf(mlx_log1p(e));
   return rbf(fmaxf(x, 0.0f) + l);
 }
 
-// ---- wave reductions (DPP inside a 16-lane row, then cross-row shuffles) ----
+// ---- cross-lane reductions: pairwise trees in lane order ----
+// DPP row ops: xor1/xor2 inside a quad, half-mirror (i <-> 7-i) and mirror
+// (i <-> 15-i) inside a 16-lane row. After xor1 and xor2 every lane of a quad
+// holds the quad sum, so the mirrors add whole quad/octet sums: the result is
+// ((l0+l1)+(l2+l3)) + ((l4+l5)+(l6+l7)) + ... in every lane.
 __device__ __forceinline__ float dpp_xor1(float v) {
   return __builtin_amdgcn_update_dpp(0.0f, v, 0xB1, 0xf, 0xf, false);
 }
@@ -69,18 +147,25 @@ __device__ __forceinline__ float dpp_half_mirror(float v) {
 __device__ __forceinline__ float dpp_mirror(float v) {
   return __builtin_amdgcn_update_dpp(0.0f, v, 0x140, 0xf, 0xf, false);
 }
-// Sum over the 4 lanes of a quad; every lane receives the result.
-__device__ __forceinline__ float quad_sum(float v) {
-  v += dpp_xor1(v);
-  v += dpp_xor2(v);
+__device__ __forceinline__ float tree4(float v) {
+  v = v + dpp_xor1(v);
+  v = v + dpp_xor2(v);
   return v;
 }
-// Sum over a 16-lane row; every lane of the row receives the result.
-__device__ __forceinline__ float row16_sum(float v) {
-  v += dpp_xor1(v);
-  v += dpp_xor2(v);
-  v += dpp_half_mirror(v);
-  v += dpp_mirror(v);
+__device__ __forceinline__ float tree16(float v) {
+  v = tree4(v);
+  v = v + dpp_half_mirror(v);
+  v = v + dpp_mirror(v);
+  return v;
+}
+__device__ __forceinline__ float tree32(float v) {
+  v = tree16(v);
+  v = v + __shfl_xor(v, 16, 64);
+  return v;
+}
+__device__ __forceinline__ float tree64(float v) {
+  v = tree32(v);
+  v = v + __shfl_xor(v, 32, 64);
   return v;
 }
 __device__ __forceinline__ float row16_max(float v) {
@@ -88,17 +173,6 @@ __device__ __forceinline__ float row16_max(float v) {
   v = fmaxf(v, dpp_xor2(v));
   v = fmaxf(v, dpp_half_mirror(v));
   v = fmaxf(v, dpp_mirror(v));
-  return v;
-}
-// Sum over a 32-lane half wave; every lane of the half receives the result.
-__device__ __forceinline__ float half_sum(float v) {
-  v = row16_sum(v);
-  v += __shfl_xor(v, 16, 64);
-  return v;
-}
-__device__ __forceinline__ float wave_sum(float v) {
-  v = half_sum(v);
-  v += __shfl_xor(v, 32, 64);
   return v;
 }
 __device__ __forceinline__ float wave_max(float v) {
@@ -110,15 +184,17 @@ __device__ __forceinline__ float wave_max(float v) {
 
 // ---- Q4 affine group-64 dot over one 32-element slice ----
 // codes: 4 u32 words = 32 nibbles for elements k..k+31 (nibble j of word w is
-// element 8w+j, linear.metal:21). xr holds x with odd elements pre-divided by
-// 16, so masking (not shifting) the odd nibbles gives exact 16*q products.
+// element 8w+j, linear.metal:21). Two fma chains: a0 over the even elements
+// in order, a1 over the odd ones; dot = a0 + a1. xr holds x with the odd
+// elements pre-divided by 16, so masking (not shifting) the odd nibbles gives
+// (x/16)*(16q), the same exact product as x*q.
 __device__ __forceinline__ float q4_dot32(const u32x4 c, const float* xr) {
   float a0 = 0.0f, a1 = 0.0f;
 #pragma unroll
   for (int w = 0; w < 4; ++w) {
-    uint32_t word = c[w];
-    uint32_t lo = word & 0x0F0F0F0Fu;
-    uint32_t hi = word & 0xF0F0F0F0u;
+    const uint32_t word = c[w];
+    const uint32_t lo = word & 0x0F0F0F0Fu;
+    const uint32_t hi = word & 0xF0F0F0F0u;
     a0 = fmaf(xr[8 * w + 0], (float)(lo & 0xffu), a0);
     a1 = fmaf(xr[8 * w + 1], (float)(hi & 0xffu), a1);
     a0 = fmaf(xr[8 * w + 2], (float)((lo >> 8) & 0xffu), a0);
@@ -131,12 +207,18 @@ __device__ __forceinline__ float q4_dot32(const u32x4 c, const float* xr) {
   return a0 + a1;
 }
 
+// Slice partial of a row: fma(xs, bias, scale * dot).
+__device__ __forceinline__ float q4_slice(const u32x4 c, uint32_t scale, uint32_t bias,
+                                          const float* xr, float xs) {
+  return fmaf(xs, bf2f(bias), bf2f(scale) * q4_dot32(c, xr));
+}
+
 // Load a 32-element bf16 slice (64 B) as floats.
 __device__ __forceinline__ void load_bf16x32(const uint16_t* p, float* out) {
   const u32x4* q = reinterpret_cast<const u32x4*>(p);
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    u32x4 v = q[i];
+    const u32x4 v = q[i];
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       out[8 * i + 2 * j] = bf_lo(v[j]);
@@ -145,15 +227,23 @@ __device__ __forceinline__ void load_bf16x32(const uint16_t* p, float* out) {
   }
 }
 
-// Turn a slice of x into the register form used by q4_dot32; returns sum(x).
+// Register form of a slice for q4_dot32; returns the sequential sum of x.
 __device__ __forceinline__ float prep_slice(const float* x, float* xr) {
   float xs = 0.0f;
 #pragma unroll
   for (int j = 0; j < 32; ++j) {
-    xs += x[j];
+    xs = xs + x[j];
     xr[j] = (j & 1) ? x[j] * 0.0625f : x[j];
   }
   return xs;
+}
+
+// Sequential fma chain of squares over a 32-element slice.
+__device__ __forceinline__ float sumsq32(const float* x) {
+  float ss = 0.0f;
+#pragma unroll
+  for (int j = 0; j < 32; ++j) ss = fmaf(x[j], x[j], ss);
+  return ss;
 }
 
 struct Q4 {
@@ -169,7 +259,7 @@ struct StepState {
   int pos;          // absolute position of the token consumed by this step
   int step;         // index of the output written by this step
   uint32_t token;   // token consumed by this step
-  uint32_t head_counter;  // arrival counter of the vocab-head blocks
+  uint32_t pad;
 };
 
 __device__ __forceinline__ int load_pos(const StepState* st, int pos_val) {

@@ -39,21 +39,23 @@ __device__ __forceinline__ void head_norm4(const uint16_t* x, const uint16_t* ga
   const float gf[4] = {bf_lo(gv.x), bf_hi(gv.x), bf_lo(gv.y), bf_hi(gv.y)};
   float ss = 0.0f;
 #pragma unroll
-  for (int i = 0; i < 4; ++i) ss += xf[i] * xf[i];
-  ss = wave_sum(ss);
+  for (int i = 0; i < 4; ++i) ss = fmaf(xf[i], xf[i], ss);
+  ss = tree64(ss);
   const float inv = 1.0f / sqrtf(ss / 256.0f + 1e-6f);
 #pragma unroll
   for (int i = 0; i < 4; ++i) out[i] = rbf(rbf(xf[i] * inv) * gf[i]);
 }
 
-// Rotary component d of a normalised head (attention.metal:55-70).
+// Rotary component d of a normalised head (attention.metal:55-70):
+// d < 32: fma(lo, c, -(hi*s)); 32 <= d < 64: fma(lo, s, hi*c).
 __device__ __forceinline__ float rope_at(const float* nrm, int d, int pos, const float* inv_freq) {
   if (d >= 64) return nrm[d];
   const int pair = d & 31;
   const float angle = (float)pos * inv_freq[pair];
-  const float c = cosf(angle), s = sinf(angle);
+  float s, c;
+  es_sincos(angle, &s, &c);
   const float lo = nrm[pair], hi = nrm[pair + 32];
-  return rbf(d < 32 ? lo * c - hi * s : lo * s + hi * c);
+  return rbf(d < 32 ? fmaf(lo, c, -(hi * s)) : fmaf(lo, s, hi * c));
 }
 
 // Two consecutive positions of one 16-lane row: 32 B of K and of V each.
@@ -126,17 +128,16 @@ __global__ __launch_bounds__(256) void k_attn_split(AttnArgs a) {
     for (int i = 0; i < 4; ++i) r[i] = rope_at(nrm[wave], lane * 4 + i, pos, a.inv_freq);
     if (a.query_out && split == 0) {
       uint16_t* qo = a.query_out + (4 * g + wave) * 256 + lane * 4;
-      *reinterpret_cast<uint2*>(qo) = make_uint2(f2bf(r[0]) | (f2bf(r[1]) << 16),
-                                                 f2bf(r[2]) | (f2bf(r[3]) << 16));
+      *reinterpret_cast<uint2*>(qo) = make_uint2(pack_bf2(r[0], r[1]), pack_bf2(r[2], r[3]));
     }
-    qpk[wave][lane * 2] = f2bf(r[0] * 0.0625f) | (f2bf(r[1] * 0.0625f) << 16);
-    qpk[wave][lane * 2 + 1] = f2bf(r[2] * 0.0625f) | (f2bf(r[3] * 0.0625f) << 16);
+    qpk[wave][lane * 2] = pack_bf2(r[0] * 0.0625f, r[1] * 0.0625f);
+    qpk[wave][lane * 2 + 1] = pack_bf2(r[2] * 0.0625f, r[3] * 0.0625f);
     if (last && wave == 1) {
       float kr[4];
 #pragma unroll
       for (int i = 0; i < 4; ++i) kr[i] = rope_at(nrm[4], lane * 4 + i, pos, a.inv_freq);
-      const uint32_t k0 = f2bf(kr[0]) | (f2bf(kr[1]) << 16);
-      const uint32_t k1 = f2bf(kr[2]) | (f2bf(kr[3]) << 16);
+      const uint32_t k0 = pack_bf2(kr[0], kr[1]);
+      const uint32_t k1 = pack_bf2(kr[2], kr[3]);
       kvnew[0][lane * 2] = k0;
       kvnew[0][lane * 2 + 1] = k1;
       const size_t ci = ((size_t)g * a.capacity + pos) * 256 + lane * 4;
@@ -182,8 +183,8 @@ __global__ __launch_bounds__(256) void k_attn_split(AttnArgs a) {
         x0 = dot2(ka1[i], q[hh][4 + i], x0);
         x1 = dot2(kb1[i], q[hh][4 + i], x1);
       }
-      s0[hh] = row16_sum(x0);
-      s1[hh] = ok1 ? row16_sum(x1) : -INFINITY;
+      s0[hh] = tree16(x0);
+      s1[hh] = ok1 ? tree16(x1) : -INFINITY;
     }
     float vf0[16], vf1[16];
 #pragma unroll
@@ -214,7 +215,7 @@ __global__ __launch_bounds__(256) void k_attn_split(AttnArgs a) {
       float x0 = 0.0f;
 #pragma unroll
       for (int i = 0; i < 8; ++i) x0 = dot2(kvnew[0][j * 8 + i], q[hh][i], x0);
-      s0[hh] = row16_sum(x0);
+      s0[hh] = tree16(x0);
     }
     float vf0[16];
 #pragma unroll
@@ -313,7 +314,7 @@ __global__ __launch_bounds__(256) void k_attn_merge(AttnArgs a) {
     scale[s] = f;
     lloc += f * ml[2 * s + 1];
   }
-  lloc = wave_sum(lloc);
+  lloc = tree64(lloc);
   if (lane == 0) wred[wave] = lloc;
   __syncthreads();
   const float L = (wred[0] + wred[1]) + (wred[2] + wred[3]);

@@ -17,6 +17,9 @@
 // conv and SiLU, rsqrt(ss/128 + 1e-6/128), q x 1/128, k x bf16(128^-1/2),
 // g = exp(-exp(A_log) * softplus_bf(bf16(a+dt))), beta = sigmoid_bf(b)) and
 // gdn.metal:192-226 (decay, memory, delta, update, readout; fp32 state).
+// Order: Q/K sum of squares = tree64 over channels 0..63 plus tree64 over
+// 64..127; memory and readout = per-lane fma chains over 8 keys, tree16 over
+// the 16 lanes of a row.
 #include "es_kernels.hpp"
 
 namespace es {
@@ -76,7 +79,7 @@ __global__ __launch_bounds__(256) void k_gdn_recur(GdnRecurArgs a) {
   if (t < 16) ring_load(a.ring, a.conv_w, cv, rv);
   const int pos = load_pos(a.st, a.pos_val);
   const float v = conv_silu(rt, pos);
-  float ss = wave_sum(v * v);
+  const float ss = tree64(v * v);
   if (lane == 0) red[wave] = ss;
   if (t < 16) {
     const float vval = conv_silu(rv, pos);
@@ -85,7 +88,7 @@ __global__ __launch_bounds__(256) void k_gdn_recur(GdnRecurArgs a) {
   }
   if (t == 64) {
     const float ax = rbf(bf2f(a.ab[h]) + bf2f(a.dt_bias[h]));
-    const float g = expf(-expf(a.a_log[h]) * softplus_bf(ax));
+    const float g = es_exp(-es_exp(a.a_log[h]) * softplus_bf(ax));
     const float beta = sigmoid_bf(bf2f(a.ab[16 + h]));
     gates[0] = g;
     gates[1] = beta;
@@ -119,7 +122,7 @@ __global__ __launch_bounds__(256) void k_gdn_recur(GdnRecurArgs a) {
     S[i] = S[i] * g;
     mem = fmaf(S[i], kk[i], mem);
   }
-  mem = row16_sum(mem);
+  mem = tree16(mem);
   const float delta = (vv[t >> 4] - mem) * beta;
   float out = 0.0f;
 #pragma unroll
@@ -127,7 +130,7 @@ __global__ __launch_bounds__(256) void k_gdn_recur(GdnRecurArgs a) {
     S[i] = fmaf(kk[i], delta, S[i]);
     out = fmaf(S[i], qq[i], out);
   }
-  out = row16_sum(out);
+  out = tree16(out);
   if (j == 0) a.y[h * 128 + row] = (uint16_t)f2bf(out);
   reinterpret_cast<float4*>(sp)[0] = make_float4(S[0], S[1], S[2], S[3]);
   reinterpret_cast<float4*>(sp)[1] = make_float4(S[4], S[5], S[6], S[7]);

@@ -3,9 +3,13 @@
 // k_head: each block of 256 threads computes 256 consecutive logits (a wave
 // owns 64 rows, two per pass, loads double-buffered four passes at a time),
 // rounds them to bf16 (head_lse.metal:53) and writes its own (max, sum exp)
-// over those bf16 logits.
+// over those bf16 logits: max exact, sum = (t0 + t1) + (t2 + t3) of the four
+// waves' tree64 sums of exp(logit - max).
 // k_head_tail (one block) merges the partials into
 //   lse = bf16(log(sum) + max)                         (head_lse.metal:81)
+// where thread t sums blocks t, t+256, ... sequentially (each term
+// sum_b * exp(max_b - max)), then the four waves' tree64 sums are added as
+// (t0 + t1) + (t2 + t3),
 // and selects the lowest index whose bf16(logit - lse) equals the maximum
 // (head_lse.metal:83-97, docs/protocol.md:44). Rounding is monotone, so the
 // maximum is bf16(maxlogit - lse), and the lowest block whose own maximum
@@ -60,10 +64,7 @@ __global__ __launch_bounds__(256) void k_head(HeadArgs a) {
   float xv[32], xn[32], xr[32];
   load_bf16x32(a.h + sl * 32, xv);
   {
-    float ss = 0.0f;
-#pragma unroll
-    for (int i = 0; i < 32; ++i) ss += xv[i] * xv[i];
-    ss = half_sum(ss);
+    const float ss = tree32(sumsq32(xv));
     const float inv = 1.0f / sqrtf(ss / 1024.0f + 1e-6f);
     float gv[32];
     load_bf16x32(a.gain + sl * 32, gv);
@@ -83,8 +84,7 @@ __global__ __launch_bounds__(256) void k_head(HeadArgs a) {
     for (int p = 0; p < kPassBatch; ++p) {
       const int local = wave * 64 + it * 2 * kPassBatch + 2 * p + half;
       const int r = blockIdx.x * kRowsPerBlock + local;
-      float part = bf2f(cur.s[p]) * q4_dot32(cur.c[p], xr) + xs * bf2f(cur.b[p]);
-      part = half_sum(part);
+      const float part = tree32(q4_slice(cur.c[p], cur.s[p], cur.b[p], xr, xs));
       if (sl == 0) {
         const uint32_t b = f2bf(part);
         lg[local] = r < vocab ? bf2f(b) : -INFINITY;
@@ -101,7 +101,7 @@ __global__ __launch_bounds__(256) void k_head(HeadArgs a) {
   if (lane == 0) wred[wave] = bm;
   __syncthreads();
   bm = fmaxf(fmaxf(wred[0], wred[1]), fmaxf(wred[2], wred[3]));
-  const float se = wave_sum(v == -INFINITY ? 0.0f : expf(v - bm));
+  const float se = tree64(v == -INFINITY ? 0.0f : es_exp(v - bm));
   if (lane == 0) wred2[wave] = se;
   __syncthreads();
   if (t == 0) {
@@ -123,12 +123,12 @@ __global__ __launch_bounds__(256) void k_head_tail(HeadArgs a, int nb) {
   __syncthreads();
   gm = fmaxf(fmaxf(wred[0], wred[1]), fmaxf(wred[2], wred[3]));
   float gs = 0.0f;
-  for (int b = t; b < nb; b += 256) gs += a.part[2 * b + 1] * expf(a.part[2 * b] - gm);
-  gs = wave_sum(gs);
+  for (int b = t; b < nb; b += 256) gs = gs + a.part[2 * b + 1] * es_exp(a.part[2 * b] - gm);
+  gs = tree64(gs);
   if (lane == 0) wred2[wave] = gs;
   __syncthreads();
   gs = (wred2[0] + wred2[1]) + (wred2[2] + wred2[3]);
-  const float lse = rbf(logf(gs) + gm);
+  const float lse = rbf(es_log(gs) + gm);
   const float target = rbf(gm - lse);
   unsigned int first = 0xffffffffu;
   for (int b = t; b < nb; b += 256)

@@ -8,6 +8,13 @@
 // the 16-byte code load plus one scale and one bias. Accumulation is fp32 and
 // the result is rounded to bf16 once (linear.metal:41-72); the residual
 // epilogue rounds the projection before the add (linear.metal:121).
+//
+// Evaluation order (fixed, see es_device.hpp): slice partial
+// fma(xs, bias, scale * (even-fma-chain + odd-fma-chain)); K=1024 rows sum
+// their 32 slices with tree32, K=2048 rows their 64 slices with tree64, and a
+// K=3584 lane l first adds slice l+64 (l < 48) to slice l, then tree64.
+// Weight loads are issued at kernel entry, before the input and its RMSNorm,
+// so their latency overlaps that work.
 #include "es_kernels.hpp"
 
 namespace es {
@@ -19,7 +26,7 @@ __device__ __forceinline__ void store_bf16x32(uint16_t* p, const float* v) {
   for (int i = 0; i < 4; ++i) {
     u32x4 o;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) o[j] = f2bf(v[8 * i + 2 * j]) | (f2bf(v[8 * i + 2 * j + 1]) << 16);
+    for (int j = 0; j < 4; ++j) o[j] = pack_bf2(v[8 * i + 2 * j], v[8 * i + 2 * j + 1]);
     q[i] = o;
   }
 }
@@ -29,10 +36,7 @@ __device__ __forceinline__ void store_bf16x32(uint16_t* p, const float* v) {
 // linear.metal:311-329: fp32 sum of squares, bf16(bf16(x*inv)*gain)).
 __device__ __forceinline__ void norm_slice_1024(const float* xv, const uint16_t* gain, int sl,
                                                 float* xn) {
-  float ss = 0.0f;
-#pragma unroll
-  for (int j = 0; j < 32; ++j) ss += xv[j] * xv[j];
-  ss = half_sum(ss);
+  const float ss = tree32(sumsq32(xv));
   const float inv = 1.0f / sqrtf(ss / 1024.0f + 1e-6f);
   float gv[32];
   load_bf16x32(gain + sl * 32, gv);
@@ -49,7 +53,7 @@ __device__ __forceinline__ void embed_slice(const Q4& e, uint32_t tok, int sl, f
 #pragma unroll
   for (int w = 0; w < 4; ++w)
 #pragma unroll
-    for (int j = 0; j < 8; ++j) xv[8 * w + j] = rbf(sc * (float)((c[w] >> (4 * j)) & 15u) + bi);
+    for (int j = 0; j < 8; ++j) xv[8 * w + j] = rbf(fmaf(sc, (float)((c[w] >> (4 * j)) & 15u), bi));
 }
 
 struct MultiDev {
@@ -122,8 +126,7 @@ __global__ __launch_bounds__(256) void k_norm_multi(MultiDev a) {
   if (a.ring0) y0 += (size_t)(load_pos(a.st, a.pos_val) & 3) * a.m[0].n;
 #pragma unroll
   for (int p = 0; p < P; ++p) {
-    float part = bf2f(sv[p]) * q4_dot32(c[p], xr) + xs * bf2f(bv[p]);
-    part = half_sum(part);
+    const float part = tree32(q4_slice(c[p], sv[p], bv[p], xr, xs));
     if (sl == 0 && mi[p] >= 0) {
       uint16_t* y = mi[p] == 0 ? y0 : mi[p] == 1 ? a.y[1] : mi[p] == 2 ? a.y[2] : a.y[3];
       y[lr[p]] = (uint16_t)f2bf(part);
@@ -164,10 +167,8 @@ __global__ __launch_bounds__(256) void k_norm_gate_up(Q4 gate, Q4 up, const uint
   const float xs = prep_slice(xn, xr);
 #pragma unroll
   for (int p = 0; p < NP; ++p) {
-    float g = bf2f(sg[p]) * q4_dot32(cg[p], xr) + xs * bf2f(bg[p]);
-    float u = bf2f(su[p]) * q4_dot32(cu[p], xr) + xs * bf2f(bu[p]);
-    g = half_sum(g);
-    u = half_sum(u);
+    const float g = tree32(q4_slice(cg[p], sg[p], bg[p], xr, xs));
+    const float u = tree32(q4_slice(cu[p], su[p], bu[p], xr, xs));
     if (sl == 0 && rr[p] < gate.n) {
       const float gb = rbf(g), ub = rbf(u);
       const float silu = rbf(gb * sigmoid_bf(gb));
@@ -199,8 +200,7 @@ __global__ __launch_bounds__(256) void k_qmv_narrow(Q4 m, const uint16_t* x,
 #pragma unroll
   for (int p = 0; p < P; ++p) {
     const int r = base + 2 * p + half;
-    float part = bf2f(sv[p]) * q4_dot32(c[p], xr) + xs * bf2f(bv[p]);
-    part = half_sum(part);
+    const float part = tree32(q4_slice(c[p], sv[p], bv[p], xr, xs));
     if (sl == 0 && r < m.n) {
       if (y_f32) y_f32[r] = part;
       if (ADD) y[r] = (uint16_t)f2bf(bf2f(residual[r]) + rbf(part));
@@ -259,9 +259,9 @@ __global__ __launch_bounds__(256) void k_qmv_wide(Q4 m, const uint16_t* x,
   for (int p = 0; p < P; ++p) {
     const int r = base + p;
     float part = 0.0f;
-    if (v1) part = bf2f(sa[p]) * q4_dot32(c1[p], xr1) + xs1 * bf2f(ba[p]);
-    if (v2) part += bf2f(sb[p]) * q4_dot32(c2[p], xr2) + xs2 * bf2f(bb[p]);
-    part = wave_sum(part);
+    if (v1) part = q4_slice(c1[p], sa[p], ba[p], xr1, xs1);
+    if (v2) part = part + q4_slice(c2[p], sb[p], bb[p], xr2, xs2);
+    part = tree64(part);
     if (lane == 0 && r < m.n) {
       if (y_f32) y_f32[r] = part;
       if (ADD) y[r] = (uint16_t)f2bf(bf2f(residual[r]) + rbf(part));
@@ -305,21 +305,21 @@ __global__ __launch_bounds__(256) void k_gdn_gate_out(Q4 m, const uint16_t* y, c
     }
     float ss = 0.0f;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) ss += yf[i] * yf[i];
-    ss = row16_sum(ss);
+    for (int i = 0; i < 8; ++i) ss = fmaf(yf[i], yf[i], ss);
+    ss = tree16(ss);
     const float inv = 1.0f / sqrtf(ss / 128.0f + 1e-6f);
     uint32_t packed[4];
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
       const float norm = rbf(rbf(yf[i] * inv) * wf[i]);
       const float gz = zf[i];
-      const float sy = 1.0f / (1.0f + expf(fabsf(gz)));
+      const float sy = 1.0f / (1.0f + es_exp(fabsf(gz)));
       const float sig = gz < 0.0f ? sy : 1.0f - sy;
       const float g = rbf((gz * sig) * norm);
       const int e = e0 + i;
       xg[e + (e >> 5)] = g;
       if (i & 1) packed[i >> 1] |= f2bf(g) << 16;
-      else packed[i >> 1] = f2bf(g);
+      else packed[i >> 1] = f2bf(g);  // f2bf zero-extends
     }
     if (gated_out && blockIdx.x == 0)
       *reinterpret_cast<u32x4*>(gated_out + e0) = u32x4{packed[0], packed[1], packed[2], packed[3]};
@@ -332,8 +332,7 @@ __global__ __launch_bounds__(256) void k_gdn_gate_out(Q4 m, const uint16_t* y, c
 #pragma unroll
   for (int p = 0; p < P; ++p) {
     const int r = base + p;
-    float part = bf2f(sv[p]) * q4_dot32(c[p], xr) + xs * bf2f(bv[p]);
-    part = wave_sum(part);
+    const float part = tree64(q4_slice(c[p], sv[p], bv[p], xr, xs));
     if (lane == 0 && r < m.n) h[r] = (uint16_t)f2bf(bf2f(h[r]) + rbf(part));
   }
 }
@@ -344,7 +343,7 @@ __global__ __launch_bounds__(256) void k_embedding(Q4 e, const uint32_t* token, 
   for (int k = threadIdx.x; k < e.k; k += blockDim.x) {
     const uint32_t q = (e.w[(size_t)tok * (e.k / 8) + k / 8] >> (4 * (k % 8))) & 15u;
     const size_t g = (size_t)tok * (e.k / 64) + k / 64;
-    out[k] = (uint16_t)f2bf(bf2f(e.s[g]) * (float)q + bf2f(e.b[g]));
+    out[k] = (uint16_t)f2bf(fmaf(bf2f(e.s[g]), (float)q, bf2f(e.b[g])));
   }
 }
 

@@ -48,10 +48,78 @@ void eo_bf16_to_f32_array(const uint16_t* in, float* out, size_t n) {
 #define BF(x) eo_round_bf16(x)
 #define F(b) eo_bf16_to_f32(b)
 
+/* ---- series math, step for step the same evaluation as the kernels ----
+ * exp: x = n ln2 + r, |r| <= ln2/2 (ln2 split in a 12-bit-exact head and a
+ * tail), degree-7 Taylor polynomial of e^r by Horner with fma, times 2^n.
+ * Inputs <= -86 give 0 so every result is a normal number. */
+float eo_exp(float x) {
+  if (!(x > -86.0f)) return 0.0f;
+  if (x > 88.72f) return INFINITY;
+  const float n = rintf(x * 1.44269504088896341f);
+  float r = fmaf(n, -0.693145751953125f, x);
+  r = fmaf(n, -1.42860682030941723212e-6f, r);
+  float p = 1.0f / 5040.0f;
+  p = fmaf(p, r, 1.0f / 720.0f);
+  p = fmaf(p, r, 1.0f / 120.0f);
+  p = fmaf(p, r, 1.0f / 24.0f);
+  p = fmaf(p, r, 1.0f / 6.0f);
+  p = fmaf(p, r, 0.5f);
+  p = fmaf(p, r, 1.0f);
+  p = fmaf(p, r, 1.0f);
+  return ldexpf(p, (int)n);
+}
+
+/* log of a positive normal x: x = m 2^e, m in [sqrt(1/2), sqrt(2)),
+ * log m = 2 atanh(s) with s = (m-1)/(m+1), odd series to s^9. */
+float eo_log(float x) {
+  int e;
+  float m = frexpf(x, &e);
+  if (m < 0.70710678118654752f) {
+    m = m + m;
+    e = e - 1;
+  }
+  const float f = m - 1.0f;
+  const float s = f / (2.0f + f);
+  const float z = s * s;
+  float p = 2.0f / 9.0f;
+  p = fmaf(p, z, 2.0f / 7.0f);
+  p = fmaf(p, z, 2.0f / 5.0f);
+  p = fmaf(p, z, 2.0f / 3.0f);
+  p = fmaf(p, z, 2.0f);
+  const float lm = s * p;
+  const float ef = (float)e;
+  return fmaf(ef, 0.693145751953125f, fmaf(ef, 1.42860682030941723212e-6f, lm));
+}
+
+/* sin/cos of an fp32 angle: quadrant reduction in double precision, Taylor
+ * polynomials (sin to r^9, cos to r^10) on |r| <= pi/4 in fp32. */
+void eo_sincos(float x, float* sn, float* cs) {
+  const double xd = (double)x;
+  const double kd = rint(xd * 0.63661977236758134308);
+  double rd = fma(-kd, 1.5707963267948966192, xd);
+  rd = fma(-kd, 6.123233995736766036e-17, rd);
+  const float r = (float)rd;
+  const float z = r * r;
+  float sp = 1.0f / 362880.0f;
+  sp = fmaf(sp, z, -1.0f / 5040.0f);
+  sp = fmaf(sp, z, 1.0f / 120.0f);
+  sp = fmaf(sp, z, -1.0f / 6.0f);
+  const float sr = fmaf(sp * z, r, r);
+  float cp = -1.0f / 3628800.0f;
+  cp = fmaf(cp, z, 1.0f / 40320.0f);
+  cp = fmaf(cp, z, -1.0f / 720.0f);
+  cp = fmaf(cp, z, 1.0f / 24.0f);
+  cp = fmaf(cp, z, -0.5f);
+  const float cr = fmaf(cp, z, 1.0f);
+  const int q = (int)((long long)kd & 3);
+  *sn = q == 0 ? sr : q == 1 ? cr : q == 2 ? -sr : -cr;
+  *cs = q == 0 ? cr : q == 1 ? -sr : q == 2 ? -cr : sr;
+}
+
 /* MLX unary sigmoid with bf16 boundaries after exp, add, reciprocal and the
  * positive-branch subtraction: linear.metal:389-395, gdn.metal:10-15. */
 float eo_sigmoid_bf(float x) {
-  float e = BF(expf(fabsf(x)));
+  float e = BF(eo_exp(fabsf(x)));
   float d = BF(1.0f + e);
   float p = BF(1.0f / d);
   return BF(x < 0.0f ? p : 1.0f - p);
@@ -61,12 +129,12 @@ float eo_sigmoid_bf(float x) {
 static float mlx_log1p(float x) {
   float xp1 = 1.0f + x;
   if (xp1 == 1.0f) return x;
-  return x * (logf(xp1) / (xp1 - 1.0f));
+  return x * (eo_log(xp1) / (xp1 - 1.0f));
 }
 
 /* gdn.metal:25-29 */
 float eo_softplus_bf(float x) {
-  float e = BF(expf(-fabsf(x)));
+  float e = BF(eo_exp(-fabsf(x)));
   float l = BF(mlx_log1p(e));
   return BF(fmaxf(x, 0.0f) + l);
 }
@@ -78,10 +146,12 @@ float eo_rope_inv_freq(int pair) {
   return (float)exp2((double)t);
 }
 
-/* xor-butterfly restatement of a 2^k-lane simd_sum; destroys v */
-static float bfly_sum(float* v, int n) {
-  for (int off = n / 2; off >= 1; off /= 2)
-    for (int i = 0; i < off; ++i) v[i] = v[i] + v[i + off];
+/* Pairwise tree in lane order: ((v0+v1)+(v2+v3)) + ... for n a power of two.
+ * The reference sums across SIMD lanes with simd_sum, whose order Metal does
+ * not specify; this tree is the order the kernels use. Destroys v. */
+static float tree(float* v, int n) {
+  for (int off = 1; off < n; off *= 2)
+    for (int i = 0; i + off < n; i += 2 * off) v[i] = v[i] + v[i + off];
   return v[0];
 }
 
@@ -109,43 +179,47 @@ void eo_embedding(const uint32_t* codes, const uint16_t* scales, const uint16_t*
   for (int k = 0; k < K; ++k) {
     uint32_t q = (codes[(size_t)token * (K / 8) + k / 8] >> (4 * (k % 8))) & 15u;
     size_t g = (size_t)token * (K / 64) + k / 64;
-    out[k] = eo_f32_to_bf16(F(scales[g]) * (float)q + F(biases[g]));
+    out[k] = eo_f32_to_bf16(fmaf(F(scales[g]), (float)q, F(biases[g])));
   }
 }
 
-/* One output row of qmv_q4, linear.metal:38-72: 32 lanes, each a 16-wide K
- * slice per 512-block; lane partial s*dot + xs*b accumulated over blocks. */
+/* One output row of the Q4 matvec (linear.metal:38-72 arithmetic: affine
+ * dequant s*q + b folded as s*sum(q x) + b*sum(x) per group, fp32, one bf16
+ * round). Fixed order: the row is cut into 32-element slices (half a group);
+ * per slice xs = sequential sum of x, dot = (fma chain over the even
+ * elements) + (fma chain over the odd elements), partial = fma(xs, b, s*dot).
+ * K = 1024: tree over the 32 slice partials; K = 2048: tree over 64;
+ * other K (<= 4096): lane l holds slice l, adds slice l+64 when present, tree
+ * over 64 lanes. */
+static float slice_partial(const uint32_t* w, const uint16_t* s, const uint16_t* b, int K,
+                           const float* xf, size_t row, int slice) {
+  const uint32_t* c = w + row * (size_t)(K / 8) + (size_t)slice * 4;
+  const float* x = xf + slice * 32;
+  float xs = 0.0f, a0 = 0.0f, a1 = 0.0f;
+  for (int j = 0; j < 32; ++j) xs = xs + x[j];
+  for (int j = 0; j < 32; ++j) {
+    const float q = (float)((c[j / 8] >> (4 * (j % 8))) & 15u);
+    if (j & 1) a1 = fmaf(x[j], q, a1);
+    else a0 = fmaf(x[j], q, a0);
+  }
+  const size_t gi = row * (size_t)(K / 64) + slice / 2;
+  return fmaf(xs, F(b[gi]), F(s[gi]) * (a0 + a1));
+}
+
 static float qmv_row(const uint32_t* w, const uint16_t* s, const uint16_t* b, int K,
                      const float* xf, size_t row) {
-  float lane_acc[32];
-  for (int l = 0; l < 32; ++l) lane_acc[l] = 0.0f;
-  const uint16_t* wrow = (const uint16_t*)(w + row * (size_t)(K / 8));
-  for (int k0 = 0; k0 < K; k0 += 512) {
-    for (int lane = 0; lane < 32; ++lane) {
-      int k = k0 + lane * 16;
-      float xx[16];
-      float xs = 0.0f;
-      for (int j = 0; j < 16; j += 4) {
-        float a = xf[k + j], bb = xf[k + j + 1], c = xf[k + j + 2], d = xf[k + j + 3];
-        xs += ((a + bb) + c) + d;
-        xx[j] = a;
-        xx[j + 1] = bb / 16.0f;
-        xx[j + 2] = c / 256.0f;
-        xx[j + 3] = d / 4096.0f;
-      }
-      const uint16_t* ww = wrow + k / 4;
-      float dotq = 0.0f;
-      for (int j = 0; j < 4; ++j) {
-        uint16_t v = ww[j];
-        dotq += ((xx[4 * j] * (float)(v & 0x000f) + xx[4 * j + 1] * (float)(v & 0x00f0)) +
-                 xx[4 * j + 2] * (float)(v & 0x0f00)) +
-                xx[4 * j + 3] * (float)(v & 0xf000);
-      }
-      size_t gi = row * (size_t)(K / 64) + k / 64;
-      lane_acc[lane] += F(s[gi]) * dotq + xs * F(b[gi]);
-    }
+  float lane[64];
+  const int ns = K / 32;
+  if (K == 1024) {
+    for (int l = 0; l < 32; ++l) lane[l] = slice_partial(w, s, b, K, xf, row, l);
+    return tree(lane, 32);
   }
-  return bfly_sum(lane_acc, 32);
+  for (int l = 0; l < 64; ++l) {
+    float p = l < ns ? slice_partial(w, s, b, K, xf, row, l) : 0.0f;
+    if (l + 64 < ns) p = p + slice_partial(w, s, b, K, xf, row, l + 64);
+    lane[l] = p;
+  }
+  return tree(lane, 64);
 }
 
 void eo_q4_matvec(const uint32_t* codes, const uint16_t* scales, const uint16_t* biases,
@@ -174,28 +248,22 @@ void eo_q4_matvec_add(const uint32_t* codes, const uint16_t* scales, const uint1
   free(xf);
 }
 
-/* rms_norm_bf16, linear.metal:311-330: four contiguous values per thread,
- * simd_sum per 32 threads, then a simd_sum over the group partials. */
+/* rms_norm_bf16 arithmetic (linear.metal:311-330): fp32 sum of squares,
+ * inv = 1/sqrt(mean + eps), out = bf16(bf16(x*inv)*gain). Fixed order for the
+ * 1024-wide rows: 32 slices of 32 (fma chain of squares each), tree over the
+ * 32 slice sums. */
 void eo_rms_norm(const uint16_t* x, const uint16_t* gain, int cols, float eps, uint16_t* out) {
-  int threads = ((cols + 127) / 128) * 32;
-  int sgs = threads / 32;
-  float sums[32];
-  for (int i = 0; i < 32; ++i) sums[i] = 0.0f;
-  for (int sg = 0; sg < sgs; ++sg) {
-    float lane[32];
-    for (int l = 0; l < 32; ++l) {
-      int t = sg * 32 + l;
-      float acc = 0.0f;
-      for (int j = 0; j < 4; ++j) {
-        int c = t * 4 + j;
-        float v = c < cols ? F(x[c]) : 0.0f;
-        acc += v * v;
-      }
-      lane[l] = acc;
+  float lane[32];
+  for (int l = 0; l < 32; ++l) {
+    float ss = 0.0f;
+    for (int j = 0; j < 32; ++j) {
+      int c = l * 32 + j;
+      float v = c < cols ? F(x[c]) : 0.0f;
+      ss = fmaf(v, v, ss);
     }
-    sums[sg] = bfly_sum(lane, 32);
+    lane[l] = ss;
   }
-  float total = bfly_sum(sums, 32);
+  float total = tree(lane, 32);
   float inv = 1.0f / sqrtf(total / (float)cols + eps);
   for (int c = 0; c < cols; ++c) out[c] = eo_f32_to_bf16(BF(F(x[c]) * inv) * F(gain[c]));
 }
@@ -220,51 +288,46 @@ void eo_gdn_conv_prepare(const uint16_t* raw, uint16_t* history, const uint16_t*
   const float k_scale = BF(0.08838834764831845f);
   for (int block = 0; block < 3; ++block) {
     for (int h = 0; h < 16; ++h) {
-      float v[32][4];
-      float lane_ss[32];
-      for (int lane = 0; lane < 32; ++lane) {
-        int off = block * 2048 + h * 128 + lane * 4;
-        float ss = 0.0f;
-        for (int i = 0; i < 4; ++i) {
-          int c = off + i;
-          uint16_t old0 = history[c], old1 = history[6144 + c], old2 = history[12288 + c];
-          float acc = 0.0f;
-          for (int tap = 0; tap < 4; ++tap) {
-            float xv = tap == 0 ? F(old0) : tap == 1 ? F(old1) : tap == 2 ? F(old2) : F(raw[c]);
-            acc = fmaf(xv, F(conv_w[c * 4 + tap]), acc);
-          }
-          float xr = BF(acc);
-          v[lane][i] = BF(xr * eo_sigmoid_bf(xr));
-          ss += v[lane][i] * v[lane][i];
-          history[c] = old1;
-          history[6144 + c] = old2;
-          history[12288 + c] = raw[c];
-        }
-        lane_ss[lane] = ss;
+      float v[128];
+      for (int d = 0; d < 128; ++d) {
+        int c = block * 2048 + h * 128 + d;
+        uint16_t old0 = history[c], old1 = history[6144 + c], old2 = history[12288 + c];
+        float acc = 0.0f;
+        acc = fmaf(F(old0), F(conv_w[c * 4 + 0]), acc);
+        acc = fmaf(F(old1), F(conv_w[c * 4 + 1]), acc);
+        acc = fmaf(F(old2), F(conv_w[c * 4 + 2]), acc);
+        acc = fmaf(F(raw[c]), F(conv_w[c * 4 + 3]), acc);
+        float xr = BF(acc);
+        v[d] = BF(xr * eo_sigmoid_bf(xr));
+        history[c] = old1;
+        history[6144 + c] = old2;
+        history[12288 + c] = raw[c];
       }
       if (block < 2) {
-        float ss = bfly_sum(lane_ss, 32);
+        /* sum of squares: tree over channels 0..63 plus tree over 64..127 */
+        float sq[128];
+        for (int d = 0; d < 128; ++d) sq[d] = v[d] * v[d];
+        float ss = tree(sq, 64) + tree(sq + 64, 64);
         float inv = 1.0f / sqrtf(ss / 128.0f + 1.0e-6f / 128.0f);
         float scale = block == 0 ? q_scale : k_scale;
-        for (int lane = 0; lane < 32; ++lane)
-          for (int i = 0; i < 4; ++i)
-            conv_out[block * 2048 + h * 128 + lane * 4 + i] =
-                eo_f32_to_bf16(BF(v[lane][i] * inv) * scale);
+        for (int d = 0; d < 128; ++d)
+          conv_out[block * 2048 + h * 128 + d] = eo_f32_to_bf16(BF(v[d] * inv) * scale);
       } else {
-        for (int lane = 0; lane < 32; ++lane)
-          for (int i = 0; i < 4; ++i)
-            conv_out[block * 2048 + h * 128 + lane * 4 + i] = eo_f32_to_bf16(v[lane][i]);
+        for (int d = 0; d < 128; ++d) conv_out[block * 2048 + h * 128 + d] = eo_f32_to_bf16(v[d]);
       }
     }
   }
   for (int h = 0; h < 16; ++h) {
     float ax = BF(F(a[h]) + F(dt_bias[h]));
-    g[h] = expf(-expf(a_log[h]) * eo_softplus_bf(ax));
+    g[h] = eo_exp(-eo_exp(a_log[h]) * eo_softplus_bf(ax));
     beta[h] = eo_f32_to_bf16(eo_sigmoid_bf(F(b[h])));
   }
 }
 
-/* gdn_recur, gdn.metal:185-227 with T=1. Four lanes own a value row, 32 keys each. */
+/* gdn_recur, gdn.metal:185-227 with T=1: decay, memory = S.k, delta =
+ * (v - memory)*beta, S += k*delta, readout = S.q; fp32 state. Fixed order: a
+ * value row is 16 lanes of 8 keys; memory and readout are fma chains over the
+ * lane's 8 keys and a tree over the 16 lanes. */
 void eo_gdn_recur(const uint16_t* conv, const float* g, const uint16_t* beta,
                   float* state, uint16_t* y) {
 #pragma omp parallel for schedule(static)
@@ -272,63 +335,56 @@ void eo_gdn_recur(const uint16_t* conv, const float* g, const uint16_t* beta,
     int h = hr / 128, row = hr % 128;
     float gt = g[h];
     float bt = F(beta[h]);
-    float mem_l[4], out_l[4];
     float* st = state + ((size_t)h * 128 + row) * 128;
     const uint16_t* qv = conv + h * 128;
     const uint16_t* kv = conv + 2048 + h * 128;
     float vv = F(conv[4096 + h * 128 + row]);
-    for (int l = 0; l < 4; ++l) {
-      float part[8];
-      for (int pb = 0; pb < 8; ++pb) {
-        float acc = 0.0f;
-        for (int i = 0; i < 4; ++i) {
-          int e = l * 32 + pb * 4 + i;
-          st[e] = st[e] * gt;
-          acc += st[e] * F(kv[e]);
-        }
-        part[pb] = acc;
+    float lane[16];
+    for (int j = 0; j < 16; ++j) {
+      float acc = 0.0f;
+      for (int i = 0; i < 8; ++i) {
+        int e = 8 * j + i;
+        st[e] = st[e] * gt;
+        acc = fmaf(st[e], F(kv[e]), acc);
       }
-      mem_l[l] = ((part[0] + part[1]) + (part[2] + part[3])) + ((part[4] + part[5]) + (part[6] + part[7]));
+      lane[j] = acc;
     }
-    float memory = (mem_l[0] + mem_l[1]) + (mem_l[2] + mem_l[3]);
+    float memory = tree(lane, 16);
     float delta = (vv - memory) * bt;
-    for (int l = 0; l < 4; ++l) {
-      float part[8];
-      for (int pb = 0; pb < 8; ++pb) {
-        float acc = 0.0f;
-        for (int i = 0; i < 4; ++i) {
-          int e = l * 32 + pb * 4 + i;
-          st[e] = st[e] + F(kv[e]) * delta;
-          acc += st[e] * F(qv[e]);
-        }
-        part[pb] = acc;
+    for (int j = 0; j < 16; ++j) {
+      float acc = 0.0f;
+      for (int i = 0; i < 8; ++i) {
+        int e = 8 * j + i;
+        st[e] = fmaf(F(kv[e]), delta, st[e]);
+        acc = fmaf(st[e], F(qv[e]), acc);
       }
-      out_l[l] = ((part[0] + part[1]) + (part[2] + part[3])) + ((part[4] + part[5]) + (part[6] + part[7]));
+      lane[j] = acc;
     }
-    float out = (out_l[0] + out_l[1]) + (out_l[2] + out_l[3]);
-    y[h * 128 + row] = eo_f32_to_bf16(out);
+    y[h * 128 + row] = eo_f32_to_bf16(tree(lane, 16));
   }
 }
 
-/* gdn_norm_gate, gdn.metal:238-254 (fp32 sigmoid, unlike the MLX unary one) */
+/* gdn_norm_gate, gdn.metal:238-254 (fp32 sigmoid, unlike the MLX unary one).
+ * Fixed order: 16 lanes of 8 channels per head, fma chain of squares, tree
+ * over the 16 lanes. */
 void eo_gdn_norm_gate(const uint16_t* y, const uint16_t* z, const uint16_t* w, uint16_t* out) {
   for (int h = 0; h < 16; ++h) {
-    float lane_ss[32];
-    for (int lane = 0; lane < 32; ++lane) {
+    float lane[16];
+    for (int j = 0; j < 16; ++j) {
       float ss = 0.0f;
-      for (int i = 0; i < 4; ++i) {
-        float v = F(y[h * 128 + lane * 4 + i]);
-        ss += v * v;
+      for (int i = 0; i < 8; ++i) {
+        float v = F(y[h * 128 + 8 * j + i]);
+        ss = fmaf(v, v, ss);
       }
-      lane_ss[lane] = ss;
+      lane[j] = ss;
     }
-    float ss = bfly_sum(lane_ss, 32);
+    float ss = tree(lane, 16);
     float inv = 1.0f / sqrtf(ss / 128.0f + 1.0e-6f);
     for (int d = 0; d < 128; ++d) {
       int off = h * 128 + d;
       float norm = BF(BF(F(y[off]) * inv) * F(w[d]));
       float gate = F(z[off]);
-      float sy = 1.0f / (1.0f + expf(fabsf(gate)));
+      float sy = 1.0f / (1.0f + eo_exp(fabsf(gate)));
       float sig = gate < 0.0f ? sy : 1.0f - sy;
       out[off] = eo_f32_to_bf16((gate * sig) * norm);
     }
@@ -338,34 +394,32 @@ void eo_gdn_norm_gate(const uint16_t* y, const uint16_t* z, const uint16_t* w, u
 /* ------------------------------------------------------------------ */
 /* attention                                                           */
 /* ------------------------------------------------------------------ */
-/* attention.metal:36-53: 64 threads x 4 values, two simd sums added */
+/* attention.metal:36-53 arithmetic; fixed order: 64 lanes of 4 dims, fma
+ * chain of squares, tree over the 64 lanes. */
 static float head_inv_rms(const uint16_t* x) {
-  float sums[2];
-  for (int sg = 0; sg < 2; ++sg) {
-    float lane[32];
-    for (int l = 0; l < 32; ++l) {
-      int t = sg * 32 + l;
-      float s = 0.0f;
-      for (int i = 0; i < 4; ++i) {
-        float v = F(x[4 * t + i]);
-        s += v * v;
-      }
-      lane[l] = s;
+  float lane[64];
+  for (int t = 0; t < 64; ++t) {
+    float s = 0.0f;
+    for (int i = 0; i < 4; ++i) {
+      float v = F(x[4 * t + i]);
+      s = fmaf(v, v, s);
     }
-    sums[sg] = bfly_sum(lane, 32);
+    lane[t] = s;
   }
-  return 1.0f / sqrtf((sums[0] + sums[1]) / 256.0f + 1e-6f);
+  return 1.0f / sqrtf(tree(lane, 64) / 256.0f + 1e-6f);
 }
 
-/* attention.metal:55-70 */
+/* attention.metal:55-70: pairs (i, i+32) for i < 32, angle = pos*inv_freq;
+ * d < 32: fma(lo, c, -(hi*s)); 32 <= d < 64: fma(lo, s, hi*c). */
 static uint16_t rope_component(const float* normalized, int d, int position) {
   if (d >= 64) return eo_f32_to_bf16(normalized[d]);
   int pair = d % 32;
   float inv_freq = eo_rope_inv_freq(pair);
   float angle = (float)position * inv_freq;
-  float c = cosf(angle), s = sinf(angle);
+  float s, c;
+  eo_sincos(angle, &s, &c);
   float lo = normalized[pair], hi = normalized[pair + 32];
-  return eo_f32_to_bf16(d < 32 ? lo * c - hi * s : lo * s + hi * c);
+  return eo_f32_to_bf16(d < 32 ? fmaf(lo, c, -(hi * s)) : fmaf(lo, s, hi * c));
 }
 
 void eo_attn_prepare(const uint16_t* q_proj, const uint16_t* k, const uint16_t* v,
@@ -400,7 +454,7 @@ static float lane_score(const float* q, const uint16_t* krow, int lane) {
 static float simd_score(const float* q, const uint16_t* krow) {
   float lanes[32];
   for (int l = 0; l < 32; ++l) lanes[l] = lane_score(q, krow, l);
-  return bfly_sum(lanes, 32);
+  return tree(lanes, 32);
 }
 
 /* sdpa_vector<bf16,256>, attention_decode.metal:51-213 (32 simdgroups) */
@@ -422,8 +476,8 @@ void eo_attn_decode_single(const uint16_t* query, const uint16_t* kcache, const 
       for (int i = sg; i < length; i += 32) {
         float score = simd_score(q, kb + (size_t)i * 256);
         float new_max = fmaxf(max_score, score);
-        float factor = expf(max_score - new_max);
-        float es = expf(score - new_max);
+        float factor = eo_exp(max_score - new_max);
+        float es = eo_exp(score - new_max);
         max_score = new_max;
         sum_exp = sum_exp * factor + es;
         for (int d = 0; d < 256; ++d) o[sg][d] = o[sg][d] * factor + es * F(vb[(size_t)i * 256 + d]);
@@ -435,13 +489,13 @@ void eo_attn_decode_single(const uint16_t* query, const uint16_t* kcache, const 
     for (int s = 1; s < 32; ++s) new_max = fmaxf(new_max, mx[s]);
     float fac[32], tmp[32];
     for (int s = 0; s < 32; ++s) {
-      fac[s] = expf(mx[s] - new_max);
+      fac[s] = eo_exp(mx[s] - new_max);
       tmp[s] = sm[s] * fac[s];
     }
-    float sum_exp = bfly_sum(tmp, 32);
+    float sum_exp = tree(tmp, 32);
     for (int d = 0; d < 256; ++d) {
       for (int s = 0; s < 32; ++s) tmp[s] = o[s][d] * fac[s];
-      float v = bfly_sum(tmp, 32);
+      float v = tree(tmp, 32);
       v = sum_exp == 0.0f ? v : v / sum_exp;
       out[h * 256 + d] = eo_f32_to_bf16(v);
     }
@@ -468,8 +522,8 @@ void eo_attn_decode_split(const uint16_t* query, const uint16_t* kcache, const u
     for (int i = blk; i < length; i += 64) {
       float score = simd_score(q, kb + (size_t)i * 256);
       float new_max = fmaxf(max_score, score);
-      float factor = expf(max_score - new_max);
-      float es = expf(score - new_max);
+      float factor = eo_exp(max_score - new_max);
+      float es = eo_exp(score - new_max);
       max_score = new_max;
       sum_exp = sum_exp * factor + es;
       for (int d = 0; d < 256; ++d) o[d] = o[d] * factor + es * F(vb[(size_t)i * 256 + d]);
@@ -491,20 +545,20 @@ void eo_attn_split_merge_gate(const uint16_t* partials, const float* sums, const
     float lane[32];
     for (int l = 0; l < 32; ++l) {
       float s = 0.0f;
-      for (int bb = 0; bb < 2; ++bb) s += expf(hm[l + 32 * bb] - M) * hs[l + 32 * bb];
+      for (int bb = 0; bb < 2; ++bb) s += eo_exp(hm[l + 32 * bb] - M) * hs[l + 32 * bb];
       lane[l] = s;
     }
-    float sum_exp = bfly_sum(lane, 32);
+    float sum_exp = tree(lane, 32);
     for (int d = 0; d < 256; ++d) {
       for (int l = 0; l < 32; ++l) {
         float o = 0.0f;
         for (int bb = 0; bb < 2; ++bb) {
           int b = l + 32 * bb;
-          o += expf(hm[b] - M) * F(partials[((size_t)h * 64 + b) * 256 + d]);
+          o += eo_exp(hm[b] - M) * F(partials[((size_t)h * 64 + b) * 256 + d]);
         }
         lane[l] = o;
       }
-      float o = bfly_sum(lane, 32);
+      float o = tree(lane, 32);
       o = sum_exp == 0.0f ? o : o / sum_exp;
       float attention = BF(o);
       float gate = eo_sigmoid_bf(F(q_proj[h * 512 + 256 + d]));
@@ -541,54 +595,56 @@ void eo_attn_decode_gated(const uint16_t* query, const uint16_t* kcache, const u
 /* ------------------------------------------------------------------ */
 /* head                                                                */
 /* ------------------------------------------------------------------ */
-/* head_lse_g8 (:15-63) online (max,sum) per owner of 4-logit tiles, then
- * head_lse_tail (:66-97): lse = bf16(log(sum)+max); token = lowest index of
- * the maximum of bf16(logit - lse). */
+/* head_lse_g8 + head_lse_tail arithmetic (head_lse.metal:51-97): logits are
+ * bf16; lse = bf16(log(sum exp(l - max)) + max); token = lowest index of the
+ * maximum of bf16(l - lse) (docs/protocol.md:44). Fixed order: blocks of 256
+ * consecutive logits, block max exact, block sum = (w0 + w1) + (w2 + w3) where
+ * w is a tree over a 64-logit quarter of exp(l - blockmax) (0 past the end);
+ * the global sum has 256 accumulators, accumulator t adding
+ * sum_b * exp(max_b - max) for blocks b = t, t+256, ... in order, then the
+ * same 4 x 64 tree-and-pairs combination. */
 uint32_t eo_greedy(const uint16_t* logits, int n, float* lse_out) {
-  float pmax[1024], psum[1024];
-  int tiles = (n + 4095) / 4096;
-  for (int owner = 0; owner < 1024; ++owner) {
-    float vmax = -FLT_MAX, normalizer = 0.0f;
-    for (int tile = 0; tile < tiles; ++tile) {
-      int row0 = tile * 4096 + owner * 4;
-      float vals[4] = {-INFINITY, -INFINITY, -INFINITY, -INFINITY};
-      if (row0 < n)
-        for (int q = 0; q < 4; ++q)
-          if (row0 + q < n) vals[q] = F(logits[row0 + q]);
-      float prev = vmax;
-      for (int j = 0; j < 4; ++j) vmax = fmaxf(vmax, vals[j]);
-      normalizer *= expf(prev - vmax);
-      for (int j = 0; j < 4; ++j) normalizer += expf(vals[j] - vmax);
+  const int nb = (n + 255) / 256;
+  float* pmax = (float*)malloc(sizeof(float) * nb);
+  float* psum = (float*)malloc(sizeof(float) * nb);
+  for (int b = 0; b < nb; ++b) {
+    float m = -INFINITY;
+    for (int i = 0; i < 256; ++i)
+      if (b * 256 + i < n) m = fmaxf(m, F(logits[b * 256 + i]));
+    float w[4];
+    for (int q = 0; q < 4; ++q) {
+      float e[64];
+      for (int i = 0; i < 64; ++i) {
+        int r = b * 256 + q * 64 + i;
+        e[i] = r < n ? eo_exp(F(logits[r]) - m) : 0.0f;
+      }
+      w[q] = tree(e, 64);
     }
-    pmax[owner] = vmax;
-    psum[owner] = normalizer;
+    pmax[b] = m;
+    psum[b] = (w[0] + w[1]) + (w[2] + w[3]);
   }
-  /* tail: 32 simdgroups of 32 */
-  float sg_max[32], sg_sum[32];
-  for (int sg = 0; sg < 32; ++sg) {
-    float m = -FLT_MAX;
-    for (int l = 0; l < 32; ++l) m = fmaxf(m, pmax[sg * 32 + l]);
-    float lane[32];
-    for (int l = 0; l < 32; ++l) lane[l] = psum[sg * 32 + l] * expf(pmax[sg * 32 + l] - m);
-    sg_max[sg] = m;
-    sg_sum[sg] = bfly_sum(lane, 32);
+  float gm = -FLT_MAX;
+  for (int b = 0; b < nb; ++b) gm = fmaxf(gm, pmax[b]);
+  float acc[256];
+  for (int t = 0; t < 256; ++t) {
+    float a = 0.0f;
+    for (int b = t; b < nb; b += 256) a = a + psum[b] * eo_exp(pmax[b] - gm);
+    acc[t] = a;
   }
-  float vmax = -FLT_MAX;
-  for (int s = 0; s < 32; ++s) vmax = fmaxf(vmax, sg_max[s]);
-  float lane[32];
-  for (int s = 0; s < 32; ++s) lane[s] = sg_sum[s] * expf(sg_max[s] - vmax);
-  float normalizer = bfly_sum(lane, 32);
-  float lse = BF(logf(normalizer) + vmax);
+  float w4[4];
+  for (int q = 0; q < 4; ++q) w4[q] = tree(acc + 64 * q, 64);
+  float gs = (w4[0] + w4[1]) + (w4[2] + w4[3]);
+  float lse = BF(eo_log(gs) + gm);
   if (lse_out) *lse_out = lse;
-  float best = -INFINITY;
-  uint32_t id = 0xffffffffu;
-  for (int i = 0; i < n; ++i) {
-    float v = BF(F(logits[i]) - lse);
-    if (v > best) {
-      best = v;
+  float target = BF(gm - lse);
+  uint32_t id = 0;
+  for (int i = 0; i < n; ++i)
+    if (BF(F(logits[i]) - lse) == target) {
       id = (uint32_t)i;
+      break;
     }
-  }
+  free(pmax);
+  free(psum);
   return id;
 }
 

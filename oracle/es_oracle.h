@@ -9,11 +9,16 @@
  * Every function restates one reference kernel; the citation names the Metal
  * source (paths relative to the reference checkout). bf16 values are passed
  * as raw uint16_t bit patterns; "bf16(x)" means round-to-nearest-even of an
- * fp32 value. Floating-point accumulation is fp32 in the reference's order
- * where the order is stated in source (lane slices, fixed trees); SIMD-group
- * sums, whose hardware order is unspecified, are restated as xor-butterfly
- * trees. The library is compiled with -ffp-contract=off so no FMA is formed
- * except where the reference writes fma().
+ * fp32 value, taken at exactly the reference's rounding points. The
+ * reference's fp32 accumulation order is not fully specified (Metal simd_sum
+ * trees and FMA contraction are left to its compiler), so every reduction here
+ * follows one stated fp32 order -- the one the HIP kernels use -- which makes
+ * the parity tests bitwise where the algorithms coincide. exp/log/sin/cos are
+ * the series evaluations in es_oracle.c (the kernels evaluate the same
+ * steps). Compiled with -ffp-contract=off: FMAs appear only where fmaf is
+ * written. Decode attention keeps the reference's own algorithm (32 or 64
+ * interleaved position blocks, bf16 partials at and above 1024 positions),
+ * which the GPU's split-K decode does not reproduce bit for bit.
  *
  * Pinning status (tests/test_oracle_*.py):
  *   bf16 RNE, nibble unpack ........ exhaustive/torch cross-check, closed forms
@@ -51,6 +56,9 @@ uint16_t eo_f32_to_bf16(float f);
 float eo_round_bf16(float f);
 void eo_f32_to_bf16_array(const float* in, uint16_t* out, size_t n);
 void eo_bf16_to_f32_array(const uint16_t* in, float* out, size_t n);
+float eo_exp(float x);          /* series exp (degree-7 Taylor after ln2 reduction) */
+float eo_log(float x);          /* series log (atanh series), positive normal x */
+void eo_sincos(float x, float* s, float* c); /* double quadrant reduction + Taylor */
 float eo_sigmoid_bf(float x);   /* linear.metal:389-395, gdn.metal:10-15 */
 float eo_softplus_bf(float x);  /* gdn.metal:19-29 */
 float eo_rope_inv_freq(int pair); /* attention.metal:62-63 */

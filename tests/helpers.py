@@ -69,3 +69,18 @@ def rel_err(a, b):
     a = np.asarray(a, dtype=np.float64)
     b = np.asarray(b, dtype=np.float64)
     return float(np.linalg.norm(a - b) / max(np.linalg.norm(b), 1e-30))
+
+
+def assert_bits_equal(got, want, what=""):
+    """Bitwise equality of two arrays (bf16 bit patterns or fp32)."""
+    got = np.ascontiguousarray(got).ravel()
+    want = np.ascontiguousarray(want).ravel()
+    assert got.shape == want.shape, (what, got.shape, want.shape)
+    gv = got.view(np.uint16 if got.dtype == np.uint16 else np.uint32)
+    wv = want.view(np.uint16 if want.dtype == np.uint16 else np.uint32)
+    bad = np.nonzero(gv != wv)[0]
+    if bad.size:
+        i = int(bad[0])
+        g = f32(got[i:i + 1])[0] if got.dtype == np.uint16 else got[i]
+        w = f32(want[i:i + 1])[0] if want.dtype == np.uint16 else want[i]
+        raise AssertionError(f"{what}: {bad.size} of {gv.size} differ (first [{i}] got {g!r} want {w!r})")

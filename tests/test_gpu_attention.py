@@ -14,7 +14,7 @@ import pytest
 
 import esdecode as E
 import oracle as O
-from helpers import assert_bf16_close, bf16, f32, rel_err, rng
+from helpers import assert_bf16_close, assert_bits_equal, bf16, f32, rel_err, rng
 
 pytestmark = pytest.mark.gpu
 
@@ -69,10 +69,10 @@ def run_case(length, seed, splits=None):
 def test_attention_decode(length):
     print(f"case attention length={length}", flush=True)
     got, want, q_proj = run_case(length, 500 + length)
-    assert_bf16_close(got["query"], want["query"], max_ulp=1, max_frac=0.01, what="query")
+    assert_bits_equal(got["query"], want["query"], what="query")
     pos = length - 1
     assert np.array_equal(got["vc"][:, pos], want["vc"][:, pos]), "V row must be copied exactly"
-    assert_bf16_close(got["kc"][:, pos], want["kc"][:, pos], max_ulp=1, max_frac=0.01, what="K row")
+    assert_bits_equal(got["kc"][:, pos], want["kc"][:, pos], what="K row")
     assert np.array_equal(got["kc"][:, :pos], want["kc"][:, :pos]), "earlier cache rows must be untouched"
     exact = fp64_gated(want["query"], want["kc"], want["vc"], length, q_proj)
     # GPU: fp32 online softmax with fp32 partials -> within one bf16 ulp of fp64
