@@ -198,19 +198,19 @@ int es_rope_inv_freq(float* host_out32) {
   return ES_OK;
 }
 
-size_t es_attn_scratch_bytes(int splits) {
-  if (splits < 1 || splits > 1024) return 0;
-  return es::attn_scratch_bytes(splits);
+size_t es_attn_scratch_bytes(int capacity) {
+  if (capacity < 1) return 0;
+  return es::attn_scratch_bytes(capacity);
 }
 
 int es_attn_decode(const uint16_t* q_proj, const uint16_t* k_proj, const uint16_t* v_proj,
                    const uint16_t* q_gain, const uint16_t* k_gain, uint16_t* kcache,
                    uint16_t* vcache, int capacity, int position, const float* inv_freq,
-                   int splits, void* scratch, size_t scratch_bytes, uint16_t* gated,
+                   int blocks, void* scratch, size_t scratch_bytes, uint16_t* gated,
                    uint16_t* query_out, void* stream) {
-  if (splits < 1 || splits > 1024) return fail(ES_ERR_INVALID, "es_attn_decode: splits must be 1..1024");
+  if (blocks < 1 || blocks > 1024) return fail(ES_ERR_INVALID, "es_attn_decode: blocks must be 1..1024");
   if (position < 0 || position >= capacity) return fail(ES_ERR_INVALID, "es_attn_decode: position outside capacity");
-  if (!scratch || scratch_bytes < es::attn_scratch_bytes(splits))
+  if (!scratch || scratch_bytes < es::attn_scratch_bytes(capacity))
     return fail(ES_ERR_INVALID, "es_attn_decode: scratch too small");
   es::AttnArgs a{};
   a.q_proj = q_proj;
@@ -222,13 +222,13 @@ int es_attn_decode(const uint16_t* q_proj, const uint16_t* k_proj, const uint16_
   a.vcache = vcache;
   a.capacity = capacity;
   a.inv_freq = inv_freq;
-  a.part_o = static_cast<float*>(scratch);
-  a.part_ml = a.part_o + (size_t)8 * splits * 256;
-  a.splits = splits;
+  es::attn_bind_scratch(a, scratch);
+  a.blocks = blocks;
   a.gated = gated;
   a.query_out = query_out;
   a.pos_val = position;
-  if (int rc = hip_status(es::launch_attn_split(a, S(stream)), "es_attn_decode split")) return rc;
+  if (int rc = hip_status(es::launch_attn_scores(a, S(stream)), "es_attn_decode scores")) return rc;
+  if (int rc = hip_status(es::launch_attn_chain(a, S(stream)), "es_attn_decode chains")) return rc;
   return hip_status(es::launch_attn_merge(a, S(stream)), "es_attn_decode merge");
 }
 
@@ -367,10 +367,10 @@ int es_engine_time_decode(es_engine* e, int steps, int warmup, double* ms_total)
   std::string err;
   return engine_rc(e->impl->time_decode(steps, warmup, ms_total, &err), err);
 }
-int es_engine_time_attention(es_engine* e, int layer, int reps, double* ms_avg) {
+int es_engine_time_attention(es_engine* e, int layer, int reps, int which, double* ms_avg) {
   if (!e || !ms_avg) return fail(ES_ERR_INVALID, "null engine/output");
   std::string err;
-  return engine_rc(e->impl->time_attention(layer, reps, ms_avg, &err), err);
+  return engine_rc(e->impl->time_attention(layer, reps, which, ms_avg, &err), err);
 }
 int es_engine_time_head(es_engine* e, int reps, double* ms_avg) {
   if (!e || !ms_avg) return fail(ES_ERR_INVALID, "null engine/output");

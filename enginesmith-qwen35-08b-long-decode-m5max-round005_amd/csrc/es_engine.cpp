@@ -137,8 +137,7 @@ int Engine::init(const void* blob, uint64_t bytes, std::string* err) {
   act_ = static_cast<uint16_t*>(alloc(3584 * 2));
   logits_ = static_cast<uint16_t*>(alloc((size_t)shape_.vocab * 2));
   head_part_ = static_cast<float*>(alloc((size_t)head_blocks(shape_.vocab) * 2 * sizeof(float)));
-  part_o_ = static_cast<float*>(alloc((size_t)8 * 256 * 256 * sizeof(float)));
-  part_ml_ = static_cast<float*>(alloc((size_t)8 * 256 * 2 * sizeof(float)));
+  attn_scratch_ = alloc(attn_scratch_bytes(capacity_));
   inv_freq_ = static_cast<float*>(alloc(32 * sizeof(float)));
   st_ = static_cast<StepState*>(alloc(sizeof(StepState)));
   prompt_ = static_cast<uint32_t*>(alloc((size_t)capacity_ * 4));
@@ -146,7 +145,7 @@ int Engine::init(const void* blob, uint64_t bytes, std::string* err) {
   forced_ = static_cast<uint32_t*>(alloc((size_t)capacity_ * 4));
   for (void* p : {(void*)h_, (void*)z_, (void*)ab_, (void*)y_, (void*)q_, (void*)k_, (void*)v_,
                   (void*)act_, (void*)logits_, (void*)head_part_,
-                  (void*)part_o_, (void*)part_ml_, (void*)inv_freq_, (void*)st_, (void*)prompt_,
+                  attn_scratch_, (void*)inv_freq_, (void*)st_, (void*)prompt_,
                   (void*)out_, (void*)forced_}) {
     if (!p) {
       if (err) *err = "device allocation of scratch failed";
@@ -191,9 +190,8 @@ AttnArgs Engine::attn_args(const LayerDev& L, int splits) {
   a.vcache = L.vcache;
   a.capacity = capacity_;
   a.inv_freq = inv_freq_;
-  a.part_o = part_o_;
-  a.part_ml = part_ml_;
-  a.splits = splits;
+  attn_bind_scratch(a, attn_scratch_);
+  a.blocks = splits;
   a.gated = y_;
   a.query_out = nullptr;
   a.st = st_;
@@ -242,7 +240,8 @@ hipError_t Engine::enqueue_layers(hipStream_t s, int splits) {
       nm.m[2] = L.v; nm.y[2] = v_;
       if ((e = launch_norm_multi(nm, s)) != hipSuccess) return e;
       const AttnArgs a = attn_args(L, splits);
-      if ((e = launch_attn_split(a, s)) != hipSuccess) return e;
+      if ((e = launch_attn_scores(a, s)) != hipSuccess) return e;
+      if ((e = launch_attn_chain(a, s)) != hipSuccess) return e;
       if ((e = launch_attn_merge(a, s)) != hipSuccess) return e;
       if ((e = launch_qmv(L.o, y_, h_, h_, nullptr, s)) != hipSuccess) return e;
     }
@@ -568,20 +567,31 @@ int Engine::time_decode(int steps, int warmup, double* ms_total, std::string* er
   return 0;
 }
 
-int Engine::time_attention(int layer, int reps, double* ms_avg, std::string* err) {
-  if (layer < 0 || layer >= shape_.n_layers || !layers_[layer].attention || reps <= 0) {
+hipError_t Engine::launch_attention_part(const AttnArgs& a, int which) {
+  hipError_t e = hipSuccess;
+  if (which == 0 || which == 1) e = launch_attn_scores(a, stream_);
+  if (e == hipSuccess && (which == 0 || which == 2)) e = launch_attn_chain(a, stream_);
+  if (e == hipSuccess && (which == 0 || which == 3)) e = launch_attn_merge(a, stream_);
+  return e;
+}
+
+int Engine::time_attention(int layer, int reps, int which, double* ms_avg, std::string* err) {
+  if (layer < 0 || layer >= shape_.n_layers || !layers_[layer].attention || reps <= 0 ||
+      which < 0 || which > 3) {
     if (err) *err = "invalid attention timing request";
     return 1;
   }
   if (int rc = upload_state(position_, 0, pending_, err)) return rc;
   const AttnArgs a = attn_args(layers_[layer], splits_for(position_ + 1));
-  ES_HIP(launch_attn_split(a, stream_), "attn warmup");
+  // The timed launches write the K/V row of the current position, the row the
+  // next decode step writes before anything reads it.
+  ES_HIP(launch_attention_part(a, 0), "attn warmup");
   ES_HIP(hipStreamSynchronize(stream_), "sync");
   hipEvent_t e0, e1;
   ES_HIP(hipEventCreate(&e0), "event");
   ES_HIP(hipEventCreate(&e1), "event");
   ES_HIP(hipEventRecord(e0, stream_), "record");
-  for (int i = 0; i < reps; ++i) ES_HIP(launch_attn_split(a, stream_), "attn");
+  for (int i = 0; i < reps; ++i) ES_HIP(launch_attention_part(a, which), "attn");
   ES_HIP(hipEventRecord(e1, stream_), "record");
   ES_HIP(hipEventSynchronize(e1), "sync");
   float ms = 0.0f;

@@ -71,7 +71,8 @@ class Engine {
 
   // Timing (HIP events on the engine stream).
   int time_decode(int steps, int warmup, double* ms_total, std::string* err);
-  int time_attention(int layer, int reps, double* ms_avg, std::string* err);
+  // which: 0 = the three attention launches, 1 = scores, 2 = chains, 3 = merge.
+  int time_attention(int layer, int reps, int which, double* ms_avg, std::string* err);
   int time_head(int reps, double* ms_avg, std::string* err);
 
   int n_layers() const { return shape_.n_layers; }
@@ -90,6 +91,7 @@ class Engine {
                 uint16_t* logits_out, std::string* err);
   int upload_state(int pos, int step, uint32_t token, std::string* err);
   AttnArgs attn_args(const LayerDev& L, int splits);
+  hipError_t launch_attention_part(const AttnArgs& a, int which);
 
   ModelShape shape_{};
   int capacity_ = 0;
@@ -111,8 +113,7 @@ class Engine {
   uint16_t* act_ = nullptr;     // [3584]
   uint16_t* logits_ = nullptr;  // [vocab]
   float* head_part_ = nullptr;
-  float* part_o_ = nullptr;
-  float* part_ml_ = nullptr;
+  void* attn_scratch_ = nullptr;  // chain outputs, chain (max, sum), scores
   float* inv_freq_ = nullptr;
   StepState* st_ = nullptr;
   uint32_t* prompt_ = nullptr;  // [capacity]

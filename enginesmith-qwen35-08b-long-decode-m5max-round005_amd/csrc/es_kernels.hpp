@@ -69,6 +69,13 @@ hipError_t launch_gdn_gate_out(const Q4& w, const uint16_t* y, const uint16_t* z
                                hipStream_t s);
 
 // ---- attention, k_attention.hip ----
+// Decode attention follows the reference's two routes (model.rs:327-347):
+// below 1024 cached positions 32 interleaved position chains combined in
+// fp32 (sdpa_vector), from 1024 on 64 chains whose outputs are rounded to
+// bf16 before the gated merge (sdpa_vector_2pass_1 + split2_gate). Three
+// launches: scores, per-chain online softmax, merge + gate.
+constexpr int kAttnRouteSplit = 1024;  // first length served by 64 chains
+constexpr int kAttnMaxChains = 64;
 struct AttnArgs {
   const uint16_t* q_proj;   // [8, 512] query|gate per head
   const uint16_t* k_proj;   // [2, 256]
@@ -79,16 +86,19 @@ struct AttnArgs {
   uint16_t* vcache;         // [2, capacity, 256]
   int capacity;
   const float* inv_freq;    // [32] rotary inverse frequencies
-  float* part_o;            // [8, splits, 256]
-  float* part_ml;           // [8, splits, 2]
-  int splits;
+  float* part_o;            // [8, 64, 256] unnormalised chain outputs
+  float* part_ml;           // [8, 64, 2] chain (max, sum)
+  float* scores;            // [8, capacity] scaled q.k per position
+  int blocks;               // score blocks per KV head
   uint16_t* gated;          // [8, 256]
   uint16_t* query_out;      // optional [8, 256] roped queries
   const StepState* st;
   int pos_val;
 };
-size_t attn_scratch_bytes(int splits);
-hipError_t launch_attn_split(const AttnArgs& a, hipStream_t s);
+size_t attn_scratch_bytes(int capacity);
+void attn_bind_scratch(AttnArgs& a, void* scratch);
+hipError_t launch_attn_scores(const AttnArgs& a, hipStream_t s);
+hipError_t launch_attn_chain(const AttnArgs& a, hipStream_t s);
 hipError_t launch_attn_merge(const AttnArgs& a, hipStream_t s);
 
 // ---- vocab head, k_head.hip ----

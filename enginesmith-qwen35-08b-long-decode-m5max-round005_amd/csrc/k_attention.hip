@@ -1,34 +1,37 @@
-// Long-context GQA decode attention on gfx950 (8 query heads, 2 KV heads,
-// head dim 256, one query token), as a split-K flash decode.
+// GQA decode attention on gfx950 (8 query heads, 2 KV heads, head dim 256,
+// one query token), computing the reference's own two routes
+// (model.rs:327-347) in a fixed fp32 order:
+//   length < 1024: 32 position chains (chain c takes positions c, c+32, ...),
+//     combined in fp32 (sdpa_vector, attention_decode.metal:51-213);
+//   length >= 1024: 64 chains whose unnormalised outputs are rounded to bf16,
+//     then merged and gated (sdpa_vector_2pass_1 + attn_decode_split2_gate,
+//     attention_decode.metal:215-431, 830-891).
 //
-// k_attn_split: grid (splits, 2 KV heads), 256 threads. Each block streams a
-// contiguous chunk of one KV head's cache exactly once and serves all four
-// query heads of that group. A 16-lane row owns one position per step (16
-// dims = 32 B of K and of V per lane, 2 positions per pass); scores use
-// v_dot2 on bf16 pairs (q is bf16 and q*1/16 is exact), the 16-lane sum is a
-// DPP row reduction, and the online softmax keeps fp32 (max, sum, o[256]).
-// The 16 row-states of the block are merged in LDS and one fp32 partial per
-// (query head, split) is written.
-// The prologue fuses attn_prepare_qkv_decode (attention.metal:262-313): q/k
-// RMSNorm (eps 1e-6, bf16 normalised value, bf16 gain product) and partial
-// RoPE on dims 0..63 with pairs (i, i+32). The block of the last split also
-// writes the new K/V row at `position` and scores it from LDS.
-//
-// k_attn_merge: grid (8 heads, 8 x 32 dims): log-sum-exp merge of the
-// partials, then gated = bf16(bf16(o) * sigmoid_bf(gate))
-// (attention_decode.metal:841-890, attention.metal:140-150).
+// k_attn_scores, grid (blocks, 2 KV heads) x 256: the prologue fuses
+//   attn_prepare_qkv_decode (attention.metal:262-313: q/k RMSNorm with bf16
+//   normalised value and bf16 gain product, RoPE on dims 0..63 with pairs
+//   (i, i+32)); the block whose chunk holds the new position also writes its
+//   K/V rows. Each block then streams a contiguous chunk of the K cache once
+//   for all four query heads of the group: 8 lanes per position, lane m holds
+//   dims 8m+64i .. +7 (i = 0..3, 128 coalesced bytes per 8 lanes), one fma
+//   chain per 8 dims, (p[m]+p[m+8])+(p[m+16]+p[m+24]) in the lane and a DPP
+//   tree over the 8 lanes. Scores go to an fp32 array [8, capacity].
+// k_attn_chain, 256 blocks x 320 threads: block = (KV head, chain, query-head
+//   pair). Waves 0..3 own one value dim each for both heads; wave 4 turns the
+//   chain's scores into running max, factor and exp score, 64 steps at a time
+//   and one tile ahead (max scan by DPP, exp by the shared series). Per step
+//   o = fma(e, v, o*factor) and sum = sum*factor + e; when every factor of a
+//   tile is exactly 1 the products by 1 are skipped, which changes no bit.
+//   The two blocks of a (KV head, chain) sit on the same XCD (block ids b and
+//   b+8) so the second read of each V row is an L2 hit.
+// k_attn_merge, grid (8 heads, 4 quarters) x 64: chain combination of either
+//   route, then gated = bf16(bf16(o) * sigmoid_bf(gate)) (attention.metal:133-151).
 #include "es_kernels.hpp"
 
 namespace es {
 namespace {
 
-constexpr float kLog2e = 1.4426950408889634f;
-constexpr int kMaxSplits = 1024;
-
-__device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float c) {
-  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, a),
-                                         __builtin_bit_cast(bf16x2_t, b), c, false);
-}
+constexpr float kFiniteMin = -3.40282346638528859812e38f;
 
 // Normalise 4 consecutive dims of a 256-wide head held by a full wave.
 __device__ __forceinline__ void head_norm4(const uint16_t* x, const uint16_t* gain, int lane,
@@ -58,64 +61,56 @@ __device__ __forceinline__ float rope_at(const float* nrm, int d, int pos, const
   return rbf(d < 32 ? fmaf(lo, c, -(hi * s)) : fmaf(lo, s, hi * c));
 }
 
-// Two consecutive positions of one 16-lane row: 32 B of K and of V each.
-struct KvPair {
-  u32x4 k0[2], k1[2], v0[2], v1[2];
-};
-
-// Load positions p and p+1 when they are below `end`; positions past the end
-// are clamped to a valid row and masked by the caller.
-__device__ __forceinline__ void kv_load(const uint16_t* kb, const uint16_t* vb, int p, int end,
-                                        KvPair& r) {
-  const int pa = p < end ? p : 0;
-  const int pb = p + 1 < end ? p + 1 : pa;
-  const u32x4* k0p = reinterpret_cast<const u32x4*>(kb + (size_t)pa * 256);
-  const u32x4* k1p = reinterpret_cast<const u32x4*>(kb + (size_t)pb * 256);
-  const u32x4* v0p = reinterpret_cast<const u32x4*>(vb + (size_t)pa * 256);
-  const u32x4* v1p = reinterpret_cast<const u32x4*>(vb + (size_t)pb * 256);
-  if (p < end) {
-    r.k0[0] = k0p[0]; r.k0[1] = k0p[1];
-    r.k1[0] = k1p[0]; r.k1[1] = k1p[1];
-    r.v0[0] = v0p[0]; r.v0[1] = v0p[1];
-    r.v1[0] = v1p[0]; r.v1[1] = v1p[1];
-  }
+__device__ __forceinline__ float tree8(float v) {
+  v = tree4(v);
+  return v + dpp_half_mirror(v);
 }
 
-__global__ __launch_bounds__(256) void k_attn_split(AttnArgs a) {
-  __shared__ float nrm[5][256];           // normalised q heads 0..3, new k
-  __shared__ uint32_t qpk[4][128];        // roped q * 1/16, bf16 pairs
-  __shared__ uint32_t kvnew[2][128];      // new K (roped) and V rows, bf16 pairs
-  __shared__ float mx[16][4];
-  __shared__ float osum[4][4][256];
-  __shared__ float lsum[4][4];
+// fma chain over the 8 bf16 dims of one 16-byte K chunk.
+__device__ __forceinline__ float chunk_dot(const float* q, const u32x4& k) {
+  float s = 0.0f;
+#pragma unroll
+  for (int w = 0; w < 4; ++w) {
+    s = fmaf(q[2 * w], bf_lo(k[w]), s);
+    s = fmaf(q[2 * w + 1], bf_hi(k[w]), s);
+  }
+  return s;
+}
+
+__global__ __launch_bounds__(256, 2) void k_attn_scores(AttnArgs a) {
+  __shared__ float nrm[5][256];     // normalised q heads 0..3, new k
+  __shared__ float qs[4][256];      // roped q * 1/16
+  __shared__ u32x4 knew[32];        // new K row (roped, bf16)
 
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
-  const int g = blockIdx.y, split = blockIdx.x, S = gridDim.x;
+  const int g = blockIdx.y, B = gridDim.x;
   const int pos = load_pos(a.st, a.pos_val);
-  const int cached = pos;  // cache rows [0, pos) hold earlier tokens
-  int chunk = (cached + S - 1) / S;
-  chunk = (chunk + 7) & ~7;
-  const int start = min(split * chunk, cached);
-  const int end = min(start + chunk, cached);
-  const bool last = split == S - 1;
+  const int n = pos + 1;
+  int chunk = (n + B - 1) / B;
+  chunk = (chunk + 31) & ~31;
+  const int start = blockIdx.x * chunk;
+  if (start >= n) return;
+  const int end = min(start + chunk, n);
+  const bool owner = end == n;  // this chunk holds the new position
 
-  // First K/V rows of this block's chunk: issued before the prologue so the
-  // memory latency overlaps the q normalisation and rotary math.
-  const int grp = lane >> 4, j = lane & 15;
-  const int G = wave * 4 + grp;  // row-state id 0..15
-  const uint16_t* kb = a.kcache + (size_t)g * a.capacity * 256 + j * 16;
-  const uint16_t* vb = a.vcache + (size_t)g * a.capacity * 256 + j * 16;
-  KvPair cur, nxt;
-  int p0 = start + 2 * G;
-  kv_load(kb, vb, p0, end, cur);
+  const int grp = lane >> 3, m = lane & 7;
+  const uint16_t* kb = a.kcache + (size_t)g * a.capacity * 256 + 8 * m;
+  // First K rows, issued before the prologue so their latency overlaps it.
+  u32x4 kc[4] = {}, kn[4] = {};
+  int p = start + wave * 8 + grp;
+  if (p < end && p != pos) {
+    const u32x4* r = reinterpret_cast<const u32x4*>(kb + (size_t)p * 256);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) kc[i] = r[8 * i];
+  }
 
-  // ---- prologue: q (and new k/v for the last split) ----
+  // ---- prologue: q (and, in the owner block, the new k/v rows) ----
   {
     float o4[4];
     head_norm4(a.q_proj + (4 * g + wave) * 512, a.q_gain, lane, o4);
 #pragma unroll
     for (int i = 0; i < 4; ++i) nrm[wave][lane * 4 + i] = o4[i];
-    if (last && wave == 0) {
+    if (owner && wave == 0) {
       head_norm4(a.k_proj + g * 256, a.k_gain, lane, o4);
 #pragma unroll
       for (int i = 0; i < 4; ++i) nrm[4][lane * 4 + i] = o4[i];
@@ -126,247 +121,334 @@ __global__ __launch_bounds__(256) void k_attn_split(AttnArgs a) {
     float r[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) r[i] = rope_at(nrm[wave], lane * 4 + i, pos, a.inv_freq);
-    if (a.query_out && split == 0) {
+    if (a.query_out && blockIdx.x == 0) {
       uint16_t* qo = a.query_out + (4 * g + wave) * 256 + lane * 4;
       *reinterpret_cast<uint2*>(qo) = make_uint2(pack_bf2(r[0], r[1]), pack_bf2(r[2], r[3]));
     }
-    qpk[wave][lane * 2] = pack_bf2(r[0] * 0.0625f, r[1] * 0.0625f);
-    qpk[wave][lane * 2 + 1] = pack_bf2(r[2] * 0.0625f, r[3] * 0.0625f);
-    if (last && wave == 1) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) qs[wave][lane * 4 + i] = r[i] * 0.0625f;
+    if (owner && wave == 1) {
       float kr[4];
 #pragma unroll
       for (int i = 0; i < 4; ++i) kr[i] = rope_at(nrm[4], lane * 4 + i, pos, a.inv_freq);
       const uint32_t k0 = pack_bf2(kr[0], kr[1]);
       const uint32_t k1 = pack_bf2(kr[2], kr[3]);
-      kvnew[0][lane * 2] = k0;
-      kvnew[0][lane * 2 + 1] = k1;
+      uint32_t* kw = reinterpret_cast<uint32_t*>(knew);
+      kw[lane * 2] = k0;
+      kw[lane * 2 + 1] = k1;
       const size_t ci = ((size_t)g * a.capacity + pos) * 256 + lane * 4;
       *reinterpret_cast<uint2*>(a.kcache + ci) = make_uint2(k0, k1);
-      const uint2 vv = *reinterpret_cast<const uint2*>(a.v_proj + g * 256 + lane * 4);
-      kvnew[1][lane * 2] = vv.x;
-      kvnew[1][lane * 2 + 1] = vv.y;
-      *reinterpret_cast<uint2*>(a.vcache + ci) = vv;
+      *reinterpret_cast<uint2*>(a.vcache + ci) =
+          *reinterpret_cast<const uint2*>(a.v_proj + g * 256 + lane * 4);
     }
   }
   __syncthreads();
 
-  // ---- main loop ----
-  uint32_t q[4][8];
+  // q for this lane's dims: 4 heads x 4 chunks x 8 dims.
+  float q[4][4][8];
 #pragma unroll
   for (int hh = 0; hh < 4; ++hh)
 #pragma unroll
-    for (int i = 0; i < 8; ++i) q[hh][i] = qpk[hh][j * 8 + i];
-  float m[4], l[4], o[4][16];
+    for (int i = 0; i < 4; ++i)
 #pragma unroll
-  for (int hh = 0; hh < 4; ++hh) {
-    m[hh] = -3.402823466e38f;
-    l[hh] = 0.0f;
-#pragma unroll
-    for (int d = 0; d < 16; ++d) o[hh][d] = 0.0f;
-  }
-  for (; p0 < end; p0 += 32) {
-    kv_load(kb, vb, p0 + 32, end, nxt);
-    const bool ok1 = p0 + 1 < end;
-    const u32x4 ka0 = cur.k0[0], ka1 = cur.k0[1], kb0 = cur.k1[0], kb1 = cur.k1[1];
-    const u32x4 va0 = cur.v0[0], va1 = cur.v0[1], vb0 = cur.v1[0], vb1 = cur.v1[1];
-    float s0[4], s1[4];
-#pragma unroll
-    for (int hh = 0; hh < 4; ++hh) {
-      float x0 = 0.0f, x1 = 0.0f;
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        x0 = dot2(ka0[i], q[hh][i], x0);
-        x1 = dot2(kb0[i], q[hh][i], x1);
-      }
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        x0 = dot2(ka1[i], q[hh][4 + i], x0);
-        x1 = dot2(kb1[i], q[hh][4 + i], x1);
-      }
-      s0[hh] = tree16(x0);
-      s1[hh] = ok1 ? tree16(x1) : -INFINITY;
-    }
-    float vf0[16], vf1[16];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      vf0[2 * i] = bf_lo(va0[i]); vf0[2 * i + 1] = bf_hi(va0[i]);
-      vf0[8 + 2 * i] = bf_lo(va1[i]); vf0[8 + 2 * i + 1] = bf_hi(va1[i]);
-      vf1[2 * i] = bf_lo(vb0[i]); vf1[2 * i + 1] = bf_hi(vb0[i]);
-      vf1[8 + 2 * i] = bf_lo(vb1[i]); vf1[8 + 2 * i + 1] = bf_hi(vb1[i]);
-    }
-#pragma unroll
-    for (int hh = 0; hh < 4; ++hh) {
-      const float mn = fmaxf(m[hh], fmaxf(s0[hh], s1[hh]));
-      const float f = exp2f((m[hh] - mn) * kLog2e);
-      const float e0 = exp2f((s0[hh] - mn) * kLog2e);
-      const float e1 = exp2f((s1[hh] - mn) * kLog2e);
-      m[hh] = mn;
-      l[hh] = l[hh] * f + e0 + e1;
-#pragma unroll
-      for (int d = 0; d < 16; ++d) o[hh][d] = fmaf(e1, vf1[d], fmaf(e0, vf0[d], o[hh][d] * f));
-    }
-    cur = nxt;
-  }
-  if (last && G == 0) {
-    // the new position, from LDS
-    float s0[4];
-#pragma unroll
-    for (int hh = 0; hh < 4; ++hh) {
-      float x0 = 0.0f;
-#pragma unroll
-      for (int i = 0; i < 8; ++i) x0 = dot2(kvnew[0][j * 8 + i], q[hh][i], x0);
-      s0[hh] = tree16(x0);
-    }
-    float vf0[16];
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      vf0[2 * i] = bf_lo(kvnew[1][j * 8 + i]);
-      vf0[2 * i + 1] = bf_hi(kvnew[1][j * 8 + i]);
-    }
-#pragma unroll
-    for (int hh = 0; hh < 4; ++hh) {
-      const float mn = fmaxf(m[hh], s0[hh]);
-      const float f = exp2f((m[hh] - mn) * kLog2e);
-      const float e0 = exp2f((s0[hh] - mn) * kLog2e);
-      m[hh] = mn;
-      l[hh] = l[hh] * f + e0;
-#pragma unroll
-      for (int d = 0; d < 16; ++d) o[hh][d] = fmaf(e0, vf0[d], o[hh][d] * f);
-    }
-  }
+      for (int j = 0; j < 8; ++j) q[hh][i][j] = qs[hh][64 * i + 8 * m + j];
 
-  // ---- merge the 16 row-states of the block ----
-  if (j == 0) {
+  float* sc = a.scores + (size_t)(4 * g + (m & 3)) * a.capacity;
+  for (; p - grp < end; p += 32) {
+    const int pn = p + 32;
+    if (pn < end && pn != pos) {
+      const u32x4* r = reinterpret_cast<const u32x4*>(kb + (size_t)pn * 256);
 #pragma unroll
-    for (int hh = 0; hh < 4; ++hh) mx[G][hh] = m[hh];
-  }
-  __syncthreads();
-  float M[4];
-#pragma unroll
-  for (int hh = 0; hh < 4; ++hh) {
-    float mm = mx[0][hh];
-#pragma unroll
-    for (int r = 1; r < 16; ++r) mm = fmaxf(mm, mx[r][hh]);
-    M[hh] = mm;
-    const float f = exp2f((m[hh] - mm) * kLog2e);
-    l[hh] *= f;
-#pragma unroll
-    for (int d = 0; d < 16; ++d) o[hh][d] *= f;
-  }
-  // sum the four rows of the wave
-#pragma unroll
-  for (int hh = 0; hh < 4; ++hh) {
-    l[hh] += __shfl_xor(l[hh], 16, 64);
-    l[hh] += __shfl_xor(l[hh], 32, 64);
-#pragma unroll
-    for (int d = 0; d < 16; ++d) {
-      o[hh][d] += __shfl_xor(o[hh][d], 16, 64);
-      o[hh][d] += __shfl_xor(o[hh][d], 32, 64);
+      for (int i = 0; i < 4; ++i) kn[i] = r[8 * i];
     }
+    if (p == pos) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) kc[i] = knew[m + 8 * i];
+    }
+    float s[4];
+#pragma unroll
+    for (int hh = 0; hh < 4; ++hh) {
+      const float p0 = chunk_dot(q[hh][0], kc[0]);
+      const float p1 = chunk_dot(q[hh][1], kc[1]);
+      const float p2 = chunk_dot(q[hh][2], kc[2]);
+      const float p3 = chunk_dot(q[hh][3], kc[3]);
+      s[hh] = tree8((p0 + p1) + (p2 + p3));
+    }
+    const int hm = m & 3;
+    const float mine = hm == 0 ? s[0] : hm == 1 ? s[1] : hm == 2 ? s[2] : s[3];
+    if (p < end && m < 4) sc[p] = mine;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) kc[i] = kn[i];
   }
-  if (grp == 0) {
+}
+
+// ---- per-chain online softmax ----
+
+constexpr int kTile = 64;
+
+template <int CTRL, int ROWS>
+__device__ __forceinline__ float dpp_src(float x, float old) {
+  return __builtin_amdgcn_update_dpp(old, x, CTRL, ROWS, 0xf, false);
+}
+
+// Inclusive max scan over the 64 lanes (GFX9 row_shr and row_bcast DPP).
+__device__ __forceinline__ float wave_max_scan(float x) {
+  const float ninf = -__builtin_inff();
+  x = fmaxf(x, dpp_src<0x111, 0xf>(x, ninf));  // row_shr:1
+  x = fmaxf(x, dpp_src<0x112, 0xf>(x, ninf));  // row_shr:2
+  x = fmaxf(x, dpp_src<0x114, 0xf>(x, ninf));  // row_shr:4
+  x = fmaxf(x, dpp_src<0x118, 0xf>(x, ninf));  // row_shr:8
+  x = fmaxf(x, dpp_src<0x142, 0xa>(x, ninf));  // row_bcast:15 into rows 1, 3
+  x = fmaxf(x, dpp_src<0x143, 0xc>(x, ninf));  // row_bcast:31 into rows 2, 3
+  return x;
+}
+
+__device__ __forceinline__ float readlane63(float x) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, x), 63));
+}
+
+// Exp scores and factors of one tile for both heads of the block.
+struct ChainTile {
+  float e[2][kTile];
+  float f[2][kTile];
+  int slow;  // some factor of the tile differs from 1
+};
+
+// Raw bf16 V values of one tile through a buffer resource based at the
+// chain's first row: the row offset is a scalar, the lane's dim the vector
+// offset, so no address arithmetic runs per load. Rows past the chain's end
+// re-read its last row (in bounds; their e is 0), so the loads carry no
+// branches and all 64 stay in flight until their first use. Requires L >= 1.
+__device__ __forceinline__ void load_tile(__amdgpu_buffer_rsrc_t vb, uint32_t voff,
+                                          uint32_t row_bytes, int j0, int L, uint32_t* v) {
 #pragma unroll
-    for (int hh = 0; hh < 4; ++hh)
+  for (int s = 0; s < kTile; ++s)
+    v[s] = __builtin_amdgcn_raw_buffer_load_b16(vb, voff, (uint32_t)min(j0 + s, L - 1) * row_bytes, 0);
+}
+
+__device__ __forceinline__ float v_f32(uint32_t raw) { return __builtin_bit_cast(float, raw << 16); }
+
+// One tile of 64 steps for the dim owned by this thread; WS selects the head
+// whose sum this wave keeps. Steps past the chain's end have e = 0 and f = 1
+// and change nothing (o is never -0, v is finite).
+template <bool SLOW, int WS>
+__device__ __forceinline__ void chain_tile(const ChainTile& T, const uint32_t* raw, float& o0,
+                                           float& o1, float& sum) {
 #pragma unroll
-      for (int d = 0; d < 16; ++d) osum[wave][hh][j * 16 + d] = o[hh][d];
-    if (j == 0)
-#pragma unroll
-      for (int hh = 0; hh < 4; ++hh) lsum[wave][hh] = l[hh];
-  }
-  __syncthreads();
-  {
-    const int hh = t >> 6, d0 = (t & 63) * 4;
-    const int head = 4 * g + hh;
-    float4 acc;
-    acc.x = osum[0][hh][d0] + osum[1][hh][d0] + osum[2][hh][d0] + osum[3][hh][d0];
-    acc.y = osum[0][hh][d0 + 1] + osum[1][hh][d0 + 1] + osum[2][hh][d0 + 1] + osum[3][hh][d0 + 1];
-    acc.z = osum[0][hh][d0 + 2] + osum[1][hh][d0 + 2] + osum[2][hh][d0 + 2] + osum[3][hh][d0 + 2];
-    acc.w = osum[0][hh][d0 + 3] + osum[1][hh][d0 + 3] + osum[2][hh][d0 + 3] + osum[3][hh][d0 + 3];
-    *reinterpret_cast<float4*>(a.part_o + ((size_t)head * S + split) * 256 + d0) = acc;
-    if ((t & 63) == 0) {
-      const float L = lsum[0][hh] + lsum[1][hh] + lsum[2][hh] + lsum[3][hh];
-      *reinterpret_cast<float2*>(a.part_ml + ((size_t)head * S + split) * 2) = make_float2(M[hh], L);
+  for (int s = 0; s < kTile; ++s) {
+    const float e0 = T.e[0][s], e1 = T.e[1][s];
+    const float v = v_f32(raw[s]);
+    const float es = WS ? e1 : e0;
+    if (SLOW) {
+      o0 = fmaf(e0, v, o0 * T.f[0][s]);
+      o1 = fmaf(e1, v, o1 * T.f[1][s]);
+      sum = sum * T.f[WS][s] + es;
+    } else {
+      o0 = fmaf(e0, v, o0);
+      o1 = fmaf(e1, v, o1);
+      sum = sum + es;
     }
   }
 }
 
-// Grid (8 heads, 8 chunks of 32 dims). Every block recomputes the head's
-// (max, sum) over the splits; thread t then sums splits t/8, t/8+32, ... for
-// four dims with independent float4 loads, and 32 partial sums per dim are
-// combined in a fixed order.
-__global__ __launch_bounds__(256) void k_attn_merge(AttnArgs a) {
-  __shared__ float scale[kMaxSplits];
-  __shared__ float4 red[32][8];
-  __shared__ float wred[4];
+template <int WS>
+__device__ __forceinline__ void run_tile(const ChainTile& T, const uint32_t* v, float& o0, float& o1,
+                                         float& sum) {
+  if (T.slow)
+    chain_tile<true, WS>(T, v, o0, o1, sum);
+  else
+    chain_tile<false, WS>(T, v, o0, o1, sum);
+}
+
+template <int WS>
+__device__ __forceinline__ void dims_loop(const ChainTile* tiles, __amdgpu_buffer_rsrc_t vb,
+                                          uint32_t voff, uint32_t stride, int L, float& o0,
+                                          float& o1, float& sum) {
+  if (L == 0) return;
+  uint32_t va[kTile], vn[kTile];
+  load_tile(vb, voff, stride, 0, L, va);
+  for (int j0 = 0, k = 0; j0 < L; j0 += 2 * kTile, k += 2) {
+    load_tile(vb, voff, stride, j0 + kTile, L, vn);
+    __syncthreads();
+    run_tile<WS>(tiles[k & 1], va, o0, o1, sum);
+    if (j0 + kTile >= L) break;
+    load_tile(vb, voff, stride, j0 + 2 * kTile, L, va);
+    __syncthreads();
+    run_tile<WS>(tiles[(k + 1) & 1], vn, o0, o1, sum);
+  }
+}
+
+__global__ __launch_bounds__(320, 1) void k_attn_chain(AttnArgs a) {
+  __shared__ ChainTile tiles[2];
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
-  const int h = blockIdx.x, chunk = blockIdx.y, S = a.splits;
-  const float* ml = a.part_ml + (size_t)h * S * 2;
-  float mloc = -3.402823466e38f;
-  for (int s = t; s < S; s += 256) mloc = fmaxf(mloc, ml[2 * s]);
-  mloc = wave_max(mloc);
-  if (lane == 0) wred[wave] = mloc;
-  __syncthreads();
-  const float M = fmaxf(fmaxf(wred[0], wred[1]), fmaxf(wred[2], wred[3]));
-  __syncthreads();
-  float lloc = 0.0f;
-  for (int s = t; s < S; s += 256) {
-    const float f = exp2f((ml[2 * s] - M) * kLog2e);
-    scale[s] = f;
-    lloc += f * ml[2 * s + 1];
-  }
-  lloc = tree64(lloc);
-  if (lane == 0) wred[wave] = lloc;
-  __syncthreads();
-  const float L = (wred[0] + wred[1]) + (wred[2] + wred[3]);
-  const int quad = t & 7, sub = t >> 3;  // 8 quads of 4 dims, 32 split subsets
-  const int d0 = chunk * 32 + quad * 4;
-  const float* po = a.part_o + (size_t)h * S * 256 + d0;
-  float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
-#pragma unroll 8
-  for (int s = sub; s < S; s += 32) {
-    const float4 v = *reinterpret_cast<const float4*>(po + (size_t)s * 256);
-    const float f = scale[s];
-    acc.x = fmaf(f, v.x, acc.x);
-    acc.y = fmaf(f, v.y, acc.y);
-    acc.z = fmaf(f, v.z, acc.z);
-    acc.w = fmaf(f, v.w, acc.w);
-  }
-  red[sub][quad] = acc;
-  __syncthreads();
-  if (t < 32) {
-    const int q = t >> 2, e = t & 3;
-    float o = 0.0f;
-    for (int r = 0; r < 32; ++r) {
-      const float4 v = red[r][q];
-      o += e == 0 ? v.x : e == 1 ? v.y : e == 2 ? v.z : v.w;
+  const int bx = blockIdx.x;
+  const int hp = (bx >> 3) & 1, rest = (bx & 7) | ((bx >> 4) << 3);
+  const int kvh = rest >> 6, c = rest & 63;
+  const int pos = load_pos(a.st, a.pos_val);
+  const int n = pos + 1;
+  const int C = n < kAttnRouteSplit ? 32 : 64;
+  if (c >= C) return;
+  const int L = n > c ? (n - 1 - c) / C + 1 : 0;
+  const int h0 = 4 * kvh + 2 * hp;
+
+  if (wave == 4) {
+    // Lane = step within a tile, both heads; one tile ahead of the dim waves.
+    const float* sc0 = a.scores + (size_t)h0 * a.capacity + c;
+    const float* sc1 = sc0 + a.capacity;
+    const float ninf = -__builtin_inff();
+    float m0 = kFiniteMin, m1 = kFiniteMin;
+    float s0 = lane < L ? sc0[(size_t)lane * C] : ninf;
+    float s1 = lane < L ? sc1[(size_t)lane * C] : ninf;
+    for (int j0 = 0, k = 0; j0 < L; j0 += kTile, ++k) {
+      const int jn = j0 + kTile + lane;
+      const float s0n = jn < L ? sc0[(size_t)jn * C] : ninf;
+      const float s1n = jn < L ? sc1[(size_t)jn * C] : ninf;
+      const float mt0 = fmaxf(m0, wave_max_scan(s0));
+      const float mt1 = fmaxf(m1, wave_max_scan(s1));
+      const float pv0 = dpp_src<0x138, 0xf>(mt0, m0);  // wave_shr:1, lane 0 <- carry
+      const float pv1 = dpp_src<0x138, 0xf>(mt1, m1);
+      const float f0 = es_exp(pv0 - mt0), e0 = es_exp(s0 - mt0);
+      const float f1 = es_exp(pv1 - mt1), e1 = es_exp(s1 - mt1);
+      ChainTile& T = tiles[k & 1];
+      T.e[0][lane] = e0;
+      T.e[1][lane] = e1;
+      T.f[0][lane] = f0;
+      T.f[1][lane] = f1;
+      const bool slow = __any(f0 != 1.0f || f1 != 1.0f);
+      if (lane == 0) T.slow = slow;
+      m0 = readlane63(mt0);
+      m1 = readlane63(mt1);
+      s0 = s0n;
+      s1 = s1n;
+      __syncthreads();
     }
-    o = L == 0.0f ? o : o / L;
-    const int d = chunk * 32 + t;
-    const float attention = rbf(o);
-    const float gate = sigmoid_bf(bf2f(a.q_proj[h * 512 + 256 + d]));
-    a.gated[h * 256 + d] = (uint16_t)f2bf(attention * gate);
+    if (lane == 0) {
+      a.part_ml[((size_t)h0 * kAttnMaxChains + c) * 2] = m0;
+      a.part_ml[((size_t)(h0 + 1) * kAttnMaxChains + c) * 2] = m1;
+    }
+    return;
   }
+
+  // Buffer over this KV head's rows from the chain's first row to the end.
+  const __amdgpu_buffer_rsrc_t vb = __builtin_amdgcn_make_buffer_rsrc(
+      a.vcache + ((size_t)kvh * a.capacity + c) * 256, 0, (a.capacity - c) * 512, 0x00020000);
+  const uint32_t stride = (uint32_t)C * 512;
+  float o0 = 0.0f, o1 = 0.0f, sum = 0.0f;
+  if (wave & 1)
+    dims_loop<1>(tiles, vb, (uint32_t)t * 2, stride, L, o0, o1, sum);
+  else
+    dims_loop<0>(tiles, vb, (uint32_t)t * 2, stride, L, o0, o1, sum);
+  a.part_o[((size_t)h0 * kAttnMaxChains + c) * 256 + t] = o0;
+  a.part_o[((size_t)(h0 + 1) * kAttnMaxChains + c) * 256 + t] = o1;
+  if (wave < 2 && lane == 0)
+    a.part_ml[((size_t)(h0 + wave) * kAttnMaxChains + c) * 2 + 1] = sum;
+}
+
+// ---- merge + gate ----
+
+// Pairwise sum of 32 values in index order.
+__device__ __forceinline__ float tree_reg32(float* v) {
+#pragma unroll
+  for (int off = 1; off < 32; off *= 2)
+#pragma unroll
+    for (int i = 0; i + off < 32; i += 2 * off) v[i] = v[i] + v[i + off];
+  return v[0];
+}
+
+__global__ __launch_bounds__(64) void k_attn_merge(AttnArgs a) {
+  __shared__ float fac[kAttnMaxChains];
+  __shared__ float total;
+  const int lane = threadIdx.x, h = blockIdx.x;
+  const int d = blockIdx.y * 64 + lane;
+  const int pos = load_pos(a.st, a.pos_val);
+  const bool two_pass = pos + 1 >= kAttnRouteSplit;
+  const float* ml = a.part_ml + (size_t)h * kAttnMaxChains * 2;
+  const float* po = a.part_o + (size_t)h * kAttnMaxChains * 256 + d;
+  float v[kAttnMaxChains];
+  // Chain outputs first: independent loads in flight while the factors form.
+#pragma unroll
+  for (int c = 0; c < 32; ++c) v[c] = po[(size_t)c * 256];
+  if (two_pass) {
+#pragma unroll
+    for (int c = 32; c < 64; ++c) v[c] = po[(size_t)c * 256];
+    const float mx = ml[2 * lane];
+    const float F = es_exp(mx - wave_max(mx));
+    fac[lane] = F;
+    // lane l < 32: (0 + F_l s_l) + F_{l+32} s_{l+32}, then pairwise over lanes
+    // (attention_decode.metal:858-862).
+    const float prod = F * ml[2 * lane + 1];
+    const float hi = __shfl_down(prod, 32, 64);
+    float s = 0.0f;
+    s = s + prod;
+    s = s + hi;
+    s = tree32(s);
+    if (lane == 0) total = s;
+  } else {
+    const float mx = lane < 32 ? ml[2 * lane] : kFiniteMin;
+    const float F = es_exp(mx - wave_max(mx));
+    if (lane < 32) fac[lane] = F;
+    const float s = tree32(ml[2 * (lane & 31) + 1] * F);
+    if (lane == 0) total = s;
+  }
+  __syncthreads();
+  const float sum = total;
+  float o;
+  if (two_pass) {
+    float w[32];
+#pragma unroll
+    for (int l = 0; l < 32; ++l) {
+      float acc = 0.0f;
+      acc = acc + fac[l] * rbf(v[l]);
+      acc = acc + fac[l + 32] * rbf(v[l + 32]);
+      w[l] = acc;
+    }
+    o = tree_reg32(w);
+  } else {
+#pragma unroll
+    for (int l = 0; l < 32; ++l) v[l] = v[l] * fac[l];
+    o = tree_reg32(v);
+  }
+  o = sum == 0.0f ? o : o / sum;
+  const float attention = rbf(o);
+  const float gate = sigmoid_bf(bf2f(a.q_proj[h * 512 + 256 + d]));
+  a.gated[h * 256 + d] = (uint16_t)f2bf(attention * gate);
 }
 
 bool attn_ok(const AttnArgs& a) {
   return a.q_proj && a.k_proj && a.v_proj && a.q_gain && a.k_gain && a.kcache && a.vcache &&
-         a.inv_freq && a.part_o && a.part_ml && a.gated && a.splits >= 1 &&
-         a.splits <= kMaxSplits && a.capacity > 0 && (a.st || (a.pos_val >= 0 && a.pos_val < a.capacity));
+         a.inv_freq && a.part_o && a.part_ml && a.scores && a.gated && a.blocks >= 1 &&
+         a.blocks <= 1024 && a.capacity > 0 &&
+         (a.st || (a.pos_val >= 0 && a.pos_val < a.capacity));
 }
 
 }  // namespace
 
-size_t attn_scratch_bytes(int splits) { return (size_t)8 * splits * (256 + 2) * sizeof(float); }
+size_t attn_scratch_bytes(int capacity) {
+  return ((size_t)kQHeads * kAttnMaxChains * (256 + 2) + (size_t)kQHeads * capacity) *
+         sizeof(float);
+}
 
-hipError_t launch_attn_split(const AttnArgs& a, hipStream_t s) {
+void attn_bind_scratch(AttnArgs& a, void* scratch) {
+  a.part_o = static_cast<float*>(scratch);
+  a.part_ml = a.part_o + (size_t)kQHeads * kAttnMaxChains * 256;
+  a.scores = a.part_ml + (size_t)kQHeads * kAttnMaxChains * 2;
+}
+
+hipError_t launch_attn_scores(const AttnArgs& a, hipStream_t s) {
   if (!attn_ok(a)) return hipErrorInvalidValue;
-  hipLaunchKernelGGL(k_attn_split, dim3(a.splits, kKvHeads), dim3(256), 0, s, a);
+  hipLaunchKernelGGL(k_attn_scores, dim3(a.blocks, kKvHeads), dim3(256), 0, s, a);
+  return hipGetLastError();
+}
+
+hipError_t launch_attn_chain(const AttnArgs& a, hipStream_t s) {
+  if (!attn_ok(a)) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(k_attn_chain, dim3(kKvHeads * kAttnMaxChains * 2), dim3(320), 0, s, a);
   return hipGetLastError();
 }
 
 hipError_t launch_attn_merge(const AttnArgs& a, hipStream_t s) {
   if (!attn_ok(a)) return hipErrorInvalidValue;
-  hipLaunchKernelGGL(k_attn_merge, dim3(kQHeads, 8), dim3(256), 0, s, a);
+  hipLaunchKernelGGL(k_attn_merge, dim3(kQHeads, 4), dim3(64), 0, s, a);
   return hipGetLastError();
 }
 

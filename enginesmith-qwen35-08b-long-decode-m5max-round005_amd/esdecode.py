@@ -85,7 +85,7 @@ _SIGNATURES = {
     "es_engine_set_position": (c_int, [c_void_p, c_int, c_uint32]),
     "es_engine_fill_synthetic": (c_int, [c_void_p, c_int, c_uint64, c_uint32]),
     "es_engine_time_decode": (c_int, [c_void_p, c_int, c_int, POINTER(c_double)]),
-    "es_engine_time_attention": (c_int, [c_void_p, c_int, c_int, POINTER(c_double)]),
+    "es_engine_time_attention": (c_int, [c_void_p, c_int, c_int, c_int, POINTER(c_double)]),
     "es_engine_time_head": (c_int, [c_void_p, c_int, POINTER(c_double)]),
     "es_engine_splits_for": (c_int, [c_int]),
 }
@@ -313,9 +313,12 @@ class Engine:
         check(lib().es_engine_time_decode(self.h, steps, warmup, ctypes.byref(ms)))
         return ms.value
 
-    def time_attention(self, layer: int, reps: int) -> float:
+    ATTN_PARTS = {"all": 0, "scores": 1, "chains": 2, "merge": 3}
+
+    def time_attention(self, layer: int, reps: int, part: str = "all") -> float:
+        """Average ms of one attention layer's launches (or of one of them)."""
         ms = c_double()
-        check(lib().es_engine_time_attention(self.h, layer, reps, ctypes.byref(ms)))
+        check(lib().es_engine_time_attention(self.h, layer, reps, self.ATTN_PARTS[part], ctypes.byref(ms)))
         return ms.value
 
     def time_head(self, reps: int) -> float:

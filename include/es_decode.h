@@ -134,21 +134,26 @@ int es_gdn_gate_out_proj(const es_q4* out_proj, const uint16_t* y, const uint16_
  * host; the attention op reads them from a device copy. */
 int es_rope_inv_freq(float* host_out32);
 
-/* Scratch bytes es_attn_decode needs for `splits` KV splits (1..1024). */
-size_t es_attn_scratch_bytes(int splits);
+/* Scratch bytes es_attn_decode needs for a cache of `capacity` rows. Layout
+ * (fp32): chain outputs [8,64,256], chain (max, sum) [8,64,2], scores
+ * [8,capacity]. */
+size_t es_attn_scratch_bytes(int capacity);
 
 /* attn_prepare_qkv_decode (attention.metal:262-313) + decode attention with
- * the output gate: attn_decode/attn_gate for short contexts and
- * attn_decode_split1 + attn_decode_split2_gate for long ones
- * (attention_decode.metal:51-431, 830-891; model.rs:318-347), as one split-K
- * flash decode. q_proj [8,512] (query|gate), k_proj/v_proj [2,256]; writes
- * K/V row `position` of kcache/vcache [2, capacity, 256] and
+ * the output gate, following the reference's routes (model.rs:318-347):
+ * attn_decode + attn_gate (32 position chains, fp32 combine) below 1024
+ * attended positions, attn_decode_split1 + attn_decode_split2_gate (64
+ * chains, bf16 partials) from 1024 on (attention_decode.metal:51-431,
+ * 830-891). q_proj [8,512] (query|gate), k_proj/v_proj [2,256]; writes K/V
+ * row `position` of kcache/vcache [2, capacity, 256] and
  * gated [8,256] = bf16(bf16(attn) * sigmoid_bf(gate)). Attends to positions
- * 0..position. query_out (optional) receives the roped queries [8,256]. */
+ * 0..position. `blocks` (1..1024) is the score launch's blocks per KV head,
+ * a work split that changes no result. query_out (optional) receives the
+ * roped queries [8,256]. */
 int es_attn_decode(const uint16_t* q_proj, const uint16_t* k_proj, const uint16_t* v_proj,
                    const uint16_t* q_gain, const uint16_t* k_gain, uint16_t* kcache,
                    uint16_t* vcache, int capacity, int position, const float* inv_freq,
-                   int splits, void* scratch, size_t scratch_bytes, uint16_t* gated,
+                   int blocks, void* scratch, size_t scratch_bytes, uint16_t* gated,
                    uint16_t* query_out, void* stream);
 
 /* ------------------------------------------------------------------ */
@@ -224,9 +229,10 @@ int es_engine_fill_synthetic(es_engine* e, int length, uint64_t seed, uint32_t p
 
 /* Timing with HIP events on the engine stream. */
 int es_engine_time_decode(es_engine* e, int steps, int warmup, double* ms_total);
-int es_engine_time_attention(es_engine* e, int layer, int reps, double* ms_avg);
+/* which: 0 = all three attention launches, 1 = scores, 2 = chains, 3 = merge */
+int es_engine_time_attention(es_engine* e, int layer, int reps, int which, double* ms_avg);
 int es_engine_time_head(es_engine* e, int reps, double* ms_avg);
-/* KV splits the engine uses at attention length `length`. */
+/* Score blocks per KV head the engine uses at attention length `length`. */
 int es_engine_splits_for(int length);
 
 #ifdef __cplusplus

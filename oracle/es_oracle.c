@@ -445,19 +445,38 @@ void eo_attn_prepare(const uint16_t* q_proj, const uint16_t* k, const uint16_t* 
   }
 }
 
-static float lane_score(const float* q, const uint16_t* krow, int lane) {
-  float score = 0.0f;
-  for (int j = 0; j < 8; ++j) score += q[lane * 8 + j] * F(krow[lane * 8 + j]);
-  return score;
+/* One score, attention_decode.metal:137-144 / 321-326 (q . k with q = k-scale
+ * 1/16 times the bf16 query). Fixed order: partial l (0..31) covers dims
+ * 8l..8l+7 as an fma chain; lane m (0..7) adds its partials as
+ * (p[m] + p[m+8]) + (p[m+16] + p[m+24]); the 8 lane values are added
+ * pairwise in lane order. */
+static float score_row(const float* q, const uint16_t* krow) {
+  float p[32], a[8];
+  for (int l = 0; l < 32; ++l) {
+    float s = 0.0f;
+    for (int j = 0; j < 8; ++j) s = fmaf(q[8 * l + j], F(krow[8 * l + j]), s);
+    p[l] = s;
+  }
+  for (int m = 0; m < 8; ++m) a[m] = (p[m] + p[m + 8]) + (p[m + 16] + p[m + 24]);
+  return tree(a, 8);
 }
 
-static float simd_score(const float* q, const uint16_t* krow) {
-  float lanes[32];
-  for (int l = 0; l < 32; ++l) lanes[l] = lane_score(q, krow, l);
-  return tree(lanes, 32);
+/* One online-softmax update of a position chain (attention_decode.metal:146-157,
+ * 328-338): new max, factor and exp score, then sum = sum*factor + e and
+ * o = fma(e, v, o*factor). */
+static void chain_step(float score, const uint16_t* vrow, float* max_score, float* sum_exp,
+                       float* o) {
+  float new_max = fmaxf(*max_score, score);
+  float factor = eo_exp(*max_score - new_max);
+  float es = eo_exp(score - new_max);
+  *max_score = new_max;
+  *sum_exp = *sum_exp * factor + es;
+  for (int d = 0; d < 256; ++d) o[d] = fmaf(es, F(vrow[d]), o[d] * factor);
 }
 
-/* sdpa_vector<bf16,256>, attention_decode.metal:51-213 (32 simdgroups) */
+/* sdpa_vector<bf16,256>, attention_decode.metal:51-213: chain sg (0..31) takes
+ * positions sg, sg+32, ... in order; chains are combined with factors
+ * exp(max_sg - max), sums and outputs added pairwise over the 32 chains. */
 void eo_attn_decode_single(const uint16_t* query, const uint16_t* kcache, const uint16_t* vcache,
                            int length, int capacity, uint16_t* out) {
   const float finite_min = -FLT_MAX;
@@ -473,15 +492,9 @@ void eo_attn_decode_single(const uint16_t* query, const uint16_t* kcache, const 
     for (int sg = 0; sg < 32; ++sg) {
       float max_score = finite_min, sum_exp = 0.0f;
       for (int d = 0; d < 256; ++d) o[sg][d] = 0.0f;
-      for (int i = sg; i < length; i += 32) {
-        float score = simd_score(q, kb + (size_t)i * 256);
-        float new_max = fmaxf(max_score, score);
-        float factor = eo_exp(max_score - new_max);
-        float es = eo_exp(score - new_max);
-        max_score = new_max;
-        sum_exp = sum_exp * factor + es;
-        for (int d = 0; d < 256; ++d) o[sg][d] = o[sg][d] * factor + es * F(vb[(size_t)i * 256 + d]);
-      }
+      for (int i = sg; i < length; i += 32)
+        chain_step(score_row(q, kb + (size_t)i * 256), vb + (size_t)i * 256, &max_score,
+                   &sum_exp, o[sg]);
       mx[sg] = max_score;
       sm[sg] = sum_exp;
     }
@@ -519,15 +532,9 @@ void eo_attn_decode_split(const uint16_t* query, const uint16_t* kcache, const u
     const uint16_t* kb = kcache + (size_t)kvh * capacity * 256;
     const uint16_t* vb = vcache + (size_t)kvh * capacity * 256;
     float max_score = finite_min, sum_exp = 0.0f;
-    for (int i = blk; i < length; i += 64) {
-      float score = simd_score(q, kb + (size_t)i * 256);
-      float new_max = fmaxf(max_score, score);
-      float factor = eo_exp(max_score - new_max);
-      float es = eo_exp(score - new_max);
-      max_score = new_max;
-      sum_exp = sum_exp * factor + es;
-      for (int d = 0; d < 256; ++d) o[d] = o[d] * factor + es * F(vb[(size_t)i * 256 + d]);
-    }
+    for (int i = blk; i < length; i += 64)
+      chain_step(score_row(q, kb + (size_t)i * 256), vb + (size_t)i * 256, &max_score, &sum_exp,
+                 o);
     sums[h * 64 + blk] = sum_exp;
     maxs[h * 64 + blk] = max_score;
     for (int d = 0; d < 256; ++d) partials[((size_t)h * 64 + blk) * 256 + d] = eo_f32_to_bf16(o[d]);
