@@ -77,6 +77,14 @@ __device__ __forceinline__ float chunk_dot(const float* q, const u32x4& k) {
   return s;
 }
 
+// Row stride of the score array: j-slots per chain, for the 32-chain route,
+// rounded up to whole 64-step tiles.
+__host__ __device__ __forceinline__ int score_stride(int capacity) {
+  return (((capacity + 31) / 32) + 63) & ~63;
+}
+
+__device__ __forceinline__ int route_chains(int n) { return n < kAttnRouteSplit ? 32 : 64; }
+
 __global__ __launch_bounds__(256, 2) void k_attn_scores(AttnArgs a) {
   __shared__ float nrm[5][256];     // normalised q heads 0..3, new k
   __shared__ float qs[4][256];      // roped q * 1/16
@@ -86,22 +94,33 @@ __global__ __launch_bounds__(256, 2) void k_attn_scores(AttnArgs a) {
   const int g = blockIdx.y, B = gridDim.x;
   const int pos = load_pos(a.st, a.pos_val);
   const int n = pos + 1;
-  int chunk = (n + B - 1) / B;
-  chunk = (chunk + 31) & ~31;
-  const int start = blockIdx.x * chunk;
-  if (start >= n) return;
-  const int end = min(start + chunk, n);
-  const bool owner = end == n;  // this chunk holds the new position
-
+  const int C = route_chains(n);
+  // Work items (chain c, 8 steps from 8*j8): item i = j8*C + c covers
+  // positions c + C*(8*j8 + r), r = 0..7. Block b owns items [ib0, ib1).
+  const int jtot = (n + C - 1) / C;
+  const int items = C * ((jtot + 7) >> 3);
+  const int ipb = (items + B - 1) / B;
+  const int ib0 = blockIdx.x * ipb;
+  if (ib0 >= items) return;
+  const int ib1 = min(ib0 + ipb, items);
+  const int ipos = (pos / C >> 3) * C + pos % C;
+  const bool owner = ib0 <= ipos && ipos < ib1;  // holds the new position
   const int grp = lane >> 3, m = lane & 7;
   const uint16_t* kb = a.kcache + (size_t)g * a.capacity * 256 + 8 * m;
+  // Lane group grp takes step r = grp of the item; wave w takes items
+  // ib0 + w, ib0 + w + 4, ...
+  auto item_pos = [&](int i, int& p) {
+    p = i % C + C * (8 * (i / C) + grp);
+    return p < n;
+  };
   // First K rows, issued before the prologue so their latency overlaps it.
   u32x4 kc[4] = {}, kn[4] = {};
-  int p = start + wave * 8 + grp;
-  if (p < end && p != pos) {
+  int i = ib0 + wave, p;
+  bool ok = i < ib1 && item_pos(i, p);
+  if (ok && p != pos) {
     const u32x4* r = reinterpret_cast<const u32x4*>(kb + (size_t)p * 256);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) kc[i] = r[8 * i];
+    for (int x = 0; x < 4; ++x) kc[x] = r[8 * x];
   }
 
   // ---- prologue: q (and, in the owner block, the new k/v rows) ----
@@ -109,28 +128,28 @@ __global__ __launch_bounds__(256, 2) void k_attn_scores(AttnArgs a) {
     float o4[4];
     head_norm4(a.q_proj + (4 * g + wave) * 512, a.q_gain, lane, o4);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) nrm[wave][lane * 4 + i] = o4[i];
+    for (int x = 0; x < 4; ++x) nrm[wave][lane * 4 + x] = o4[x];
     if (owner && wave == 0) {
       head_norm4(a.k_proj + g * 256, a.k_gain, lane, o4);
 #pragma unroll
-      for (int i = 0; i < 4; ++i) nrm[4][lane * 4 + i] = o4[i];
+      for (int x = 0; x < 4; ++x) nrm[4][lane * 4 + x] = o4[x];
     }
   }
   __syncthreads();
   {
     float r[4];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) r[i] = rope_at(nrm[wave], lane * 4 + i, pos, a.inv_freq);
+    for (int x = 0; x < 4; ++x) r[x] = rope_at(nrm[wave], lane * 4 + x, pos, a.inv_freq);
     if (a.query_out && blockIdx.x == 0) {
       uint16_t* qo = a.query_out + (4 * g + wave) * 256 + lane * 4;
       *reinterpret_cast<uint2*>(qo) = make_uint2(pack_bf2(r[0], r[1]), pack_bf2(r[2], r[3]));
     }
 #pragma unroll
-    for (int i = 0; i < 4; ++i) qs[wave][lane * 4 + i] = r[i] * 0.0625f;
+    for (int x = 0; x < 4; ++x) qs[wave][lane * 4 + x] = r[x] * 0.0625f;
     if (owner && wave == 1) {
       float kr[4];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) kr[i] = rope_at(nrm[4], lane * 4 + i, pos, a.inv_freq);
+      for (int x = 0; x < 4; ++x) kr[x] = rope_at(nrm[4], lane * 4 + x, pos, a.inv_freq);
       const uint32_t k0 = pack_bf2(kr[0], kr[1]);
       const uint32_t k1 = pack_bf2(kr[2], kr[3]);
       uint32_t* kw = reinterpret_cast<uint32_t*>(knew);
@@ -149,21 +168,23 @@ __global__ __launch_bounds__(256, 2) void k_attn_scores(AttnArgs a) {
 #pragma unroll
   for (int hh = 0; hh < 4; ++hh)
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+    for (int x = 0; x < 4; ++x)
 #pragma unroll
-      for (int j = 0; j < 8; ++j) q[hh][i][j] = qs[hh][64 * i + 8 * m + j];
+      for (int j = 0; j < 8; ++j) q[hh][x][j] = qs[hh][64 * x + 8 * m + j];
 
-  float* sc = a.scores + (size_t)(4 * g + (m & 3)) * a.capacity;
-  for (; p - grp < end; p += 32) {
-    const int pn = p + 32;
-    if (pn < end && pn != pos) {
+  const int sstride = score_stride(a.capacity);
+  float* sc = a.scores + (size_t)(4 * g + (m & 3)) * kAttnMaxChains * sstride;
+  for (; i < ib1; i += 4) {
+    int pn;
+    const bool okn = i + 4 < ib1 && item_pos(i + 4, pn);
+    if (okn && pn != pos) {
       const u32x4* r = reinterpret_cast<const u32x4*>(kb + (size_t)pn * 256);
 #pragma unroll
-      for (int i = 0; i < 4; ++i) kn[i] = r[8 * i];
+      for (int x = 0; x < 4; ++x) kn[x] = r[8 * x];
     }
-    if (p == pos) {
+    if (ok && p == pos) {
 #pragma unroll
-      for (int i = 0; i < 4; ++i) kc[i] = knew[m + 8 * i];
+      for (int x = 0; x < 4; ++x) kc[x] = knew[m + 8 * x];
     }
     float s[4];
 #pragma unroll
@@ -176,15 +197,18 @@ __global__ __launch_bounds__(256, 2) void k_attn_scores(AttnArgs a) {
     }
     const int hm = m & 3;
     const float mine = hm == 0 ? s[0] : hm == 1 ? s[1] : hm == 2 ? s[2] : s[3];
-    if (p < end && m < 4) sc[p] = mine;
+    if (ok && m < 4) sc[(size_t)(p % C) * sstride + p / C] = mine;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) kc[i] = kn[i];
+    for (int x = 0; x < 4; ++x) kc[x] = kn[x];
+    ok = okn;
+    p = pn;
   }
 }
 
 // ---- per-chain online softmax ----
 
-constexpr int kTile = 64;
+constexpr int kTile = 64;    // chain steps per tile
+constexpr int kStages = 4;   // V tiles in LDS (3 in flight while one is used)
 
 template <int CTRL, int ROWS>
 __device__ __forceinline__ float dpp_src(float x, float old) {
@@ -207,141 +231,189 @@ __device__ __forceinline__ float readlane63(float x) {
   return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, x), 63));
 }
 
-// Exp scores and factors of one tile for both heads of the block.
-struct ChainTile {
-  float e[2][kTile];
-  float f[2][kTile];
-  int slow;  // some factor of the tile differs from 1
+struct __attribute__((aligned(16))) ChainSmem {
+  uint16_t v[kStages][kTile][256];  // V rows of a tile, as loaded
+  float s[kStages][2][kTile];       // scores of a tile, both heads
+  float e[2][2][kTile];             // [buffer][head][step] exp scores
+  float f[2][2][kTile];             // factors
+  int slow[2][2];                   // some factor of the tile differs from 1
 };
 
-// Raw bf16 V values of one tile through a buffer resource based at the
-// chain's first row: the row offset is a scalar, the lane's dim the vector
-// offset, so no address arithmetic runs per load. Rows past the chain's end
-// re-read its last row (in bounds; their e is 0), so the loads carry no
-// branches and all 64 stay in flight until their first use. Requires L >= 1.
-__device__ __forceinline__ void load_tile(__amdgpu_buffer_rsrc_t vb, uint32_t voff,
-                                          uint32_t row_bytes, int j0, int L, uint32_t* v) {
-#pragma unroll
-  for (int s = 0; s < kTile; ++s)
-    v[s] = __builtin_amdgcn_raw_buffer_load_b16(vb, voff, (uint32_t)min(j0 + s, L - 1) * row_bytes, 0);
+typedef __attribute__((address_space(3))) void* lds_ptr_t;
+
+// Barrier for LDS written by ds_write and by global->LDS DMA. The caller has
+// waited for its own DMA (vmcnt); lgkmcnt(0) covers ds_write. The empty asm
+// keeps the compiler from moving LDS accesses across the barrier.
+__device__ __forceinline__ void lds_barrier() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0), vmcnt and expcnt untouched
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
 }
 
-__device__ __forceinline__ float v_f32(uint32_t raw) { return __builtin_bit_cast(float, raw << 16); }
+// Wait until at most N vector-memory operations of this wave are pending
+// (gfx9 encoding: vmcnt[3:0] | expcnt 7 | lgkmcnt 15 | vmcnt[5:4] << 14).
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+  __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
+}
 
-// One tile of 64 steps for the dim owned by this thread; WS selects the head
-// whose sum this wave keeps. Steps past the chain's end have e = 0 and f = 1
-// and change nothing (o is never -0, v is finite).
-template <bool SLOW, int WS>
-__device__ __forceinline__ void chain_tile(const ChainTile& T, const uint32_t* raw, float& o0,
-                                           float& o1, float& sum) {
+// Issue this wave's share of tile T: 16 V rows (8 DMA of 1 KB: lanes 0..31
+// one row, 32..63 the next) and 32 floats of scores (8 lanes x 16 B). Steps
+// past the chain's end re-read its last row and are masked by e = 0.
+__device__ __forceinline__ void issue_tile(ChainSmem& sm, const uint16_t* vrow0, const float* sc0,
+                                           int sstride, int C, int L, int T, int wave, int lane) {
+  const int st = T % kStages;
 #pragma unroll
-  for (int s = 0; s < kTile; ++s) {
-    const float e0 = T.e[0][s], e1 = T.e[1][s];
-    const float v = v_f32(raw[s]);
-    const float es = WS ? e1 : e0;
+  for (int x = 0; x < 8; ++x) {
+    const int r = 16 * wave + 2 * x;
+    const int j = min(T * kTile + r + (lane >> 5), L - 1);
+    const uint16_t* g = vrow0 + (size_t)j * C * 256 + (lane & 31) * 8;
+    __builtin_amdgcn_global_load_lds(g, (lds_ptr_t)&sm.v[st][r][0], 16, 0, 0);
+  }
+  if (lane < 8) {
+    const int head = wave >> 1, part = wave & 1;
+    const float* g = sc0 + (size_t)head * kAttnMaxChains * sstride + T * kTile + part * 32 + lane * 4;
+    __builtin_amdgcn_global_load_lds(g, (lds_ptr_t)&sm.s[st][head][part * 32], 16, 0, 0);
+  }
+}
+
+// Exp scores and factors of tile T for one head from its staged scores.
+__device__ __forceinline__ void tile_exps(ChainSmem& sm, int T, int L, int head, int lane,
+                                          float& carry) {
+  const float ninf = -__builtin_inff();
+  const float s = T * kTile + lane < L ? sm.s[T % kStages][head][lane] : ninf;
+  const float mt = fmaxf(carry, wave_max_scan(s));
+  const float pv = dpp_src<0x138, 0xf>(mt, carry);  // wave_shr:1, lane 0 <- carry
+  const float f = es_exp(pv - mt), e = es_exp(s - mt);
+  sm.e[T & 1][head][lane] = e;
+  sm.f[T & 1][head][lane] = f;
+  const bool slow = __any(f != 1.0f);
+  if (lane == 0) sm.slow[T & 1][head] = slow;
+  carry = readlane63(mt);
+}
+
+// 64 steps of the dim owned by this thread for both heads; SUM waves also
+// keep head WS's sum. Steps past the chain's end have e = 0 and f = 1 and
+// change nothing (o is never -0, V rows are finite). Software-pipelined in
+// batches of 8 steps: the LDS reads of batch q+1 are issued before batch q
+// is computed, so one wave per SIMD hides the LDS latency.
+template <bool SLOW>
+struct Batch {
+  uint32_t v[8];
+  float4 e[2][2];
+  float4 f[SLOW ? 2 : 1][SLOW ? 2 : 1];
+};
+
+template <bool SLOW>
+__device__ __forceinline__ void load_batch(const ChainSmem& sm, int st, int b, int d, int q,
+                                           Batch<SLOW>& x) {
+#pragma unroll
+  for (int i = 0; i < 8; ++i) x.v[i] = sm.v[st][8 * q + i][d];
+#pragma unroll
+  for (int h = 0; h < 2; ++h)
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+      x.e[h][k] = reinterpret_cast<const float4*>(sm.e[b][h])[2 * q + k];
+      if (SLOW) x.f[h][k] = reinterpret_cast<const float4*>(sm.f[b][h])[2 * q + k];
+    }
+}
+
+__device__ __forceinline__ float lane4(const float4& v, int i) {
+  return i == 0 ? v.x : i == 1 ? v.y : i == 2 ? v.z : v.w;
+}
+
+template <bool SLOW, bool SUM, int WS>
+__device__ __forceinline__ void run_batch(const Batch<SLOW>& x, float& o0, float& o1, float& sum) {
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const float v = __builtin_bit_cast(float, x.v[i] << 16);
+    const float e0 = lane4(x.e[0][i >> 2], i & 3), e1 = lane4(x.e[1][i >> 2], i & 3);
     if (SLOW) {
-      o0 = fmaf(e0, v, o0 * T.f[0][s]);
-      o1 = fmaf(e1, v, o1 * T.f[1][s]);
-      sum = sum * T.f[WS][s] + es;
+      const float f0 = lane4(x.f[0][i >> 2], i & 3), f1 = lane4(x.f[1][i >> 2], i & 3);
+      o0 = fmaf(e0, v, o0 * f0);
+      o1 = fmaf(e1, v, o1 * f1);
+      if (SUM) sum = sum * (WS ? f1 : f0) + (WS ? e1 : e0);
     } else {
       o0 = fmaf(e0, v, o0);
       o1 = fmaf(e1, v, o1);
-      sum = sum + es;
+      if (SUM) sum = sum + (WS ? e1 : e0);
     }
   }
 }
 
-template <int WS>
-__device__ __forceinline__ void run_tile(const ChainTile& T, const uint32_t* v, float& o0, float& o1,
-                                         float& sum) {
-  if (T.slow)
-    chain_tile<true, WS>(T, v, o0, o1, sum);
-  else
-    chain_tile<false, WS>(T, v, o0, o1, sum);
-}
-
-template <int WS>
-__device__ __forceinline__ void dims_loop(const ChainTile* tiles, __amdgpu_buffer_rsrc_t vb,
-                                          uint32_t voff, uint32_t stride, int L, float& o0,
-                                          float& o1, float& sum) {
-  if (L == 0) return;
-  uint32_t va[kTile], vn[kTile];
-  load_tile(vb, voff, stride, 0, L, va);
-  for (int j0 = 0, k = 0; j0 < L; j0 += 2 * kTile, k += 2) {
-    load_tile(vb, voff, stride, j0 + kTile, L, vn);
-    __syncthreads();
-    run_tile<WS>(tiles[k & 1], va, o0, o1, sum);
-    if (j0 + kTile >= L) break;
-    load_tile(vb, voff, stride, j0 + 2 * kTile, L, va);
-    __syncthreads();
-    run_tile<WS>(tiles[(k + 1) & 1], vn, o0, o1, sum);
+template <bool SLOW, bool SUM, int WS>
+__device__ __forceinline__ void chain_steps(const ChainSmem& sm, int T, int d, float& o0,
+                                            float& o1, float& sum) {
+  const int st = T % kStages, b = T & 1;
+  Batch<SLOW> x[2];
+  load_batch<SLOW>(sm, st, b, d, 0, x[0]);
+#pragma unroll
+  for (int q = 0; q < kTile / 8; ++q) {
+    if (q + 1 < kTile / 8) load_batch<SLOW>(sm, st, b, d, q + 1, x[(q + 1) & 1]);
+    run_batch<SLOW, SUM, WS>(x[q & 1], o0, o1, sum);
   }
 }
 
-__global__ __launch_bounds__(320, 1) void k_attn_chain(AttnArgs a) {
-  __shared__ ChainTile tiles[2];
+template <bool SUM, int WS>
+__device__ __forceinline__ void run_tile(const ChainSmem& sm, int T, int d, float& o0, float& o1,
+                                         float& sum) {
+  if (sm.slow[T & 1][0] | sm.slow[T & 1][1])
+    chain_steps<true, SUM, WS>(sm, T, d, o0, o1, sum);
+  else
+    chain_steps<false, SUM, WS>(sm, T, d, o0, o1, sum);
+}
+
+// Block = (KV head, chain, query-head pair), 4 waves, thread = value dim.
+// Per tile T: wait for this wave's DMA of tiles up to T+1, barrier, issue
+// tile T+3 into the stage tile T-1 used, waves 2/3 form the exps of tile T+1
+// (heads 0/1), all waves run tile T. Waves 0/1 keep the sums of heads 0/1.
+__global__ __launch_bounds__(256, 1) void k_attn_chain(AttnArgs a) {
+  __shared__ ChainSmem sm;
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
   const int bx = blockIdx.x;
   const int hp = (bx >> 3) & 1, rest = (bx & 7) | ((bx >> 4) << 3);
   const int kvh = rest >> 6, c = rest & 63;
   const int pos = load_pos(a.st, a.pos_val);
   const int n = pos + 1;
-  const int C = n < kAttnRouteSplit ? 32 : 64;
+  const int C = route_chains(n);
   if (c >= C) return;
   const int L = n > c ? (n - 1 - c) / C + 1 : 0;
   const int h0 = 4 * kvh + 2 * hp;
-
-  if (wave == 4) {
-    // Lane = step within a tile, both heads; one tile ahead of the dim waves.
-    const float* sc0 = a.scores + (size_t)h0 * a.capacity + c;
-    const float* sc1 = sc0 + a.capacity;
-    const float ninf = -__builtin_inff();
-    float m0 = kFiniteMin, m1 = kFiniteMin;
-    float s0 = lane < L ? sc0[(size_t)lane * C] : ninf;
-    float s1 = lane < L ? sc1[(size_t)lane * C] : ninf;
-    for (int j0 = 0, k = 0; j0 < L; j0 += kTile, ++k) {
-      const int jn = j0 + kTile + lane;
-      const float s0n = jn < L ? sc0[(size_t)jn * C] : ninf;
-      const float s1n = jn < L ? sc1[(size_t)jn * C] : ninf;
-      const float mt0 = fmaxf(m0, wave_max_scan(s0));
-      const float mt1 = fmaxf(m1, wave_max_scan(s1));
-      const float pv0 = dpp_src<0x138, 0xf>(mt0, m0);  // wave_shr:1, lane 0 <- carry
-      const float pv1 = dpp_src<0x138, 0xf>(mt1, m1);
-      const float f0 = es_exp(pv0 - mt0), e0 = es_exp(s0 - mt0);
-      const float f1 = es_exp(pv1 - mt1), e1 = es_exp(s1 - mt1);
-      ChainTile& T = tiles[k & 1];
-      T.e[0][lane] = e0;
-      T.e[1][lane] = e1;
-      T.f[0][lane] = f0;
-      T.f[1][lane] = f1;
-      const bool slow = __any(f0 != 1.0f || f1 != 1.0f);
-      if (lane == 0) T.slow = slow;
-      m0 = readlane63(mt0);
-      m1 = readlane63(mt1);
-      s0 = s0n;
-      s1 = s1n;
-      __syncthreads();
-    }
-    if (lane == 0) {
-      a.part_ml[((size_t)h0 * kAttnMaxChains + c) * 2] = m0;
-      a.part_ml[((size_t)(h0 + 1) * kAttnMaxChains + c) * 2] = m1;
-    }
-    return;
-  }
-
-  // Buffer over this KV head's rows from the chain's first row to the end.
-  const __amdgpu_buffer_rsrc_t vb = __builtin_amdgcn_make_buffer_rsrc(
-      a.vcache + ((size_t)kvh * a.capacity + c) * 256, 0, (a.capacity - c) * 512, 0x00020000);
-  const uint32_t stride = (uint32_t)C * 512;
   float o0 = 0.0f, o1 = 0.0f, sum = 0.0f;
-  if (wave & 1)
-    dims_loop<1>(tiles, vb, (uint32_t)t * 2, stride, L, o0, o1, sum);
-  else
-    dims_loop<0>(tiles, vb, (uint32_t)t * 2, stride, L, o0, o1, sum);
+  float carry = kFiniteMin;  // waves 2/3: running max of head wave-2
+  if (L > 0) {
+    const int nt = (L + kTile - 1) / kTile;
+    const int sstride = score_stride(a.capacity);
+    const uint16_t* vrow0 = a.vcache + ((size_t)kvh * a.capacity + c) * 256;
+    const float* sc0 = a.scores + ((size_t)h0 * kAttnMaxChains + c) * sstride;
+    for (int T = 0; T < kStages - 1 && T < nt; ++T) issue_tile(sm, vrow0, sc0, sstride, C, L, T, wave, lane);
+    // Every wave issues 9 operations per tile (8 V rows pairs, 1 score part).
+    // Exps of tile 0 need tile 0 complete; tiles 1 and 2 may stay pending.
+    if (nt >= 3) wait_vm<18>(); else if (nt == 2) wait_vm<9>(); else wait_vm<0>();
+    lds_barrier();
+    if (wave >= 2) tile_exps(sm, 0, L, wave - 2, lane, carry);
+    for (int T = 0; T < nt; ++T) {
+      // Tiles up to T+1 complete (V of T, scores of T+1); tile T+2 may pend.
+      if (T + 2 < nt) wait_vm<9>(); else wait_vm<0>();
+      lds_barrier();
+      if (T + kStages - 1 < nt) issue_tile(sm, vrow0, sc0, sstride, C, L, T + kStages - 1, wave, lane);
+      if (wave >= 2 && T + 1 < nt) tile_exps(sm, T + 1, L, wave - 2, lane, carry);
+      if (wave == 0)
+        run_tile<true, 0>(sm, T, t, o0, o1, sum);
+      else if (wave == 1)
+        run_tile<true, 1>(sm, T, t, o0, o1, sum);
+      else
+        run_tile<false, 0>(sm, T, t, o0, o1, sum);
+    }
+  }
   a.part_o[((size_t)h0 * kAttnMaxChains + c) * 256 + t] = o0;
   a.part_o[((size_t)(h0 + 1) * kAttnMaxChains + c) * 256 + t] = o1;
-  if (wave < 2 && lane == 0)
-    a.part_ml[((size_t)(h0 + wave) * kAttnMaxChains + c) * 2 + 1] = sum;
+  if (lane == 0) {
+    float* ml = a.part_ml + ((size_t)(h0 + (wave & 1)) * kAttnMaxChains + c) * 2;
+    if (wave < 2) ml[1] = sum;
+    else ml[0] = carry;
+  }
 }
 
 // ---- merge + gate ----
@@ -424,8 +496,7 @@ bool attn_ok(const AttnArgs& a) {
 }  // namespace
 
 size_t attn_scratch_bytes(int capacity) {
-  return ((size_t)kQHeads * kAttnMaxChains * (256 + 2) + (size_t)kQHeads * capacity) *
-         sizeof(float);
+  return (size_t)kQHeads * kAttnMaxChains * (256 + 2 + score_stride(capacity)) * sizeof(float);
 }
 
 void attn_bind_scratch(AttnArgs& a, void* scratch) {
@@ -442,7 +513,7 @@ hipError_t launch_attn_scores(const AttnArgs& a, hipStream_t s) {
 
 hipError_t launch_attn_chain(const AttnArgs& a, hipStream_t s) {
   if (!attn_ok(a)) return hipErrorInvalidValue;
-  hipLaunchKernelGGL(k_attn_chain, dim3(kKvHeads * kAttnMaxChains * 2), dim3(320), 0, s, a);
+  hipLaunchKernelGGL(k_attn_chain, dim3(kKvHeads * kAttnMaxChains * 2), dim3(256), 0, s, a);
   return hipGetLastError();
 }
 

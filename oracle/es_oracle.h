@@ -17,19 +17,23 @@
  * the series evaluations in es_oracle.c (the kernels evaluate the same
  * steps). Compiled with -ffp-contract=off: FMAs appear only where fmaf is
  * written. Decode attention keeps the reference's own algorithm (32 or 64
- * interleaved position blocks, bf16 partials at and above 1024 positions),
- * which the GPU's split-K decode does not reproduce bit for bit.
+ * interleaved position chains, bf16 chain outputs at and above 1024
+ * positions) with one stated order for each score, chain update and merge.
  *
- * Pinning status (tests/test_oracle_*.py):
- *   bf16 RNE, nibble unpack ........ exhaustive/torch cross-check, closed forms
- *   sigmoid/softplus/SwiGLU ........ special values, bounded error vs fp64 math
- *   Q4 matvec / embedding .......... closed forms + fp64 dequant-then-dot brute force
- *   RMSNorm ........................ closed form on constant vectors + fp64
- *   GDN conv/prepare/recur/gate .... delta-rule invariants + fp64 recurrence
- *   attention prepare (RoPE) ....... position-0 identity, pair-norm, additivity
- *   attention decode/split/merge ... N=1, equal keys, fp64 softmax, split==single
- *   greedy ......................... planted maxima and exact ties
- * No function is "parity unpinned"; see each test file for the checks.
+ * Pinning (tests/test_oracle_*.py, tests/test_golden.py):
+ *   bf16 RNE, widening ............. exhaustive / 2M patterns vs torch, ties
+ *   exp, log / sin, cos ............ <= 2 ulp / <= 2.5e-7 vs fp64 libm, specials
+ *   sigmoid/softplus (bf16 steps) .. all 65,536 bf16 inputs vs fp64 model
+ *   rotary frequencies ............. closed form 1e7^(-i/32)
+ *   Q4 matvec / embedding .......... integer-dot exactness, zero-code closed
+ *                                    form, fp64 dequant brute force, linearity
+ *   RMSNorm ........................ constant-vector closed form (bitwise), fp64
+ *   GDN conv/prepare/recur/gate .... delta-rule invariants, fp64 recurrence
+ *   attention prepare (RoPE) ....... position-0 identity, fp64 rotation, norms
+ *   attention decode/split/merge ... N=1, equal keys, dominant key, fp64 route
+ *                                    model, split vs single, chain states
+ *   greedy ......................... planted maxima, exact ties, fp64 lse
+ * No function is "parity unpinned".
  */
 #ifndef ES_ORACLE_H
 #define ES_ORACLE_H

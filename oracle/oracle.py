@@ -59,6 +59,10 @@ def lib():
             "eo_f32_to_bf16": (c_uint16, [c_float]),
             "eo_round_bf16": (c_float, [c_float]),
             "eo_f32_to_bf16_array": (None, [vp, vp, ctypes.c_size_t]),
+            "eo_bf16_to_f32_array": (None, [vp, vp, ctypes.c_size_t]),
+            "eo_exp": (c_float, [c_float]),
+            "eo_log": (c_float, [c_float]),
+            "eo_sincos": (None, [c_float, POINTER(c_float), POINTER(c_float)]),
             "eo_sigmoid_bf": (c_float, [c_float]),
             "eo_softplus_bf": (c_float, [c_float]),
             "eo_rope_inv_freq": (c_float, [c_int]),
@@ -102,6 +106,28 @@ def f32_to_bf16(a: np.ndarray) -> np.ndarray:
     a = np.ascontiguousarray(a, dtype=np.float32)
     out = np.empty(a.shape, dtype=np.uint16)
     lib().eo_f32_to_bf16_array(P(a), P(out), a.size)
+    return out
+
+
+def exp(x: float) -> float:
+    return float(lib().eo_exp(x))
+
+
+def log(x: float) -> float:
+    return float(lib().eo_log(x))
+
+
+def sincos(x: float):
+    s, c = c_float(), c_float()
+    lib().eo_sincos(x, ctypes.byref(s), ctypes.byref(c))
+    return float(s.value), float(c.value)
+
+
+def bf16_to_f32_c(a: np.ndarray) -> np.ndarray:
+    """The oracle's own bf16 -> fp32 widening (checked against bf16_to_f32)."""
+    a = np.ascontiguousarray(a, dtype=np.uint16)
+    out = np.empty(a.shape, dtype=np.float32)
+    lib().eo_bf16_to_f32_array(P(a), P(out), a.size)
     return out
 
 

@@ -84,3 +84,37 @@ def assert_bits_equal(got, want, what=""):
         g = f32(got[i:i + 1])[0] if got.dtype == np.uint16 else got[i]
         w = f32(want[i:i + 1])[0] if want.dtype == np.uint16 else want[i]
         raise AssertionError(f"{what}: {bad.size} of {gv.size} differ (first [{i}] got {g!r} want {w!r})")
+
+
+def fp64_attention_gated(query, kc, vc, length, q_proj):
+    """Decode attention of the reference's route in fp64 with its rounding
+    points: below 1024 positions one softmax; from 1024 on 64 position chains
+    (positions c, c+64, ...) whose unnormalised outputs are rounded to bf16
+    before the merge (attention_decode.metal:423-430); then
+    bf16(bf16(o) * sigmoid_bf(gate)) (attention_decode.metal:876-889)."""
+    q = f32(query).reshape(8, 256).astype(np.float64) * 0.0625
+    out = np.empty((8, 256))
+    for h in range(8):
+        K = f32(kc[h // 4, :length]).astype(np.float64)
+        V = f32(vc[h // 4, :length]).astype(np.float64)
+        s = K @ q[h]
+        if length < 1024:
+            p = np.exp(s - s.max())
+            out[h] = (p @ V) / p.sum()
+            continue
+        m = np.array([s[c::64].max() for c in range(64)])
+        sums = np.array([np.exp(s[c::64] - m[c]).sum() for c in range(64)])
+        parts = np.stack([f32(bf16(np.exp(s[c::64] - m[c]) @ V[c::64])) for c in range(64)])
+        f = np.exp(m - m.max())
+        out[h] = (f @ parts.astype(np.float64)) / (f @ sums)
+    gate = f32(q_proj).reshape(8, 512)[:, 256:].ravel()
+    sig = np.array([O.lib().eo_sigmoid_bf(float(x)) for x in gate], dtype=np.float32)
+    o = f32(bf16(out.ravel()))
+    return bf16(o * sig)
+
+
+def fp32_ulp(x):
+    """Spacing of fp32 numbers at |x| (normal range)."""
+    x = np.abs(np.asarray(x, dtype=np.float64))
+    e = np.floor(np.log2(np.maximum(x, np.finfo(np.float32).tiny)))
+    return np.exp2(e - 23)

@@ -14,36 +14,9 @@ import pytest
 
 import esdecode as E
 import oracle as O
-from helpers import assert_bf16_close, assert_bits_equal, bf16, f32, rng
+from helpers import assert_bf16_close, assert_bits_equal, bf16, f32, fp64_attention_gated, rng
 
 pytestmark = pytest.mark.gpu
-
-
-def fp64_gated(query, kc, vc, length, q_proj):
-    """The route's mathematics in fp64 with the reference's rounding points:
-    below 1024 positions one softmax; from 1024 on 64 position chains whose
-    unnormalised outputs are rounded to bf16 before the merge
-    (attention_decode.metal:423-430), then bf16(bf16(o) * sigmoid_bf(gate))
-    (attention_decode.metal:876-889)."""
-    q = f32(query).reshape(8, 256).astype(np.float64) * 0.0625
-    out = np.empty((8, 256))
-    for h in range(8):
-        K = f32(kc[h // 4, :length]).astype(np.float64)
-        V = f32(vc[h // 4, :length]).astype(np.float64)
-        s = K @ q[h]
-        if length < 1024:
-            p = np.exp(s - s.max())
-            out[h] = (p @ V) / p.sum()
-            continue
-        m = np.array([s[c::64].max() for c in range(64)])
-        sums = np.array([np.exp(s[c::64] - m[c]).sum() for c in range(64)])
-        parts = np.stack([f32(bf16(np.exp(s[c::64] - m[c]) @ V[c::64])) for c in range(64)])
-        f = np.exp(m - m.max())
-        out[h] = (f @ parts.astype(np.float64)) / (f @ sums)
-    gate = f32(q_proj).reshape(8, 512)[:, 256:].ravel()
-    sig = np.array([O.lib().eo_sigmoid_bf(float(x)) for x in gate], dtype=np.float32)
-    o = f32(bf16(out.ravel()))
-    return bf16(o * sig)
 
 
 def make_inputs(length, seed, cap=None):
@@ -93,7 +66,7 @@ def test_attention_decode(length):
     assert_bits_equal(got["kc"][:, pos], want["kc"][:, pos], what="K row")
     assert np.array_equal(got["kc"][:, :pos], want["kc"][:, :pos]), "earlier cache rows must be untouched"
     assert_bits_equal(got["gated"], want["gated"], what="gated")
-    exact = fp64_gated(want["query"], want["kc"], want["vc"], length, x["q"])
+    exact = fp64_attention_gated(want["query"], want["kc"], want["vc"], length, x["q"])
     assert_bf16_close(got["gated"], exact, max_ulp=2, max_frac=0.1, atol_rel=2e-3, what="gpu vs fp64")
 
 
