@@ -26,6 +26,28 @@ HBM_PEAK = 8.0e12
 GDN_STATE_BYTES = 18 * 2 * 16 * 128 * 128 * 4      # fp32 state read + write
 CONV_HISTORY_BYTES = 18 * 73728                      # history read + write (reference byte model)
 KV_BYTES_PER_POS = 6 * 2 * 2 * 256 * 2               # 6 layers x {K,V} x 2 heads x 256 x bf16
+# k_attn_chain per attended position: V rows of 2 heads (1024 B) + 8 fp32
+# scores (32 B); per launch: chain outputs and (max, sum) written.
+CHAIN_BYTES_PER_POS = 2 * 256 * 2 + 8 * 4
+CHAIN_FIXED_BYTES = 8 * 64 * (256 + 2) * 4
+PROFILES = os.path.join(ROOT, "profiles")
+
+
+def committed_traffic(kernel, ctx):
+    """HBM bytes per launch from the committed counter summary, if any
+    (lines 'fetch_bytes_per_launch: N' and 'write_bytes_per_launch: N')."""
+    path = os.path.join(PROFILES, f"{kernel}_ctx{ctx}_counters.txt")
+    if not os.path.exists(path):
+        return None
+    vals = {}
+    for line in open(path):
+        if ":" in line:
+            k, v = line.split(":", 1)
+            vals[k.strip()] = v.strip()
+    try:
+        return int(float(vals["fetch_bytes_per_launch"]) + float(vals["write_bytes_per_launch"]))
+    except (KeyError, ValueError):
+        return None
 
 
 def weight_bytes():
@@ -76,6 +98,8 @@ def main():
     ap.add_argument("--cpu-steps", type=int, default=2)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--attn-reps", type=int, default=20)
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="also run the 1 GiB plain-copy kernel that calibrates the HBM byte counters")
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this engine runs on one GPU; multi-GPU decode is not built "
@@ -106,12 +130,18 @@ def main():
         print(f"# ctx {ctx}: {tps:.1f} tok/s, {ms / args.steps * 1e3:.1f} us/step, "
               f"{b * tps / 1e9:.0f} GB/s ({b * tps / HBM_PEAK * 100:.1f}% of 8 TB/s)", file=sys.stderr, flush=True)
     head_ctx = max(contexts)
-    # dominant kernel: split-K attention of one layer at the headline context
+    # dominant kernel: the per-chain online softmax of one attention layer at
+    # the headline context (it streams the layer's V cache and scores)
     eng.fill_synthetic(head_ctx - 1, seed=1, pending=1)
-    attn_ms = eng.time_attention(3, args.attn_reps)
-    attn_bytes = KV_BYTES_PER_POS // 6 * head_ctx + 8 * 512 * 2
+    parts = {p: eng.time_attention(3, args.attn_reps, p) for p in ("scores", "chains", "merge", "all")}
+    chain_ms = parts["chains"]
+    n_att = head_ctx  # attended positions, including the new one
+    chain_bytes = CHAIN_BYTES_PER_POS * n_att + CHAIN_FIXED_BYTES
     head_ms = eng.time_head(args.attn_reps)
     eng.close()
+    copy_bytes = 1 << 30
+    copy_ms = E.time_copy(copy_bytes, reps=20 if args.copy_calibration else 5)
+    copy_gbs = 2 * copy_bytes / (copy_ms / 1e3) / 1e9
 
     cpu = None
     if not args.no_cpu:
@@ -141,15 +171,17 @@ def main():
             "head_kernel_us": round(head_ms * 1e3, 2),
         },
         "roofline": {
-            "kernel": "k_attn_split (one attention layer, split-K decode)",
+            "kernel": f"k_attn_chain (per-chain online softmax over V, one attention layer, {n_att} positions)",
             "bound": "hbm",
-            "achieved": round(attn_bytes / (attn_ms / 1e3) / 1e9, 1),
+            "achieved": round(chain_bytes / (chain_ms / 1e3) / 1e9, 1),
             "peak": 8000.0,
             "unit": "GB/s",
-            "frac": round(attn_bytes / (attn_ms / 1e3) / HBM_PEAK, 4),
-            "traffic": None,
-            "launch_us": round(attn_ms * 1e3, 2),
-            "algorithmic_bytes": attn_bytes,
+            "frac": round(chain_bytes / (chain_ms / 1e3) / HBM_PEAK, 4),
+            "traffic": committed_traffic("k_attn_chain", head_ctx),
+            "algorithmic_bytes": chain_bytes,
+            "launch_us": round(chain_ms * 1e3, 2),
+            "attention_layer_us": {k: round(v * 1e3, 2) for k, v in parts.items()},
+            "measured_copy_GBs": round(copy_gbs, 1),
         },
         "cpu_baseline": cpu,
     }

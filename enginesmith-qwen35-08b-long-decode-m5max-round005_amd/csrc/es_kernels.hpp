@@ -125,6 +125,8 @@ hipError_t launch_set_token(StepState* st, const uint32_t* src, hipStream_t s);
 // Fill with N(0, sigma) bf16 / fp32 values from a counter-based generator.
 hipError_t launch_fill_normal_bf16(uint16_t* dst, size_t n, float sigma, uint64_t seed,
                                    hipStream_t s);
+// Device-to-device copy of `bytes` (a multiple of 16) by a plain kernel.
+hipError_t launch_copy16(void* dst, const void* src, size_t bytes, hipStream_t s);
 hipError_t launch_fill_normal_f32(float* dst, size_t n, float sigma, uint64_t seed,
                                   hipStream_t s);
 

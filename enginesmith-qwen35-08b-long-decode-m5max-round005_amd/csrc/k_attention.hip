@@ -16,12 +16,13 @@
 //   dims 8m+64i .. +7 (i = 0..3, 128 coalesced bytes per 8 lanes), one fma
 //   chain per 8 dims, (p[m]+p[m+8])+(p[m+16]+p[m+24]) in the lane and a DPP
 //   tree over the 8 lanes. Scores go to an fp32 array [8, capacity].
-// k_attn_chain, 256 blocks x 320 threads: block = (KV head, chain, query-head
-//   pair). Waves 0..3 own one value dim each for both heads; wave 4 turns the
-//   chain's scores into running max, factor and exp score, 64 steps at a time
-//   and one tile ahead (max scan by DPP, exp by the shared series). Per step
-//   o = fma(e, v, o*factor) and sum = sum*factor + e; when every factor of a
-//   tile is exactly 1 the products by 1 are skipped, which changes no bit.
+// k_attn_chain, 256 blocks x 256 threads: block = (KV head, chain, query-head
+//   pair), thread = value dim of both heads. V rows and scores are staged in
+//   LDS by 16-byte global->LDS DMA, four 64-step tiles deep. Two waves turn
+//   the chain's scores into running max, factor and exp score one tile ahead
+//   (max scan by DPP, exp by the shared series). Per step o = fma(e, v, o*factor)
+//   and sum = sum*factor + e; when every factor of a tile is exactly 1 the
+//   products by 1 are skipped, which changes no bit.
 //   The two blocks of a (KV head, chain) sit on the same XCD (block ids b and
 //   b+8) so the second read of each V row is an L2 hit.
 // k_attn_merge, grid (8 heads, 4 quarters) x 64: chain combination of either
@@ -258,9 +259,10 @@ __device__ __forceinline__ void wait_vm() {
   __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
 }
 
-// Issue this wave's share of tile T: 16 V rows (8 DMA of 1 KB: lanes 0..31
-// one row, 32..63 the next) and 32 floats of scores (8 lanes x 16 B). Steps
-// past the chain's end re-read its last row and are masked by e = 0.
+// Issue this wave's share of tile T (4 waves): 16 V rows as 8 DMA of 1 KB
+// (lanes 0..31 one row, 32..63 the next) and 8 x 16 B of scores. Rows past
+// the chain's end re-read its last row (in bounds; their slots are masked by
+// e = 0).
 __device__ __forceinline__ void issue_tile(ChainSmem& sm, const uint16_t* vrow0, const float* sc0,
                                            int sstride, int C, int L, int T, int wave, int lane) {
   const int st = T % kStages;
@@ -288,35 +290,37 @@ __device__ __forceinline__ void tile_exps(ChainSmem& sm, int T, int L, int head,
   const float f = es_exp(pv - mt), e = es_exp(s - mt);
   sm.e[T & 1][head][lane] = e;
   sm.f[T & 1][head][lane] = f;
-  const bool slow = __any(f != 1.0f);
-  if (lane == 0) sm.slow[T & 1][head] = slow;
+  sm.slow[T & 1][head] = __any(f != 1.0f);  // wave-uniform, stored by every lane
   carry = readlane63(mt);
 }
 
 // 64 steps of the dim owned by this thread for both heads; SUM waves also
 // keep head WS's sum. Steps past the chain's end have e = 0 and f = 1 and
-// change nothing (o is never -0, V rows are finite). Software-pipelined in
-// batches of 8 steps: the LDS reads of batch q+1 are issued before batch q
-// is computed, so one wave per SIMD hides the LDS latency.
+// change nothing (o is never -0, V rows are finite). V rows are read as
+// dwords (the thread's dim and its neighbour; two rows per LDS read pair)
+// and the thread's half is moved to bits 31:16 by one byte permute; exp
+// scores come 4 steps per read. Batches of 4 steps are software-pipelined
+// two deep.
+constexpr int kBatch = 4;
+
 template <bool SLOW>
 struct Batch {
-  uint32_t v[8];
-  float4 e[2][2];
-  float4 f[SLOW ? 2 : 1][SLOW ? 2 : 1];
+  uint32_t w[kBatch];
+  float4 e[2];
+  float4 f[SLOW ? 2 : 1];
 };
 
 template <bool SLOW>
-__device__ __forceinline__ void load_batch(const ChainSmem& sm, int st, int b, int d, int q,
+__device__ __forceinline__ void load_batch(const ChainSmem& sm, int st, int b, int kw, int q,
                                            Batch<SLOW>& x) {
+  const uint32_t* vw = reinterpret_cast<const uint32_t*>(&sm.v[st][0][0]);
 #pragma unroll
-  for (int i = 0; i < 8; ++i) x.v[i] = sm.v[st][8 * q + i][d];
+  for (int i = 0; i < kBatch; ++i) x.w[i] = vw[(kBatch * q + i) * 128 + kw];
 #pragma unroll
-  for (int h = 0; h < 2; ++h)
-#pragma unroll
-    for (int k = 0; k < 2; ++k) {
-      x.e[h][k] = reinterpret_cast<const float4*>(sm.e[b][h])[2 * q + k];
-      if (SLOW) x.f[h][k] = reinterpret_cast<const float4*>(sm.f[b][h])[2 * q + k];
-    }
+  for (int h = 0; h < 2; ++h) {
+    x.e[h] = reinterpret_cast<const float4*>(sm.e[b][h])[q];
+    if (SLOW) x.f[h] = reinterpret_cast<const float4*>(sm.f[b][h])[q];
+  }
 }
 
 __device__ __forceinline__ float lane4(const float4& v, int i) {
@@ -324,13 +328,14 @@ __device__ __forceinline__ float lane4(const float4& v, int i) {
 }
 
 template <bool SLOW, bool SUM, int WS>
-__device__ __forceinline__ void run_batch(const Batch<SLOW>& x, float& o0, float& o1, float& sum) {
+__device__ __forceinline__ void run_batch(const Batch<SLOW>& x, uint32_t sel, float& o0, float& o1,
+                                          float& sum) {
 #pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    const float v = __builtin_bit_cast(float, x.v[i] << 16);
-    const float e0 = lane4(x.e[0][i >> 2], i & 3), e1 = lane4(x.e[1][i >> 2], i & 3);
+  for (int i = 0; i < kBatch; ++i) {
+    const float v = __builtin_bit_cast(float, __builtin_amdgcn_perm(0u, x.w[i], sel));
+    const float e0 = lane4(x.e[0], i), e1 = lane4(x.e[1], i);
     if (SLOW) {
-      const float f0 = lane4(x.f[0][i >> 2], i & 3), f1 = lane4(x.f[1][i >> 2], i & 3);
+      const float f0 = lane4(x.f[0], i), f1 = lane4(x.f[1], i);
       o0 = fmaf(e0, v, o0 * f0);
       o1 = fmaf(e1, v, o1 * f1);
       if (SUM) sum = sum * (WS ? f1 : f0) + (WS ? e1 : e0);
@@ -345,13 +350,18 @@ __device__ __forceinline__ void run_batch(const Batch<SLOW>& x, float& o0, float
 template <bool SLOW, bool SUM, int WS>
 __device__ __forceinline__ void chain_steps(const ChainSmem& sm, int T, int d, float& o0,
                                             float& o1, float& sum) {
-  const int st = T % kStages, b = T & 1;
-  Batch<SLOW> x[2];
-  load_batch<SLOW>(sm, st, b, d, 0, x[0]);
+  const int st = T % kStages, b = T & 1, kw = d >> 1;
+  // byte permute: the thread's bf16 (low half for even dims, high half for
+  // odd) into bits 31:16, zeros below
+  const uint32_t sel = (d & 1) ? 0x03020c0cu : 0x01000c0cu;
+  constexpr int nb = kTile / kBatch;
+  Batch<SLOW> x[3];
+  load_batch<SLOW>(sm, st, b, kw, 0, x[0]);
+  load_batch<SLOW>(sm, st, b, kw, 1, x[1]);
 #pragma unroll
-  for (int q = 0; q < kTile / 8; ++q) {
-    if (q + 1 < kTile / 8) load_batch<SLOW>(sm, st, b, d, q + 1, x[(q + 1) & 1]);
-    run_batch<SLOW, SUM, WS>(x[q & 1], o0, o1, sum);
+  for (int q = 0; q < nb; ++q) {
+    if (q + 2 < nb) load_batch<SLOW>(sm, st, b, kw, q + 2, x[(q + 2) % 3]);
+    run_batch<SLOW, SUM, WS>(x[q % 3], sel, o0, o1, sum);
   }
 }
 
@@ -364,10 +374,11 @@ __device__ __forceinline__ void run_tile(const ChainSmem& sm, int T, int d, floa
     chain_steps<false, SUM, WS>(sm, T, d, o0, o1, sum);
 }
 
-// Block = (KV head, chain, query-head pair), 4 waves, thread = value dim.
-// Per tile T: wait for this wave's DMA of tiles up to T+1, barrier, issue
-// tile T+3 into the stage tile T-1 used, waves 2/3 form the exps of tile T+1
-// (heads 0/1), all waves run tile T. Waves 0/1 keep the sums of heads 0/1.
+// Block = (KV head, chain, query-head pair), 4 waves, thread = value dim of
+// both heads. Per tile T: wait for this wave's DMA of tiles up to T+1,
+// barrier, issue tile T+3 into the stage tile T-1 used, waves 2/3 form the
+// exps of tile T+1 (heads 0/1), all waves run tile T; waves 0/1 keep the
+// sums of heads 0/1.
 __global__ __launch_bounds__(256, 1) void k_attn_chain(AttnArgs a) {
   __shared__ ChainSmem sm;
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
@@ -387,8 +398,9 @@ __global__ __launch_bounds__(256, 1) void k_attn_chain(AttnArgs a) {
     const int sstride = score_stride(a.capacity);
     const uint16_t* vrow0 = a.vcache + ((size_t)kvh * a.capacity + c) * 256;
     const float* sc0 = a.scores + ((size_t)h0 * kAttnMaxChains + c) * sstride;
-    for (int T = 0; T < kStages - 1 && T < nt; ++T) issue_tile(sm, vrow0, sc0, sstride, C, L, T, wave, lane);
-    // Every wave issues 9 operations per tile (8 V rows pairs, 1 score part).
+    for (int T = 0; T < kStages - 1 && T < nt; ++T)
+      issue_tile(sm, vrow0, sc0, sstride, C, L, T, wave, lane);
+    // Every wave issues 9 operations per tile (8 V row pairs, 1 score part).
     // Exps of tile 0 need tile 0 complete; tiles 1 and 2 may stay pending.
     if (nt >= 3) wait_vm<18>(); else if (nt == 2) wait_vm<9>(); else wait_vm<0>();
     lds_barrier();

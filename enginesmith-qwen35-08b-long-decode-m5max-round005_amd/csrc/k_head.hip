@@ -204,7 +204,27 @@ __global__ void k_fill_normal_f32(float* dst, size_t n, float sigma, uint64_t se
   }
 }
 
+// Plain streaming copy, 16 bytes per thread per step (also the reference
+// point for the HBM byte counters: it reads and writes exactly `n16` x 16 B).
+__global__ __launch_bounds__(256) void k_copy16(u32x4* __restrict__ dst,
+                                                const u32x4* __restrict__ src, size_t n16) {
+  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n16;
+       i += (size_t)gridDim.x * blockDim.x)
+    dst[i] = __builtin_nontemporal_load(src + i);
+}
+
 }  // namespace
+
+hipError_t launch_copy16(void* dst, const void* src, size_t bytes, hipStream_t s) {
+  if (!dst || !src || bytes % 16 != 0) return hipErrorInvalidValue;
+  if (bytes == 0) return hipSuccess;
+  const size_t n16 = bytes / 16;
+  size_t blocks = (n16 + 255) / 256;
+  if (blocks > 8192) blocks = 8192;
+  hipLaunchKernelGGL(k_copy16, dim3((unsigned)blocks), dim3(256), 0, s, static_cast<u32x4*>(dst),
+                     static_cast<const u32x4*>(src), n16);
+  return hipGetLastError();
+}
 
 int head_blocks(int vocab) { return (vocab + kRowsPerBlock - 1) / kRowsPerBlock; }
 size_t head_scratch_bytes(int vocab) { return (size_t)head_blocks(vocab) * 2 * sizeof(float); }

@@ -45,6 +45,8 @@ _SIGNATURES = {
     "es_memcpy_htod": (c_int, [c_void_p, c_void_p, c_size_t]),
     "es_memcpy_dtoh": (c_int, [c_void_p, c_void_p, c_size_t]),
     "es_memset": (c_int, [c_void_p, c_int, c_size_t]),
+    "es_copy_d2d": (c_int, [c_void_p, c_void_p, c_size_t, c_void_p]),
+    "es_time_copy_d2d": (c_int, [c_void_p, c_void_p, c_size_t, c_int, POINTER(c_double)]),
     "es_synchronize": (c_int, []),
     "es_stream_create": (c_int, [POINTER(c_void_p)]),
     "es_stream_destroy": (c_int, [c_void_p]),
@@ -329,6 +331,18 @@ class Engine:
 
 def splits_for(length: int) -> int:
     return int(lib().es_engine_splits_for(length))
+
+
+def time_copy(nbytes: int, reps: int = 10) -> float:
+    """Average ms of a device-to-device copy of nbytes by the plain copy kernel."""
+    src, dst = DeviceBuffer(nbytes), DeviceBuffer(nbytes)
+    ms = c_double()
+    try:
+        check(lib().es_time_copy_d2d(dst.ptr, src.ptr, nbytes, reps, ctypes.byref(ms)))
+    finally:
+        src.close()
+        dst.close()
+    return ms.value
 
 
 def rope_inv_freq() -> np.ndarray:

@@ -60,6 +60,13 @@ int es_free(void* ptr);
 int es_memcpy_htod(void* dst, const void* src, size_t bytes);
 int es_memcpy_dtoh(void* dst, const void* src, size_t bytes);
 int es_memset(void* dst, int value, size_t bytes);
+/* Device-to-device copy by a plain streaming kernel (bytes a multiple of
+ * 16); no reference counterpart: plumbing, and the known-size workload that
+ * calibrates the HBM byte counters. */
+int es_copy_d2d(void* dst, const void* src, size_t bytes, void* stream);
+/* Average ms of `reps` es_copy_d2d launches on the null stream (HIP events):
+ * the measured streaming-copy peak beside the nameplate HBM figure. */
+int es_time_copy_d2d(void* dst, const void* src, size_t bytes, int reps, double* ms_avg);
 int es_synchronize(void);
 int es_stream_create(void** stream);
 int es_stream_destroy(void* stream);
