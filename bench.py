@@ -133,7 +133,8 @@ def main():
     # dominant kernel: the per-chain online softmax of one attention layer at
     # the headline context (it streams the layer's V cache and scores)
     eng.fill_synthetic(head_ctx - 1, seed=1, pending=1)
-    parts = {p: eng.time_attention(3, args.attn_reps, p) for p in ("scores", "chains", "merge", "all")}
+    # rotate over the six attention layers: every launch streams a cold cache
+    parts = {p: eng.time_attention(-1, args.attn_reps, p) for p in ("scores", "chains", "merge", "all")}
     chain_ms = parts["chains"]
     n_att = head_ctx  # attended positions, including the new one
     chain_bytes = CHAIN_BYTES_PER_POS * n_att + CHAIN_FIXED_BYTES

@@ -575,23 +575,31 @@ hipError_t Engine::launch_attention_part(const AttnArgs& a, int which) {
   return e;
 }
 
+// layer < 0 rotates over every attention layer, so each launch streams a KV
+// cache the previous launches did not touch (as in a decode step, where the
+// six layers' caches together exceed the on-package cache); layer >= 0
+// repeats one layer.
 int Engine::time_attention(int layer, int reps, int which, double* ms_avg, std::string* err) {
-  if (layer < 0 || layer >= shape_.n_layers || !layers_[layer].attention || reps <= 0 ||
-      which < 0 || which > 3) {
+  std::vector<int> att;
+  for (int l = 0; l < shape_.n_layers; ++l)
+    if (layers_[l].attention && (layer < 0 || l == layer)) att.push_back(l);
+  if (att.empty() || layer >= shape_.n_layers || reps <= 0 || which < 0 || which > 3) {
     if (err) *err = "invalid attention timing request";
     return 1;
   }
   if (int rc = upload_state(position_, 0, pending_, err)) return rc;
-  const AttnArgs a = attn_args(layers_[layer], splits_for(position_ + 1));
+  std::vector<AttnArgs> args;
+  for (int l : att) args.push_back(attn_args(layers_[l], splits_for(position_ + 1)));
   // The timed launches write the K/V row of the current position, the row the
   // next decode step writes before anything reads it.
-  ES_HIP(launch_attention_part(a, 0), "attn warmup");
+  for (const AttnArgs& a : args) ES_HIP(launch_attention_part(a, 0), "attn warmup");
   ES_HIP(hipStreamSynchronize(stream_), "sync");
   hipEvent_t e0, e1;
   ES_HIP(hipEventCreate(&e0), "event");
   ES_HIP(hipEventCreate(&e1), "event");
   ES_HIP(hipEventRecord(e0, stream_), "record");
-  for (int i = 0; i < reps; ++i) ES_HIP(launch_attention_part(a, which), "attn");
+  for (int i = 0; i < reps; ++i)
+    ES_HIP(launch_attention_part(args[i % args.size()], which), "attn");
   ES_HIP(hipEventRecord(e1, stream_), "record");
   ES_HIP(hipEventSynchronize(e1), "sync");
   float ms = 0.0f;

@@ -236,7 +236,9 @@ int es_engine_fill_synthetic(es_engine* e, int length, uint64_t seed, uint32_t p
 
 /* Timing with HIP events on the engine stream. */
 int es_engine_time_decode(es_engine* e, int steps, int warmup, double* ms_total);
-/* which: 0 = all three attention launches, 1 = scores, 2 = chains, 3 = merge */
+/* which: 0 = all three attention launches, 1 = scores, 2 = chains, 3 = merge.
+ * layer < 0 rotates over every attention layer (cold KV caches, as in a
+ * decode step); layer >= 0 repeats that layer. */
 int es_engine_time_attention(es_engine* e, int layer, int reps, int which, double* ms_avg);
 int es_engine_time_head(es_engine* e, int reps, double* ms_avg);
 /* Score blocks per KV head the engine uses at attention length `length`. */
