@@ -16,8 +16,9 @@
 //   dims 8m+64i .. +7 (i = 0..3, 128 coalesced bytes per 8 lanes), one fma
 //   chain per 8 dims, (p[m]+p[m+8])+(p[m+16]+p[m+24]) in the lane and a DPP
 //   tree over the 8 lanes. Scores go to an fp32 array [8, capacity].
-// k_attn_chain, 256 blocks x 256 threads: block = (KV head, chain, query-head
-//   pair), thread = value dim of both heads. V rows and scores are staged in
+// k_attn_chain, 256 blocks x 320 threads: block = (KV head, chain, query-head
+//   pair), thread = two adjacent value dims of one head, plus one data-moving
+//   wave. V rows and scores are staged in
 //   LDS by 16-byte global->LDS DMA, four 64-step tiles deep. Two waves turn
 //   the chain's scores into running max, factor and exp score one tile ahead
 //   (max scan by DPP, exp by the shared series). Per step o = fma(e, v, o*factor)
@@ -256,27 +257,29 @@ __device__ __forceinline__ void lds_barrier() {
 // (gfx9 encoding: vmcnt[3:0] | expcnt 7 | lgkmcnt 15 | vmcnt[5:4] << 14).
 template <int N>
 __device__ __forceinline__ void wait_vm() {
+  static_assert(N >= 0 && N <= 63, "vmcnt is a 6-bit counter");
   __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
 }
 
-// Issue this wave's share of tile T (4 waves): 16 V rows as 8 DMA of 1 KB
-// (lanes 0..31 one row, 32..63 the next) and 8 x 16 B of scores. Rows past
-// the chain's end re-read its last row (in bounds; their slots are masked by
-// e = 0).
+// Issue tile T from the producer wave: 64 V rows as 32 DMA of 1 KB (lanes
+// 0..31 one row, 32..63 the next) and the tile's 2 x 64 scores as one DMA of
+// 32 x 16 B (33 vector-memory operations). Rows past the chain's end re-read
+// its last row (in bounds; their slots are masked by e = 0).
+constexpr int kTileOps = 33;
 __device__ __forceinline__ void issue_tile(ChainSmem& sm, const uint16_t* vrow0, const float* sc0,
-                                           int sstride, int C, int L, int T, int wave, int lane) {
+                                           int sstride, int C, int L, int T, int lane) {
   const int st = T % kStages;
-#pragma unroll
-  for (int x = 0; x < 8; ++x) {
-    const int r = 16 * wave + 2 * x;
+#pragma unroll 4
+  for (int x = 0; x < 32; ++x) {
+    const int r = 2 * x;
     const int j = min(T * kTile + r + (lane >> 5), L - 1);
     const uint16_t* g = vrow0 + (size_t)j * C * 256 + (lane & 31) * 8;
     __builtin_amdgcn_global_load_lds(g, (lds_ptr_t)&sm.v[st][r][0], 16, 0, 0);
   }
-  if (lane < 8) {
-    const int head = wave >> 1, part = wave & 1;
-    const float* g = sc0 + (size_t)head * kAttnMaxChains * sstride + T * kTile + part * 32 + lane * 4;
-    __builtin_amdgcn_global_load_lds(g, (lds_ptr_t)&sm.s[st][head][part * 32], 16, 0, 0);
+  if (lane < 32) {
+    const int head = lane >> 4, part = lane & 15;
+    const float* g = sc0 + (size_t)head * kAttnMaxChains * sstride + T * kTile + part * 4;
+    __builtin_amdgcn_global_load_lds(g, (lds_ptr_t)&sm.s[st][0][0], 16, 0, 0);
   }
 }
 
@@ -294,94 +297,90 @@ __device__ __forceinline__ void tile_exps(ChainSmem& sm, int T, int L, int head,
   carry = readlane63(mt);
 }
 
-// 64 steps of the dim owned by this thread for both heads; SUM waves also
-// keep head WS's sum. Steps past the chain's end have e = 0 and f = 1 and
-// change nothing (o is never -0, V rows are finite). V rows are read as
-// dwords (the thread's dim and its neighbour; two rows per LDS read pair)
-// and the thread's half is moved to bits 31:16 by one byte permute; exp
-// scores come 4 steps per read. Batches of 4 steps are software-pipelined
-// two deep.
+// 64 steps of the two adjacent dims owned by this thread for one head; SUM
+// waves also keep the head's sum. Steps past the chain's end have e = 0 and
+// f = 1 and change nothing (o is never -0, V rows are finite). One dword
+// read gives both dims' bf16 values (two rows per LDS read pair); exp scores
+// come 4 steps per read. Batches of 4 steps are software-pipelined two deep.
 constexpr int kBatch = 4;
 
 template <bool SLOW>
 struct Batch {
   uint32_t w[kBatch];
-  float4 e[2];
-  float4 f[SLOW ? 2 : 1];
+  float4 e;
+  float4 f;
 };
 
 template <bool SLOW>
-__device__ __forceinline__ void load_batch(const ChainSmem& sm, int st, int b, int kw, int q,
-                                           Batch<SLOW>& x) {
+__device__ __forceinline__ void load_batch(const ChainSmem& sm, int st, int b, int hh, int kw,
+                                           int q, Batch<SLOW>& x) {
   const uint32_t* vw = reinterpret_cast<const uint32_t*>(&sm.v[st][0][0]);
 #pragma unroll
   for (int i = 0; i < kBatch; ++i) x.w[i] = vw[(kBatch * q + i) * 128 + kw];
-#pragma unroll
-  for (int h = 0; h < 2; ++h) {
-    x.e[h] = reinterpret_cast<const float4*>(sm.e[b][h])[q];
-    if (SLOW) x.f[h] = reinterpret_cast<const float4*>(sm.f[b][h])[q];
-  }
+  x.e = reinterpret_cast<const float4*>(sm.e[b][hh])[q];
+  if (SLOW) x.f = reinterpret_cast<const float4*>(sm.f[b][hh])[q];
 }
 
 __device__ __forceinline__ float lane4(const float4& v, int i) {
   return i == 0 ? v.x : i == 1 ? v.y : i == 2 ? v.z : v.w;
 }
 
-template <bool SLOW, bool SUM, int WS>
-__device__ __forceinline__ void run_batch(const Batch<SLOW>& x, uint32_t sel, float& o0, float& o1,
-                                          float& sum) {
+template <bool SLOW, bool SUM>
+__device__ __forceinline__ void run_batch(const Batch<SLOW>& x, float& oa, float& ob, float& sum) {
 #pragma unroll
   for (int i = 0; i < kBatch; ++i) {
-    const float v = __builtin_bit_cast(float, __builtin_amdgcn_perm(0u, x.w[i], sel));
-    const float e0 = lane4(x.e[0], i), e1 = lane4(x.e[1], i);
+    const float va = bf_lo(x.w[i]), vb = bf_hi(x.w[i]);
+    const float e = lane4(x.e, i);
     if (SLOW) {
-      const float f0 = lane4(x.f[0], i), f1 = lane4(x.f[1], i);
-      o0 = fmaf(e0, v, o0 * f0);
-      o1 = fmaf(e1, v, o1 * f1);
-      if (SUM) sum = sum * (WS ? f1 : f0) + (WS ? e1 : e0);
+      const float f = lane4(x.f, i);
+      oa = fmaf(e, va, oa * f);
+      ob = fmaf(e, vb, ob * f);
+      if (SUM) sum = sum * f + e;
     } else {
-      o0 = fmaf(e0, v, o0);
-      o1 = fmaf(e1, v, o1);
-      if (SUM) sum = sum + (WS ? e1 : e0);
+      oa = fmaf(e, va, oa);
+      ob = fmaf(e, vb, ob);
+      if (SUM) sum = sum + e;
     }
   }
 }
 
-template <bool SLOW, bool SUM, int WS>
-__device__ __forceinline__ void chain_steps(const ChainSmem& sm, int T, int d, float& o0,
-                                            float& o1, float& sum) {
-  const int st = T % kStages, b = T & 1, kw = d >> 1;
-  // byte permute: the thread's bf16 (low half for even dims, high half for
-  // odd) into bits 31:16, zeros below
-  const uint32_t sel = (d & 1) ? 0x03020c0cu : 0x01000c0cu;
+template <bool SLOW, bool SUM>
+__device__ __forceinline__ void chain_steps(const ChainSmem& sm, int T, int hh, int kw, float& oa,
+                                            float& ob, float& sum) {
+  const int st = T % kStages, b = T & 1;
   constexpr int nb = kTile / kBatch;
   Batch<SLOW> x[3];
-  load_batch<SLOW>(sm, st, b, kw, 0, x[0]);
-  load_batch<SLOW>(sm, st, b, kw, 1, x[1]);
+  load_batch<SLOW>(sm, st, b, hh, kw, 0, x[0]);
+  load_batch<SLOW>(sm, st, b, hh, kw, 1, x[1]);
 #pragma unroll
   for (int q = 0; q < nb; ++q) {
-    if (q + 2 < nb) load_batch<SLOW>(sm, st, b, kw, q + 2, x[(q + 2) % 3]);
-    run_batch<SLOW, SUM, WS>(x[q % 3], sel, o0, o1, sum);
+    if (q + 2 < nb) load_batch<SLOW>(sm, st, b, hh, kw, q + 2, x[(q + 2) % 3]);
+    run_batch<SLOW, SUM>(x[q % 3], oa, ob, sum);
   }
 }
 
-template <bool SUM, int WS>
-__device__ __forceinline__ void run_tile(const ChainSmem& sm, int T, int d, float& o0, float& o1,
-                                         float& sum) {
-  if (sm.slow[T & 1][0] | sm.slow[T & 1][1])
-    chain_steps<true, SUM, WS>(sm, T, d, o0, o1, sum);
+template <bool SUM>
+__device__ __forceinline__ void run_tile(const ChainSmem& sm, int T, int hh, int kw, float& oa,
+                                         float& ob, float& sum) {
+  if (sm.slow[T & 1][hh])
+    chain_steps<true, SUM>(sm, T, hh, kw, oa, ob, sum);
   else
-    chain_steps<false, SUM, WS>(sm, T, d, o0, o1, sum);
+    chain_steps<false, SUM>(sm, T, hh, kw, oa, ob, sum);
 }
 
-// Block = (KV head, chain, query-head pair), 4 waves, thread = value dim of
-// both heads. Per tile T: wait for this wave's DMA of tiles up to T+1,
-// barrier, issue tile T+3 into the stage tile T-1 used, waves 2/3 form the
-// exps of tile T+1 (heads 0/1), all waves run tile T; waves 0/1 keep the
-// sums of heads 0/1.
-__global__ __launch_bounds__(256, 1) void k_attn_chain(AttnArgs a) {
+// Block = (KV head, chain, query-head pair): waves 0,1 own head 0 and waves
+// 2,3 head 1, each thread two adjacent value dims; wave 4 only moves data
+// (global->LDS DMA), so the compute waves never wait on memory counters.
+// Per tile T: the producer waits until tiles up to T+1 are in LDS; barrier;
+// the producer issues tile T+3 into the stage tile T-1 used; waves 1 and 3
+// form the exps of tile T+1 for their head; all compute waves run tile T;
+// waves 0 and 2 keep their head's sum.
+__global__ __launch_bounds__(320, 1) void k_attn_chain(AttnArgs a) {
   __shared__ ChainSmem sm;
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+  const bool producer = wave == 4;
+  const int hh = (wave >> 1) & 1, kw = (wave & 1) * 64 + lane;  // dims 2kw, 2kw+1
+  const bool sum_wave = (wave & 1) == 0;
   const int bx = blockIdx.x;
   const int hp = (bx >> 3) & 1, rest = (bx & 7) | ((bx >> 4) << 3);
   const int kvh = rest >> 6, c = rest & 63;
@@ -391,39 +390,43 @@ __global__ __launch_bounds__(256, 1) void k_attn_chain(AttnArgs a) {
   if (c >= C) return;
   const int L = n > c ? (n - 1 - c) / C + 1 : 0;
   const int h0 = 4 * kvh + 2 * hp;
-  float o0 = 0.0f, o1 = 0.0f, sum = 0.0f;
-  float carry = kFiniteMin;  // waves 2/3: running max of head wave-2
+  float oa = 0.0f, ob = 0.0f, sum = 0.0f;
+  float carry = kFiniteMin;  // exps waves: running max of their head
   if (L > 0) {
     const int nt = (L + kTile - 1) / kTile;
     const int sstride = score_stride(a.capacity);
     const uint16_t* vrow0 = a.vcache + ((size_t)kvh * a.capacity + c) * 256;
     const float* sc0 = a.scores + ((size_t)h0 * kAttnMaxChains + c) * sstride;
-    for (int T = 0; T < kStages - 1 && T < nt; ++T)
-      issue_tile(sm, vrow0, sc0, sstride, C, L, T, wave, lane);
-    // Every wave issues 9 operations per tile (8 V row pairs, 1 score part).
-    // Exps of tile 0 need tile 0 complete; tiles 1 and 2 may stay pending.
-    if (nt >= 3) wait_vm<18>(); else if (nt == 2) wait_vm<9>(); else wait_vm<0>();
+    if (producer) {
+      for (int T = 0; T < kStages - 1 && T < nt; ++T) issue_tile(sm, vrow0, sc0, sstride, C, L, T, lane);
+      // tile 0 complete; tiles 1 and 2 may stay pending (at most 63 operations
+      // are ever outstanding, and loads complete in order)
+      if (nt >= 3) wait_vm<63>(); else if (nt == 2) wait_vm<kTileOps>(); else wait_vm<0>();
+    }
     lds_barrier();
-    if (wave >= 2) tile_exps(sm, 0, L, wave - 2, lane, carry);
+    if (!producer && !sum_wave) tile_exps(sm, 0, L, hh, lane, carry);
     for (int T = 0; T < nt; ++T) {
-      // Tiles up to T+1 complete (V of T, scores of T+1); tile T+2 may pend.
-      if (T + 2 < nt) wait_vm<9>(); else wait_vm<0>();
+      // tiles up to T+1 complete (V of T, scores of T+1); tile T+2 may pend
+      if (producer) {
+        if (T + 2 < nt) wait_vm<kTileOps>(); else wait_vm<0>();
+      }
       lds_barrier();
-      if (T + kStages - 1 < nt) issue_tile(sm, vrow0, sc0, sstride, C, L, T + kStages - 1, wave, lane);
-      if (wave >= 2 && T + 1 < nt) tile_exps(sm, T + 1, L, wave - 2, lane, carry);
-      if (wave == 0)
-        run_tile<true, 0>(sm, T, t, o0, o1, sum);
-      else if (wave == 1)
-        run_tile<true, 1>(sm, T, t, o0, o1, sum);
-      else
-        run_tile<false, 0>(sm, T, t, o0, o1, sum);
+      if (producer) {
+        if (T + kStages - 1 < nt) issue_tile(sm, vrow0, sc0, sstride, C, L, T + kStages - 1, lane);
+      } else if (sum_wave) {
+        run_tile<true>(sm, T, hh, kw, oa, ob, sum);
+      } else {
+        if (T + 1 < nt) tile_exps(sm, T + 1, L, hh, lane, carry);
+        run_tile<false>(sm, T, hh, kw, oa, ob, sum);
+      }
     }
   }
-  a.part_o[((size_t)h0 * kAttnMaxChains + c) * 256 + t] = o0;
-  a.part_o[((size_t)(h0 + 1) * kAttnMaxChains + c) * 256 + t] = o1;
+  if (producer) return;
+  float* po = a.part_o + ((size_t)(h0 + hh) * kAttnMaxChains + c) * 256 + 2 * kw;
+  *reinterpret_cast<float2*>(po) = make_float2(oa, ob);
   if (lane == 0) {
-    float* ml = a.part_ml + ((size_t)(h0 + (wave & 1)) * kAttnMaxChains + c) * 2;
-    if (wave < 2) ml[1] = sum;
+    float* ml = a.part_ml + ((size_t)(h0 + hh) * kAttnMaxChains + c) * 2;
+    if (sum_wave) ml[1] = sum;
     else ml[0] = carry;
   }
 }
@@ -525,7 +528,7 @@ hipError_t launch_attn_scores(const AttnArgs& a, hipStream_t s) {
 
 hipError_t launch_attn_chain(const AttnArgs& a, hipStream_t s) {
   if (!attn_ok(a)) return hipErrorInvalidValue;
-  hipLaunchKernelGGL(k_attn_chain, dim3(kKvHeads * kAttnMaxChains * 2), dim3(256), 0, s, a);
+  hipLaunchKernelGGL(k_attn_chain, dim3(kKvHeads * kAttnMaxChains * 2), dim3(320), 0, s, a);
   return hipGetLastError();
 }
 
