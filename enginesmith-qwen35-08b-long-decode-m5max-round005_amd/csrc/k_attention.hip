@@ -301,7 +301,7 @@ __device__ __forceinline__ void tile_exps(ChainSmem& sm, int T, int L, int head,
 // waves also keep the head's sum. Steps past the chain's end have e = 0 and
 // f = 1 and change nothing (o is never -0, V rows are finite). One dword
 // read gives both dims' bf16 values (two rows per LDS read pair); exp scores
-// come 4 steps per read. Batches of 4 steps are software-pipelined two deep.
+// come 4 steps per read. Batches of 4 steps are software-pipelined three deep.
 constexpr int kBatch = 4;
 
 template <bool SLOW>
@@ -349,13 +349,14 @@ __device__ __forceinline__ void chain_steps(const ChainSmem& sm, int T, int hh, 
                                             float& ob, float& sum) {
   const int st = T % kStages, b = T & 1;
   constexpr int nb = kTile / kBatch;
-  Batch<SLOW> x[3];
-  load_batch<SLOW>(sm, st, b, hh, kw, 0, x[0]);
-  load_batch<SLOW>(sm, st, b, hh, kw, 1, x[1]);
+  constexpr int ahead = 3;  // batches in flight ahead of the one computed
+  Batch<SLOW> x[ahead + 1];
+#pragma unroll
+  for (int q = 0; q < ahead; ++q) load_batch<SLOW>(sm, st, b, hh, kw, q, x[q]);
 #pragma unroll
   for (int q = 0; q < nb; ++q) {
-    if (q + 2 < nb) load_batch<SLOW>(sm, st, b, hh, kw, q + 2, x[(q + 2) % 3]);
-    run_batch<SLOW, SUM>(x[q % 3], oa, ob, sum);
+    if (q + ahead < nb) load_batch<SLOW>(sm, st, b, hh, kw, q + ahead, x[(q + ahead) % (ahead + 1)]);
+    run_batch<SLOW, SUM>(x[q % (ahead + 1)], oa, ob, sum);
   }
 }
 
