@@ -193,8 +193,12 @@ __device__ __forceinline__ float q4_dot32(const u32x4 c, const float* xr) {
 #pragma unroll
   for (int w = 0; w < 4; ++w) {
     const uint32_t word = c[w];
-    const uint32_t lo = word & 0x0F0F0F0Fu;
-    const uint32_t hi = word & 0xF0F0F0F0u;
+    uint32_t lo = word & 0x0F0F0F0Fu;
+    uint32_t hi = word & 0xF0F0F0F0u;
+    // Opaque to known-bits analysis, so each byte converts with one
+    // v_cvt_f32_ubyteN instead of a separate nibble extract per element.
+    asm("" : "+v"(lo));
+    asm("" : "+v"(hi));
     a0 = fmaf(xr[8 * w + 0], (float)(lo & 0xffu), a0);
     a1 = fmaf(xr[8 * w + 1], (float)(hi & 0xffu), a1);
     a0 = fmaf(xr[8 * w + 2], (float)((lo >> 8) & 0xffu), a0);
@@ -226,6 +230,30 @@ __device__ __forceinline__ void load_bf16x32(const uint16_t* p, float* out) {
     }
   }
 }
+
+// Raw 64-byte slice (32 bf16) as four 16-byte words, for loads issued early.
+struct Raw64 {
+  u32x4 q[4];
+};
+
+__device__ __forceinline__ Raw64 load_raw64(const uint16_t* p) {
+  const u32x4* q = reinterpret_cast<const u32x4*>(p);
+  return Raw64{{q[0], q[1], q[2], q[3]}};
+}
+
+__device__ __forceinline__ void unpack_bf16x32(const Raw64& r, float* out) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      out[8 * i + 2 * j] = bf_lo(r.q[i][j]);
+      out[8 * i + 2 * j + 1] = bf_hi(r.q[i][j]);
+    }
+}
+
+// Keeps the machine scheduler from moving instructions across this point, so
+// loads issued above it are in flight before the arithmetic below starts.
+__device__ __forceinline__ void issue_fence() { __builtin_amdgcn_sched_barrier(0); }
 
 // Register form of a slice for q4_dot32; returns the sequential sum of x.
 __device__ __forceinline__ float prep_slice(const float* x, float* xr) {
@@ -265,5 +293,6 @@ struct StepState {
 __device__ __forceinline__ int load_pos(const StepState* st, int pos_val) {
   return st ? st->pos : pos_val;
 }
+
 
 }  // namespace es

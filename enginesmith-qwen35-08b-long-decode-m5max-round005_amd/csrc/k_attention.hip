@@ -36,10 +36,8 @@ namespace {
 constexpr float kFiniteMin = -3.40282346638528859812e38f;
 
 // Normalise 4 consecutive dims of a 256-wide head held by a full wave.
-__device__ __forceinline__ void head_norm4(const uint16_t* x, const uint16_t* gain, int lane,
-                                           float* out) {
-  const uint2 xv = *reinterpret_cast<const uint2*>(x + lane * 4);
-  const uint2 gv = *reinterpret_cast<const uint2*>(gain + lane * 4);
+// xv, gv: the lane's 4 bf16 values of the head and of the gain.
+__device__ __forceinline__ void head_norm4(const uint2 xv, const uint2 gv, float* out) {
   const float xf[4] = {bf_lo(xv.x), bf_hi(xv.x), bf_lo(xv.y), bf_hi(xv.y)};
   const float gf[4] = {bf_lo(gv.x), bf_hi(gv.x), bf_lo(gv.y), bf_hi(gv.y)};
   float ss = 0.0f;
@@ -53,10 +51,11 @@ __device__ __forceinline__ void head_norm4(const uint16_t* x, const uint16_t* ga
 
 // Rotary component d of a normalised head (attention.metal:55-70):
 // d < 32: fma(lo, c, -(hi*s)); 32 <= d < 64: fma(lo, s, hi*c).
-__device__ __forceinline__ float rope_at(const float* nrm, int d, int pos, const float* inv_freq) {
+// inv is inv_freq[d & 31] (read by the caller, only used for d < 64).
+__device__ __forceinline__ float rope_at(const float* nrm, int d, int pos, float inv) {
   if (d >= 64) return nrm[d];
   const int pair = d & 31;
-  const float angle = (float)pos * inv_freq[pair];
+  const float angle = (float)pos * inv;
   float s, c;
   es_sincos(angle, &s, &c);
   const float lo = nrm[pair], hi = nrm[pair + 32];
@@ -87,12 +86,15 @@ __host__ __device__ __forceinline__ int score_stride(int capacity) {
 
 __device__ __forceinline__ int route_chains(int n) { return n < kAttnRouteSplit ? 32 : 64; }
 
+constexpr int kRing = 4;  // K-row register slots per lane in k_attn_scores
+
 __global__ __launch_bounds__(256, 2) void k_attn_scores(AttnArgs a) {
   __shared__ float nrm[5][256];     // normalised q heads 0..3, new k
   __shared__ float qs[4][256];      // roped q * 1/16
   __shared__ u32x4 knew[32];        // new K row (roped, bf16)
 
-  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+  // wave is uniform; readfirstlane lets the compiler keep the item loop scalar.
+  const int t = threadIdx.x, lane = t & 63, wave = __builtin_amdgcn_readfirstlane(t >> 6);
   const int g = blockIdx.y, B = gridDim.x;
   const int pos = load_pos(a.st, a.pos_val);
   const int n = pos + 1;
@@ -111,28 +113,48 @@ __global__ __launch_bounds__(256, 2) void k_attn_scores(AttnArgs a) {
   const uint16_t* kb = a.kcache + (size_t)g * a.capacity * 256 + 8 * m;
   // Lane group grp takes step r = grp of the item; wave w takes items
   // ib0 + w, ib0 + w + 4, ...
+  const int lc = C == 32 ? 5 : 6;  // log2 C
   auto item_pos = [&](int i, int& p) {
-    p = i % C + C * (8 * (i / C) + grp);
+    p = (i & (C - 1)) + ((8 * (i >> lc) + grp) << lc);
     return p < n;
   };
-  // First K rows, issued before the prologue so their latency overlaps it.
-  u32x4 kc[4] = {}, kn[4] = {};
-  int i = ib0 + wave, p;
-  bool ok = i < ib1 && item_pos(i, p);
-  if (ok && p != pos) {
-    const u32x4* r = reinterpret_cast<const u32x4*>(kb + (size_t)p * 256);
+  // Prologue inputs, read before the K ring so that waiting for them does not
+  // wait for K (vector-memory counters complete in order).
+  const uint2 qx = *reinterpret_cast<const uint2*>(a.q_proj + (4 * g + wave) * 512 + lane * 4);
+  const uint2 qg = *reinterpret_cast<const uint2*>(a.q_gain + lane * 4);
+  const uint2 kx = *reinterpret_cast<const uint2*>(a.k_proj + g * 256 + lane * 4);
+  const uint2 kg = *reinterpret_cast<const uint2*>(a.k_gain + lane * 4);
+  const uint2 vx = *reinterpret_cast<const uint2*>(a.v_proj + g * 256 + lane * 4);
+  float inv[4];
 #pragma unroll
-    for (int x = 0; x < 4; ++x) kc[x] = r[8 * x];
-  }
+  for (int x = 0; x < 4; ++x) inv[x] = a.inv_freq[((lane * 4) & 31) + x];
+  // Wave w takes items ib0 + w + 4*it, it = 0 .. nit-1. K rows stream
+  // through a ring of kRing register slots, kRing - 1 items in flight while
+  // one is computed; the first kRing - 1 are issued before the prologue so
+  // their latency overlaps it. Loads are unconditional: an item past the end
+  // reads row 0 and the new position's row (written by this kernel) is read
+  // but replaced by the LDS copy, so no branch holds a load back.
+  const int nit = ib1 - ib0 > wave ? (ib1 - ib0 - wave + 3) / 4 : 0;
+  u32x4 kr[kRing][4];
+  int pr[kRing];
+  bool okr[kRing];
+  auto issue = [&](int it, u32x4* dst, int& pp, bool& okk) {
+    okk = it < nit && item_pos(ib0 + wave + 4 * it, pp);
+    const u32x4* r = reinterpret_cast<const u32x4*>(kb + (size_t)(okk ? pp : 0) * 256);
+#pragma unroll
+    for (int x = 0; x < 4; ++x) dst[x] = r[8 * x];
+  };
+#pragma unroll
+  for (int u = 0; u < kRing - 1; ++u) issue(u, kr[u], pr[u], okr[u]);
 
   // ---- prologue: q (and, in the owner block, the new k/v rows) ----
   {
     float o4[4];
-    head_norm4(a.q_proj + (4 * g + wave) * 512, a.q_gain, lane, o4);
+    head_norm4(qx, qg, o4);
 #pragma unroll
     for (int x = 0; x < 4; ++x) nrm[wave][lane * 4 + x] = o4[x];
     if (owner && wave == 0) {
-      head_norm4(a.k_proj + g * 256, a.k_gain, lane, o4);
+      head_norm4(kx, kg, o4);
 #pragma unroll
       for (int x = 0; x < 4; ++x) nrm[4][lane * 4 + x] = o4[x];
     }
@@ -141,7 +163,7 @@ __global__ __launch_bounds__(256, 2) void k_attn_scores(AttnArgs a) {
   {
     float r[4];
 #pragma unroll
-    for (int x = 0; x < 4; ++x) r[x] = rope_at(nrm[wave], lane * 4 + x, pos, a.inv_freq);
+    for (int x = 0; x < 4; ++x) r[x] = rope_at(nrm[wave], lane * 4 + x, pos, inv[x]);
     if (a.query_out && blockIdx.x == 0) {
       uint16_t* qo = a.query_out + (4 * g + wave) * 256 + lane * 4;
       *reinterpret_cast<uint2*>(qo) = make_uint2(pack_bf2(r[0], r[1]), pack_bf2(r[2], r[3]));
@@ -151,7 +173,7 @@ __global__ __launch_bounds__(256, 2) void k_attn_scores(AttnArgs a) {
     if (owner && wave == 1) {
       float kr[4];
 #pragma unroll
-      for (int x = 0; x < 4; ++x) kr[x] = rope_at(nrm[4], lane * 4 + x, pos, a.inv_freq);
+      for (int x = 0; x < 4; ++x) kr[x] = rope_at(nrm[4], lane * 4 + x, pos, inv[x]);
       const uint32_t k0 = pack_bf2(kr[0], kr[1]);
       const uint32_t k1 = pack_bf2(kr[2], kr[3]);
       uint32_t* kw = reinterpret_cast<uint32_t*>(knew);
@@ -159,8 +181,7 @@ __global__ __launch_bounds__(256, 2) void k_attn_scores(AttnArgs a) {
       kw[lane * 2 + 1] = k1;
       const size_t ci = ((size_t)g * a.capacity + pos) * 256 + lane * 4;
       *reinterpret_cast<uint2*>(a.kcache + ci) = make_uint2(k0, k1);
-      *reinterpret_cast<uint2*>(a.vcache + ci) =
-          *reinterpret_cast<const uint2*>(a.v_proj + g * 256 + lane * 4);
+      *reinterpret_cast<uint2*>(a.vcache + ci) = vx;
     }
   }
   __syncthreads();
@@ -176,34 +197,29 @@ __global__ __launch_bounds__(256, 2) void k_attn_scores(AttnArgs a) {
 
   const int sstride = score_stride(a.capacity);
   float* sc = a.scores + (size_t)(4 * g + (m & 3)) * kAttnMaxChains * sstride;
-  for (; i < ib1; i += 4) {
-    int pn;
-    const bool okn = i + 4 < ib1 && item_pos(i + 4, pn);
-    if (okn && pn != pos) {
-      const u32x4* r = reinterpret_cast<const u32x4*>(kb + (size_t)pn * 256);
+  for (int it0 = 0; it0 < nit; it0 += kRing) {
 #pragma unroll
-      for (int x = 0; x < 4; ++x) kn[x] = r[8 * x];
+    for (int u = 0; u < kRing; ++u) {
+      const int it = it0 + u;  // items past nit compute on row 0 and store nothing
+      const int nx = (u + kRing - 1) % kRing;  // slot freed by the previous item
+      issue(it + kRing - 1, kr[nx], pr[nx], okr[nx]);
+      u32x4 kc[4];
+#pragma unroll
+      for (int x = 0; x < 4; ++x) kc[x] = okr[u] && pr[u] == pos ? knew[m + 8 * x] : kr[u][x];
+      float s[4];
+#pragma unroll
+      for (int hh = 0; hh < 4; ++hh) {
+        const float p0 = chunk_dot(q[hh][0], kc[0]);
+        const float p1 = chunk_dot(q[hh][1], kc[1]);
+        const float p2 = chunk_dot(q[hh][2], kc[2]);
+        const float p3 = chunk_dot(q[hh][3], kc[3]);
+        s[hh] = tree8((p0 + p1) + (p2 + p3));
+      }
+      const int hm = m & 3;
+      const float mine = hm == 0 ? s[0] : hm == 1 ? s[1] : hm == 2 ? s[2] : s[3];
+      const int p = pr[u];
+      if (okr[u] && m < 4) sc[(size_t)(p & (C - 1)) * sstride + (p >> lc)] = mine;
     }
-    if (ok && p == pos) {
-#pragma unroll
-      for (int x = 0; x < 4; ++x) kc[x] = knew[m + 8 * x];
-    }
-    float s[4];
-#pragma unroll
-    for (int hh = 0; hh < 4; ++hh) {
-      const float p0 = chunk_dot(q[hh][0], kc[0]);
-      const float p1 = chunk_dot(q[hh][1], kc[1]);
-      const float p2 = chunk_dot(q[hh][2], kc[2]);
-      const float p3 = chunk_dot(q[hh][3], kc[3]);
-      s[hh] = tree8((p0 + p1) + (p2 + p3));
-    }
-    const int hm = m & 3;
-    const float mine = hm == 0 ? s[0] : hm == 1 ? s[1] : hm == 2 ? s[2] : s[3];
-    if (ok && m < 4) sc[(size_t)(p % C) * sstride + p / C] = mine;
-#pragma unroll
-    for (int x = 0; x < 4; ++x) kc[x] = kn[x];
-    ok = okn;
-    p = pn;
   }
 }
 

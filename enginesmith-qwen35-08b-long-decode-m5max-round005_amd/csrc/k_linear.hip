@@ -34,14 +34,42 @@ __device__ __forceinline__ void store_bf16x32(uint16_t* p, const float* v) {
 // RMSNorm of a K=1024 vector whose 32-element slice `sl` this lane holds; the
 // 32 lanes of a half-wave cover the vector once (rms_norm_bf16 arithmetic,
 // linear.metal:311-329: fp32 sum of squares, bf16(bf16(x*inv)*gain)).
-__device__ __forceinline__ void norm_slice_1024(const float* xv, const uint16_t* gain, int sl,
-                                                float* xn) {
+__device__ __forceinline__ void norm_slice_1024(const float* xv, const Raw64& gain, float* xn) {
   const float ss = tree32(sumsq32(xv));
   const float inv = 1.0f / sqrtf(ss / 1024.0f + 1e-6f);
   float gv[32];
-  load_bf16x32(gain + sl * 32, gv);
+  unpack_bf16x32(gain, gv);
 #pragma unroll
   for (int j = 0; j < 32; ++j) xn[j] = rbf(rbf(xv[j] * inv) * gv[j]);
+}
+
+// The same RMSNorm computed once per 256-thread block: every lane forms the
+// inverse RMS from its own slice (same order as above), thread t normalises
+// elements 4t..4t+3 (x4, g4: their bf16 values) into LDS, and after the
+// barrier each lane reads back its 32-element slice. Slice k sits at
+// xs_lds[36k ..] so that the 16-byte reads of a half-wave spread over banks.
+constexpr int kNormLds = 32 * 36;
+__device__ __forceinline__ void norm_block_1024(const float* xv, uint2 x4, uint2 g4, float* lds,
+                                                float* xn) {
+  const float ss = tree32(sumsq32(xv));
+  const float inv = 1.0f / sqrtf(ss / 1024.0f + 1e-6f);
+  const int t = threadIdx.x;
+  const float xe[4] = {bf_lo(x4.x), bf_hi(x4.x), bf_lo(x4.y), bf_hi(x4.y)};
+  const float ge[4] = {bf_lo(g4.x), bf_hi(g4.x), bf_lo(g4.y), bf_hi(g4.y)};
+  float4 o;
+  o.x = rbf(rbf(xe[0] * inv) * ge[0]);
+  o.y = rbf(rbf(xe[1] * inv) * ge[1]);
+  o.z = rbf(rbf(xe[2] * inv) * ge[2]);
+  o.w = rbf(rbf(xe[3] * inv) * ge[3]);
+  *reinterpret_cast<float4*>(lds + (t >> 3) * 36 + (t & 7) * 4) = o;
+  __syncthreads();
+  const int sl = threadIdx.x & 31;
+  const float4* r = reinterpret_cast<const float4*>(lds + sl * 36);
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const float4 v = r[i];
+    xn[4 * i] = v.x; xn[4 * i + 1] = v.y; xn[4 * i + 2] = v.z; xn[4 * i + 3] = v.w;
+  }
 }
 
 // Dequantised embedding slice (embedding_q4, linear.metal:20-23).
@@ -72,7 +100,7 @@ struct MultiDev {
   int pos_val;
 };
 
-template <int P>
+template <int P, bool EMBED>
 __global__ __launch_bounds__(256) void k_norm_multi(MultiDev a) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, half = lane >> 5, sl = lane & 31;
   // Weight loads first: they do not depend on the input, so their latency
@@ -84,23 +112,20 @@ __global__ __launch_bounds__(256) void k_norm_multi(MultiDev a) {
 #pragma unroll
   for (int p = 0; p < P; ++p) {
     const int r = base + 2 * p + half;
+    // Row r of the concatenation -> (matrix m, local row), without branches so
+    // that every load below is issued before the first wait.
     int local = r < a.total ? r : 0;
     int m = 0;
-    const uint32_t* w = a.m[0].w;
-    const uint16_t* s = a.m[0].s;
-    const uint16_t* b = a.m[0].b;
-    if (a.count > 1 && local >= a.m[0].n) {
-      local -= a.m[0].n; m = 1;
-      w = a.m[1].w; s = a.m[1].s; b = a.m[1].b;
-      if (a.count > 2 && local >= a.m[1].n) {
-        local -= a.m[1].n; m = 2;
-        w = a.m[2].w; s = a.m[2].s; b = a.m[2].b;
-        if (a.count > 3 && local >= a.m[2].n) {
-          local -= a.m[2].n; m = 3;
-          w = a.m[3].w; s = a.m[3].s; b = a.m[3].b;
-        }
-      }
+#pragma unroll
+    for (int i = 0; i < 3; ++i) {
+      const bool adv = m == i && i + 1 < a.count && local >= a.m[i].n;
+      local = adv ? local - a.m[i].n : local;
+      m = adv ? i + 1 : m;
     }
+    const Q4& q = a.m[0];
+    const uint32_t* w = m == 0 ? q.w : m == 1 ? a.m[1].w : m == 2 ? a.m[2].w : a.m[3].w;
+    const uint16_t* s = m == 0 ? q.s : m == 1 ? a.m[1].s : m == 2 ? a.m[2].s : a.m[3].s;
+    const uint16_t* b = m == 0 ? q.b : m == 1 ? a.m[1].b : m == 2 ? a.m[2].b : a.m[3].b;
     mi[p] = r < a.total ? m : -1;
     lr[p] = local;
     c[p] = *reinterpret_cast<const u32x4*>(w + (size_t)local * 128 + sl * 4);
@@ -108,22 +133,34 @@ __global__ __launch_bounds__(256) void k_norm_multi(MultiDev a) {
     bv[p] = b[(size_t)local * 16 + sl / 2];
   }
 
+  __shared__ float norm_lds[kNormLds];
+  const Raw64 graw = EMBED ? load_raw64(a.gain + sl * 32) : Raw64{};
+  const uint2 x4 = EMBED ? uint2{0u, 0u} : reinterpret_cast<const uint2*>(a.x)[threadIdx.x];
+  const uint2 g4 = EMBED ? uint2{0u, 0u} : reinterpret_cast<const uint2*>(a.gain)[threadIdx.x];
+  // Ring slot of the first output: the step's position (read early, used at the store).
+  int zero;
+  asm volatile("v_mov_b32 %0, 0" : "=v"(zero));
+  const int* pos_src = a.st ? &a.st->pos : reinterpret_cast<const int*>(a.gain);
+  const int pos_raw = pos_src[zero];
   float xv[32];
-  if (a.embed.w) {
+  if (EMBED) {
     const uint32_t tok = a.st ? a.st->token : a.token_val;
     embed_slice(a.embed, tok, sl, xv);
     if (a.h_out && blockIdx.x == 0 && threadIdx.x < 32) store_bf16x32(a.h_out + sl * 32, xv);
   } else {
-    load_bf16x32(a.x + sl * 32, xv);
+    const Raw64 xraw = load_raw64(a.x + sl * 32);
+    issue_fence();
+    unpack_bf16x32(xraw, xv);
   }
   float xn[32];
-  norm_slice_1024(xv, a.gain, sl, xn);
+  if (EMBED) norm_slice_1024(xv, graw, xn);
+  else norm_block_1024(xv, x4, g4, norm_lds, xn);
   if (a.norm_out && blockIdx.x == 0 && threadIdx.x < 32) store_bf16x32(a.norm_out + sl * 32, xn);
   float xr[32];
   const float xs = prep_slice(xn, xr);
 
   uint16_t* y0 = a.y[0];
-  if (a.ring0) y0 += (size_t)(load_pos(a.st, a.pos_val) & 3) * a.m[0].n;
+  if (a.ring0) y0 += (size_t)((a.st ? pos_raw : a.pos_val) & 3) * a.m[0].n;
 #pragma unroll
   for (int p = 0; p < P; ++p) {
     const float part = tree32(q4_slice(c[p], sv[p], bv[p], xr, xs));
@@ -158,10 +195,15 @@ __global__ __launch_bounds__(256) void k_norm_gate_up(Q4 gate, Q4 up, const uint
     su[p] = up.s[(size_t)rl * 16 + sl / 2];
     bu[p] = up.b[(size_t)rl * 16 + sl / 2];
   }
+  __shared__ float norm_lds[kNormLds];
+  const Raw64 xraw = load_raw64(x + sl * 32);
+  const uint2 x4 = reinterpret_cast<const uint2*>(x)[threadIdx.x];
+  const uint2 g4 = reinterpret_cast<const uint2*>(gain)[threadIdx.x];
+  issue_fence();
   float xv[32];
-  load_bf16x32(x + sl * 32, xv);
+  unpack_bf16x32(xraw, xv);
   float xn[32];
-  norm_slice_1024(xv, gain, sl, xn);
+  norm_block_1024(xv, x4, g4, norm_lds, xn);
   if (norm_out && blockIdx.x == 0 && threadIdx.x < 32) store_bf16x32(norm_out + sl * 32, xn);
   float xr[32];
   const float xs = prep_slice(xn, xr);
@@ -194,8 +236,16 @@ __global__ __launch_bounds__(256) void k_qmv_narrow(Q4 m, const uint16_t* x,
     sv[p] = m.s[(size_t)rl * 16 + sl / 2];
     bv[p] = m.b[(size_t)rl * 16 + sl / 2];
   }
+  uint32_t res[P];
+#pragma unroll
+  for (int p = 0; p < P; ++p) {
+    const int r = base + 2 * p + half;
+    res[p] = ADD ? residual[r < m.n ? r : 0] : 0u;
+  }
+  const Raw64 xraw = load_raw64(x + sl * 32);
+  issue_fence();
   float xv[32], xr[32];
-  load_bf16x32(x + sl * 32, xv);
+  unpack_bf16x32(xraw, xv);
   const float xs = prep_slice(xv, xr);
 #pragma unroll
   for (int p = 0; p < P; ++p) {
@@ -203,7 +253,7 @@ __global__ __launch_bounds__(256) void k_qmv_narrow(Q4 m, const uint16_t* x,
     const float part = tree32(q4_slice(c[p], sv[p], bv[p], xr, xs));
     if (sl == 0 && r < m.n) {
       if (y_f32) y_f32[r] = part;
-      if (ADD) y[r] = (uint16_t)f2bf(bf2f(residual[r]) + rbf(part));
+      if (ADD) y[r] = (uint16_t)f2bf(bf2f(res[p]) + rbf(part));
       else y[r] = (uint16_t)f2bf(part);
     }
   }
@@ -226,30 +276,34 @@ __global__ __launch_bounds__(256) void k_qmv_wide(Q4 m, const uint16_t* x,
   for (int p = 0; p < P; ++p) {
     const int r = base + p;
     const size_t rl = r < m.n ? r : 0;
+    // Slices past the row end (lanes >= K/32) load slice 0 and are masked below.
     c1[p] = *reinterpret_cast<const u32x4*>(m.w + rl * wpr + s1 * 4);
     sa[p] = m.s[rl * gpr + s1 / 2];
     ba[p] = m.b[rl * gpr + s1 / 2];
-    if (v2) {
-      c2[p] = *reinterpret_cast<const u32x4*>(m.w + rl * wpr + s2 * 4);
-      sb[p] = m.s[rl * gpr + s2 / 2];
-      bb[p] = m.b[rl * gpr + s2 / 2];
-    } else {
-      c2[p] = u32x4{0u, 0u, 0u, 0u};
-      sb[p] = 0u;
-      bb[p] = 0u;
-    }
+    c2[p] = *reinterpret_cast<const u32x4*>(m.w + rl * wpr + s2 * 4);
+    sb[p] = m.s[rl * gpr + s2 / 2];
+    bb[p] = m.b[rl * gpr + s2 / 2];
   }
+  uint32_t res[P];
+#pragma unroll
+  for (int p = 0; p < P; ++p) {
+    const int r = base + p;
+    res[p] = ADD ? residual[r < m.n ? r : 0] : 0u;
+  }
+  const Raw64 xa = load_raw64(x + s1 * 32);
+  const Raw64 xb = load_raw64(x + s2 * 32);
+  issue_fence();
   float xv[32], xr1[32], xr2[32];
   float xs1 = 0.0f, xs2 = 0.0f;
   if (v1) {
-    load_bf16x32(x + lane * 32, xv);
+    unpack_bf16x32(xa, xv);
     xs1 = prep_slice(xv, xr1);
   } else {
 #pragma unroll
     for (int j = 0; j < 32; ++j) xr1[j] = 0.0f;
   }
   if (v2) {
-    load_bf16x32(x + (lane + 64) * 32, xv);
+    unpack_bf16x32(xb, xv);
     xs2 = prep_slice(xv, xr2);
   } else {
 #pragma unroll
@@ -258,13 +312,14 @@ __global__ __launch_bounds__(256) void k_qmv_wide(Q4 m, const uint16_t* x,
 #pragma unroll
   for (int p = 0; p < P; ++p) {
     const int r = base + p;
-    float part = 0.0f;
-    if (v1) part = q4_slice(c1[p], sa[p], ba[p], xr1, xs1);
-    if (v2) part = part + q4_slice(c2[p], sb[p], bb[p], xr2, xs2);
+    const float p1 = q4_slice(c1[p], sa[p], ba[p], xr1, xs1);
+    const float p2 = q4_slice(c2[p], sb[p], bb[p], xr2, xs2);
+    float part = v1 ? p1 : 0.0f;
+    if (v2) part = part + p2;
     part = tree64(part);
     if (lane == 0 && r < m.n) {
       if (y_f32) y_f32[r] = part;
-      if (ADD) y[r] = (uint16_t)f2bf(bf2f(residual[r]) + rbf(part));
+      if (ADD) y[r] = (uint16_t)f2bf(bf2f(res[p]) + rbf(part));
       else y[r] = (uint16_t)f2bf(part);
     }
   }
@@ -291,11 +346,18 @@ __global__ __launch_bounds__(256) void k_gdn_gate_out(Q4 m, const uint16_t* y, c
     sv[p] = m.s[rl * 32 + lane / 2];
     bv[p] = m.b[rl * 32 + lane / 2];
   }
+  uint32_t res[P];
+#pragma unroll
+  for (int p = 0; p < P; ++p) {
+    const int r = base + p;
+    res[p] = h[r < m.n ? r : 0];
+  }
   {
     const int e0 = (t >> 4) * 128 + (t & 15) * 8;  // head t/16, eight channels
     const u32x4 yv = *reinterpret_cast<const u32x4*>(y + e0);
     const u32x4 zv = *reinterpret_cast<const u32x4*>(z + e0);
     const u32x4 wv = *reinterpret_cast<const u32x4*>(norm_w + (t & 15) * 8);
+    issue_fence();
     float yf[8], zf[8], wf[8];
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
@@ -333,7 +395,7 @@ __global__ __launch_bounds__(256) void k_gdn_gate_out(Q4 m, const uint16_t* y, c
   for (int p = 0; p < P; ++p) {
     const int r = base + p;
     const float part = tree64(q4_slice(c[p], sv[p], bv[p], xr, xs));
-    if (lane == 0 && r < m.n) h[r] = (uint16_t)f2bf(bf2f(h[r]) + rbf(part));
+    if (lane == 0 && r < m.n) h[r] = (uint16_t)f2bf(bf2f(res[p]) + rbf(part));
   }
 }
 
@@ -384,7 +446,10 @@ hipError_t launch_norm_multi(const NormMultiArgs& a, hipStream_t s) {
   d.pos_val = a.pos_val;
   const int rows_per_block = 4 * 2 * kMultiP;
   const int blocks = (total + rows_per_block - 1) / rows_per_block;
-  hipLaunchKernelGGL(k_norm_multi<kMultiP>, dim3(blocks), dim3(256), 0, s, d);
+  if (a.embed.w)
+    hipLaunchKernelGGL((k_norm_multi<kMultiP, true>), dim3(blocks), dim3(256), 0, s, d);
+  else
+    hipLaunchKernelGGL((k_norm_multi<kMultiP, false>), dim3(blocks), dim3(256), 0, s, d);
   return hipGetLastError();
 }
 
