@@ -274,6 +274,38 @@ __device__ __forceinline__ float sumsq32(const float* x) {
   return ss;
 }
 
+// RMSNorm of a K=1024 vector (rms_norm_bf16 arithmetic, linear.metal:311-329:
+// fp32 sum of squares, bf16(bf16(x*inv)*gain)) computed once per 256-thread
+// block. Every lane holds a 32-element slice (lane & 31) in xv and forms the
+// inverse RMS from it: a sequential fma chain of squares over the slice, then
+// tree32 over the 32 slices. Thread t normalises elements 4t..4t+3 (x4, g4:
+// their bf16 values) into LDS, and after the barrier each lane reads back its
+// slice. Slice k sits at lds[36k ..] so that the 16-byte reads of a half-wave
+// spread over the banks.
+constexpr int kNormLds = 32 * 36;
+__device__ __forceinline__ void norm_block_1024(const float* xv, uint2 x4, uint2 g4, float* lds,
+                                                float* xn) {
+  const float ss = tree32(sumsq32(xv));
+  const float inv = 1.0f / sqrtf(ss / 1024.0f + 1e-6f);
+  const int t = threadIdx.x;
+  const float xe[4] = {bf_lo(x4.x), bf_hi(x4.x), bf_lo(x4.y), bf_hi(x4.y)};
+  const float ge[4] = {bf_lo(g4.x), bf_hi(g4.x), bf_lo(g4.y), bf_hi(g4.y)};
+  float4 o;
+  o.x = rbf(rbf(xe[0] * inv) * ge[0]);
+  o.y = rbf(rbf(xe[1] * inv) * ge[1]);
+  o.z = rbf(rbf(xe[2] * inv) * ge[2]);
+  o.w = rbf(rbf(xe[3] * inv) * ge[3]);
+  *reinterpret_cast<float4*>(lds + (t >> 3) * 36 + (t & 7) * 4) = o;
+  __syncthreads();
+  const int sl = threadIdx.x & 31;
+  const float4* r = reinterpret_cast<const float4*>(lds + sl * 36);
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const float4 v = r[i];
+    xn[4 * i] = v.x; xn[4 * i + 1] = v.y; xn[4 * i + 2] = v.z; xn[4 * i + 3] = v.w;
+  }
+}
+
 struct Q4 {
   const uint32_t* w;
   const uint16_t* s;

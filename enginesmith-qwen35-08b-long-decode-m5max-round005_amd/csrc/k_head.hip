@@ -37,15 +37,21 @@ struct HeadBatch {
   uint32_t s[kPassBatch], b[kPassBatch];
 };
 
-__device__ __forceinline__ void head_load(const Q4& e, int row0, int it, int half, int sl, int vocab,
+// Buffer resources over the codes, scales and biases of the table: rows past
+// the vocabulary are out of range and read as zero, so no row is clamped, and
+// the per-row offsets are immediates on one per-lane base offset.
+struct HeadRsrc {
+  __amdgpu_buffer_rsrc_t w, s, b;
+};
+
+__device__ __forceinline__ void head_load(const HeadRsrc& rs, int voff_c, int voff_s, int it,
                                           HeadBatch& hb) {
 #pragma unroll
   for (int p = 0; p < kPassBatch; ++p) {
-    const int r = row0 + it * 2 * kPassBatch + 2 * p + half;
-    const size_t rl = r < vocab ? r : 0;
-    hb.c[p] = *reinterpret_cast<const u32x4*>(e.w + rl * 128 + sl * 4);
-    hb.s[p] = e.s[rl * 16 + sl / 2];
-    hb.b[p] = e.b[rl * 16 + sl / 2];
+    const int dr = it * 2 * kPassBatch + 2 * p;  // rows past the lane's first row
+    hb.c[p] = __builtin_amdgcn_raw_buffer_load_b128(rs.w, voff_c + dr * 512, 0, 0);
+    hb.s[p] = __builtin_amdgcn_raw_buffer_load_b16(rs.s, voff_s + dr * 32, 0, 0);
+    hb.b[p] = __builtin_amdgcn_raw_buffer_load_b16(rs.b, voff_s + dr * 32, 0, 0);
   }
 }
 
@@ -53,24 +59,28 @@ __global__ __launch_bounds__(256) void k_head(HeadArgs a) {
   __shared__ float lg[kRowsPerBlock];
   __shared__ float wred[4];
   __shared__ float wred2[4];
+  __shared__ float norm_lds[kNormLds];
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6, half = lane >> 5, sl = lane & 31;
   const int vocab = a.embed.n;
   const int row0 = blockIdx.x * kRowsPerBlock + wave * 64;
+  const HeadRsrc rs{
+      __builtin_amdgcn_make_buffer_rsrc((void*)a.embed.w, 0, vocab * 512, 0x00020000),
+      __builtin_amdgcn_make_buffer_rsrc((void*)a.embed.s, 0, vocab * 32, 0x00020000),
+      __builtin_amdgcn_make_buffer_rsrc((void*)a.embed.b, 0, vocab * 32, 0x00020000)};
+  const int voff_c = (row0 + half) * 512 + sl * 16;
+  const int voff_s = (row0 + half) * 32 + (sl >> 1) * 2;
 
   HeadBatch cur, nxt;
-  head_load(a.embed, row0, 0, half, sl, vocab, cur);
+  head_load(rs, voff_c, voff_s, 0, cur);
 
   // normalised input slice (rms_norm_bf16 with the final norm gain)
+  const Raw64 xraw = load_raw64(a.h + sl * 32);
+  const uint2 x4 = reinterpret_cast<const uint2*>(a.h)[t];
+  const uint2 g4 = reinterpret_cast<const uint2*>(a.gain)[t];
+  issue_fence();
   float xv[32], xn[32], xr[32];
-  load_bf16x32(a.h + sl * 32, xv);
-  {
-    const float ss = tree32(sumsq32(xv));
-    const float inv = 1.0f / sqrtf(ss / 1024.0f + 1e-6f);
-    float gv[32];
-    load_bf16x32(a.gain + sl * 32, gv);
-#pragma unroll
-    for (int i = 0; i < 32; ++i) xn[i] = rbf(rbf(xv[i] * inv) * gv[i]);
-  }
+  unpack_bf16x32(xraw, xv);
+  norm_block_1024(xv, x4, g4, norm_lds, xn);
   if (a.norm_out && blockIdx.x == 0 && t < 32) {
 #pragma unroll
     for (int i = 0; i < 32; ++i) a.norm_out[sl * 32 + i] = (uint16_t)f2bf(xn[i]);
@@ -79,7 +89,7 @@ __global__ __launch_bounds__(256) void k_head(HeadArgs a) {
 
 #pragma unroll
   for (int it = 0; it < kBatches; ++it) {
-    if (it + 1 < kBatches) head_load(a.embed, row0, it + 1, half, sl, vocab, nxt);
+    if (it + 1 < kBatches) head_load(rs, voff_c, voff_s, it + 1, nxt);
 #pragma unroll
     for (int p = 0; p < kPassBatch; ++p) {
       const int local = wave * 64 + it * 2 * kPassBatch + 2 * p + half;
@@ -230,8 +240,9 @@ int head_blocks(int vocab) { return (vocab + kRowsPerBlock - 1) / kRowsPerBlock;
 size_t head_scratch_bytes(int vocab) { return (size_t)head_blocks(vocab) * 2 * sizeof(float); }
 
 hipError_t launch_head(const HeadArgs& a, hipStream_t s) {
-  if (!a.embed.w || !a.embed.s || !a.embed.b || a.embed.k != kHidden || a.embed.n <= 0 || !a.h ||
-      !a.gain || !a.logits || !a.part)
+  // vocab < 2^22 keeps every byte offset of the code table within 31 bits
+  if (!a.embed.w || !a.embed.s || !a.embed.b || a.embed.k != kHidden || a.embed.n <= 0 ||
+      a.embed.n >= (1 << 22) || !a.h || !a.gain || !a.logits || !a.part)
     return hipErrorInvalidValue;
   const int nb = head_blocks(a.embed.n);
   hipLaunchKernelGGL(k_head, dim3(nb), dim3(256), 0, s, a);

@@ -43,35 +43,6 @@ __device__ __forceinline__ void norm_slice_1024(const float* xv, const Raw64& ga
   for (int j = 0; j < 32; ++j) xn[j] = rbf(rbf(xv[j] * inv) * gv[j]);
 }
 
-// The same RMSNorm computed once per 256-thread block: every lane forms the
-// inverse RMS from its own slice (same order as above), thread t normalises
-// elements 4t..4t+3 (x4, g4: their bf16 values) into LDS, and after the
-// barrier each lane reads back its 32-element slice. Slice k sits at
-// xs_lds[36k ..] so that the 16-byte reads of a half-wave spread over banks.
-constexpr int kNormLds = 32 * 36;
-__device__ __forceinline__ void norm_block_1024(const float* xv, uint2 x4, uint2 g4, float* lds,
-                                                float* xn) {
-  const float ss = tree32(sumsq32(xv));
-  const float inv = 1.0f / sqrtf(ss / 1024.0f + 1e-6f);
-  const int t = threadIdx.x;
-  const float xe[4] = {bf_lo(x4.x), bf_hi(x4.x), bf_lo(x4.y), bf_hi(x4.y)};
-  const float ge[4] = {bf_lo(g4.x), bf_hi(g4.x), bf_lo(g4.y), bf_hi(g4.y)};
-  float4 o;
-  o.x = rbf(rbf(xe[0] * inv) * ge[0]);
-  o.y = rbf(rbf(xe[1] * inv) * ge[1]);
-  o.z = rbf(rbf(xe[2] * inv) * ge[2]);
-  o.w = rbf(rbf(xe[3] * inv) * ge[3]);
-  *reinterpret_cast<float4*>(lds + (t >> 3) * 36 + (t & 7) * 4) = o;
-  __syncthreads();
-  const int sl = threadIdx.x & 31;
-  const float4* r = reinterpret_cast<const float4*>(lds + sl * 36);
-#pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    const float4 v = r[i];
-    xn[4 * i] = v.x; xn[4 * i + 1] = v.y; xn[4 * i + 2] = v.z; xn[4 * i + 3] = v.w;
-  }
-}
-
 // Dequantised embedding slice (embedding_q4, linear.metal:20-23).
 __device__ __forceinline__ void embed_slice(const Q4& e, uint32_t tok, int sl, float* xv) {
   if (tok >= (uint32_t)e.n) tok = 0;  // ids come from validated prompts or the head's argmax

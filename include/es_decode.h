@@ -172,7 +172,7 @@ size_t es_head_scratch_bytes(int vocab);
 /* u = RMSNorm(h)*gain; logits[vocab] = bf16(E u) over the tied table;
  * lse = bf16(log(sum exp) + max) over the bf16 logits; *token = lowest index
  * of max bf16(logit - lse) (docs/protocol.md:44). token/lse are device
- * pointers; norm_out and lse are optional. */
+ * pointers; norm_out and lse are optional. vocab must be below 2^22. */
 int es_head_greedy(const es_q4* embed, const uint16_t* h, const uint16_t* gain,
                    uint16_t* norm_out, uint16_t* logits, void* scratch, size_t scratch_bytes,
                    uint32_t* token, float* lse, void* stream);
