@@ -16,12 +16,14 @@
 //   dims 8m+64i .. +7 (i = 0..3, 128 coalesced bytes per 8 lanes), one fma
 //   chain per 8 dims, (p[m]+p[m+8])+(p[m+16]+p[m+24]) in the lane and a DPP
 //   tree over the 8 lanes. Scores go to an fp32 array [8, capacity].
-// k_attn_chain, 256 blocks x 320 threads: block = (KV head, chain, query-head
-//   pair), thread = two adjacent value dims of one head, plus one data-moving
-//   wave. V rows and scores are staged in
-//   LDS by 16-byte global->LDS DMA, four 64-step tiles deep. Two waves turn
-//   the chain's scores into running max, factor and exp score one tile ahead
-//   (max scan by DPP, exp by the shared series). Per step o = fma(e, v, o*factor)
+// k_attn_chain, 256 blocks x 448 threads: block = (KV head, chain, query-head
+//   pair), thread = two adjacent value dims of one head (four compute waves),
+//   plus one data-moving wave and one exps wave per head. V rows and scores
+//   are staged in
+//   LDS by 16-byte global->LDS DMA, four 64-step tiles deep. The exps waves
+//   turn the chain's scores into running max, factor and exp score one tile ahead
+//   (max scan by DPP, exp by the shared series), which reach the compute
+//   lanes by DPP row broadcast. Per step o = fma(e, v, o*factor)
 //   and sum = sum*factor + e; when every factor of a tile is exactly 1 the
 //   products by 1 are skipped, which changes no bit.
 //   The two blocks of a (KV head, chain) sit on the same XCD (block ids b and
@@ -313,91 +315,138 @@ __device__ __forceinline__ void tile_exps(ChainSmem& sm, int T, int L, int head,
   carry = readlane63(mt);
 }
 
+// Exp scores and factors reach the compute waves through DPP: each lane
+// holds e[16r + (lane & 15)] for r = 0..3 (one 4-byte LDS read per r), and
+// step s = 16r + k uses row_newbcast:k, which gives every lane of a 16-lane
+// row the value of that row's lane k, as the first operand of the
+// arithmetic. The registers read this way are only ever written by LDS loads,
+// so no VALU-write-to-DPP-read wait states are needed.
+template <int K>
+__device__ __forceinline__ void fmac_bcast(float& acc, float e_row, float v) {
+  asm("v_fmac_f32_dpp %0, %1, %2 row_newbcast:%3 row_mask:0xf bank_mask:0xf"
+      : "+v"(acc) : "v"(e_row), "v"(v), "n"(K));
+}
+template <int K>
+__device__ __forceinline__ float mul_bcast(float f_row, float x) {
+  float r;
+  asm("v_mul_f32_dpp %0, %1, %2 row_newbcast:%3 row_mask:0xf bank_mask:0xf"
+      : "=v"(r) : "v"(f_row), "v"(x), "n"(K));
+  return r;
+}
+template <int K>
+__device__ __forceinline__ float add_bcast(float e_row, float x) {
+  float r;
+  asm("v_add_f32_dpp %0, %1, %2 row_newbcast:%3 row_mask:0xf bank_mask:0xf"
+      : "=v"(r) : "v"(e_row), "v"(x), "n"(K));
+  return r;
+}
+
+// One chain step of the two dims (va, vb) owned by this thread, exp score
+// and factor of step 16r + K broadcast from er / fr:
+// o = fma(e, v, o*f) and sum = sum*f + e, or with f == 1 for the whole tile
+// o = fma(e, v, o) and sum = sum + e (products by 1 skipped, same bits).
+template <int K, bool SLOW, bool SUM>
+__device__ __forceinline__ void chain_step(float er, float fr, float va, float vb, float& oa,
+                                           float& ob, float& sum) {
+  if (SLOW) {
+    oa = mul_bcast<K>(fr, oa);
+    ob = mul_bcast<K>(fr, ob);
+    if (SUM) sum = mul_bcast<K>(fr, sum);
+  }
+  fmac_bcast<K>(oa, er, va);
+  fmac_bcast<K>(ob, er, vb);
+  if (SUM) sum = add_bcast<K>(er, sum);
+}
+
+// Eight steps 8g .. 8g+7: the two dims of a step are one dword and the
+// loads pair rows 512 B apart into one LDS read (four reads per group).
+__device__ __forceinline__ void load_group(const uint32_t* vw, int kw, int g, uint32_t* w) {
+#pragma unroll
+  for (int i = 0; i < 8; ++i) w[i] = vw[(8 * g + i) * 128 + kw];
+}
+
+template <int G, bool SLOW, bool SUM>
+__device__ __forceinline__ void chain_group(const uint32_t* w, float er, float fr, float& oa,
+                                            float& ob, float& sum) {
+  constexpr int k0 = 8 * (G & 1);  // lane of the 16-lane row holding step 8G
+#define ES_STEP(I) chain_step<k0 + I, SLOW, SUM>(er, fr, bf_lo(w[I]), bf_hi(w[I]), oa, ob, sum)
+  ES_STEP(0); ES_STEP(1); ES_STEP(2); ES_STEP(3); ES_STEP(4); ES_STEP(5); ES_STEP(6); ES_STEP(7);
+#undef ES_STEP
+}
+
+// Groups G .. 7 of a tile: compute group G, then issue the loads of group
+// G + AHEAD into the slot it frees. LDS reads complete in order and at most
+// 15 may be outstanding (the counter's width), so a fast tile keeps three
+// groups in flight (plus two reads of exp scores) and a slow tile, which also
+// reads factors, two.
+template <int G, bool SLOW, bool SUM>
+__device__ __forceinline__ void chain_groups(const uint32_t* vw, int kw, const float* er,
+                                             const float* fr, uint32_t (&w)[4][8], float& oa,
+                                             float& ob, float& sum) {
+  if constexpr (G < 8) {
+    constexpr int ahead = SLOW ? 2 : 3;
+    chain_group<G, SLOW, SUM>(w[G % 4], er[G / 2], fr[G / 2], oa, ob, sum);
+    issue_fence();
+    if constexpr (G + ahead < 8) {
+      load_group(vw, kw, G + ahead, w[(G + ahead) % 4]);
+      issue_fence();
+    }
+    chain_groups<G + 1, SLOW, SUM>(vw, kw, er, fr, w, oa, ob, sum);
+  }
+}
+
 // 64 steps of the two adjacent dims owned by this thread for one head; SUM
 // waves also keep the head's sum. Steps past the chain's end have e = 0 and
-// f = 1 and change nothing (o is never -0, V rows are finite). One dword
-// read gives both dims' bf16 values (two rows per LDS read pair); exp scores
-// come 4 steps per read. Batches of 4 steps are software-pipelined three deep.
-constexpr int kBatch = 4;
-
-template <bool SLOW>
-struct Batch {
-  uint32_t w[kBatch];
-  float4 e;
-  float4 f;
-};
-
-template <bool SLOW>
-__device__ __forceinline__ void load_batch(const ChainSmem& sm, int st, int b, int hh, int kw,
-                                           int q, Batch<SLOW>& x) {
-  const uint32_t* vw = reinterpret_cast<const uint32_t*>(&sm.v[st][0][0]);
-#pragma unroll
-  for (int i = 0; i < kBatch; ++i) x.w[i] = vw[(kBatch * q + i) * 128 + kw];
-  x.e = reinterpret_cast<const float4*>(sm.e[b][hh])[q];
-  if (SLOW) x.f = reinterpret_cast<const float4*>(sm.f[b][hh])[q];
-}
-
-__device__ __forceinline__ float lane4(const float4& v, int i) {
-  return i == 0 ? v.x : i == 1 ? v.y : i == 2 ? v.z : v.w;
-}
-
+// f = 1 and change nothing (o is never -0, V rows are finite).
 template <bool SLOW, bool SUM>
-__device__ __forceinline__ void run_batch(const Batch<SLOW>& x, float& oa, float& ob, float& sum) {
-#pragma unroll
-  for (int i = 0; i < kBatch; ++i) {
-    const float va = bf_lo(x.w[i]), vb = bf_hi(x.w[i]);
-    const float e = lane4(x.e, i);
-    if (SLOW) {
-      const float f = lane4(x.f, i);
-      oa = fmaf(e, va, oa * f);
-      ob = fmaf(e, vb, ob * f);
-      if (SUM) sum = sum * f + e;
-    } else {
-      oa = fmaf(e, va, oa);
-      ob = fmaf(e, vb, ob);
-      if (SUM) sum = sum + e;
-    }
-  }
-}
-
-template <bool SLOW, bool SUM>
-__device__ __forceinline__ void chain_steps(const ChainSmem& sm, int T, int hh, int kw, float& oa,
-                                            float& ob, float& sum) {
+__device__ __forceinline__ void chain_tile(const ChainSmem& sm, int T, int hh, int kw, int lane,
+                                           float& oa, float& ob, float& sum) {
   const int st = T % kStages, b = T & 1;
-  constexpr int nb = kTile / kBatch;
-  constexpr int ahead = 3;  // batches in flight ahead of the one computed
-  Batch<SLOW> x[ahead + 1];
+  const uint32_t* vw = reinterpret_cast<const uint32_t*>(&sm.v[st][0][0]);
+  const float* ep = sm.e[b][hh] + (lane & 15);
+  const float* fp = sm.f[b][hh] + (lane & 15);
+  float er[4], fr[4];
 #pragma unroll
-  for (int q = 0; q < ahead; ++q) load_batch<SLOW>(sm, st, b, hh, kw, q, x[q]);
-#pragma unroll
-  for (int q = 0; q < nb; ++q) {
-    if (q + ahead < nb) load_batch<SLOW>(sm, st, b, hh, kw, q + ahead, x[(q + ahead) % (ahead + 1)]);
-    run_batch<SLOW, SUM>(x[q % (ahead + 1)], oa, ob, sum);
+  for (int r = 0; r < 4; ++r) {
+    er[r] = ep[16 * r];
+    fr[r] = SLOW ? fp[16 * r] : 1.0f;
   }
+  issue_fence();
+  uint32_t w[4][8];
+  constexpr int ahead = SLOW ? 2 : 3;
+#pragma unroll
+  for (int g = 0; g < ahead; ++g) load_group(vw, kw, g, w[g]);
+  issue_fence();
+  chain_groups<0, SLOW, SUM>(vw, kw, er, fr, w, oa, ob, sum);
 }
 
 template <bool SUM>
-__device__ __forceinline__ void run_tile(const ChainSmem& sm, int T, int hh, int kw, float& oa,
-                                         float& ob, float& sum) {
+__device__ __forceinline__ void run_tile(const ChainSmem& sm, int T, int hh, int kw, int lane,
+                                         float& oa, float& ob, float& sum) {
   if (sm.slow[T & 1][hh])
-    chain_steps<true, SUM>(sm, T, hh, kw, oa, ob, sum);
+    chain_tile<true, SUM>(sm, T, hh, kw, lane, oa, ob, sum);
   else
-    chain_steps<false, SUM>(sm, T, hh, kw, oa, ob, sum);
+    chain_tile<false, SUM>(sm, T, hh, kw, lane, oa, ob, sum);
 }
 
-// Block = (KV head, chain, query-head pair): waves 0,1 own head 0 and waves
-// 2,3 head 1, each thread two adjacent value dims; wave 4 only moves data
-// (global->LDS DMA), so the compute waves never wait on memory counters.
-// Per tile T: the producer waits until tiles up to T+1 are in LDS; barrier;
-// the producer issues tile T+3 into the stage tile T-1 used; waves 1 and 3
-// form the exps of tile T+1 for their head; all compute waves run tile T;
-// waves 0 and 2 keep their head's sum.
-__global__ __launch_bounds__(320, 1) void k_attn_chain(AttnArgs a) {
+// Block = (KV head, chain, query-head pair): compute waves 0,1 own head 0 and
+// 2,3 head 1, two adjacent value dims per thread. Wave 4 only moves data
+// (global->LDS DMA), so no compute wave waits on memory counters, and waves
+// 5 and 6 only turn head 0's and head 1's scores into exps, one tile ahead,
+// so that work runs beside the value steps instead of before them. Waves 0
+// and 3 also keep their head's sum (the SIMDs that host no exps wave). Per
+// tile T: the producer waits until tiles up to T+1 are in LDS; barrier; the
+// producer issues tile T+3 into the stage tile T-1 used; the exps waves form
+// the exps of tile T+1; the compute waves run tile T.
+constexpr int kChainThreads = 7 * 64;
+
+__global__ __launch_bounds__(kChainThreads, 1) void k_attn_chain(AttnArgs a) {
   __shared__ ChainSmem sm;
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
   const bool producer = wave == 4;
-  const int hh = (wave >> 1) & 1, kw = (wave & 1) * 64 + lane;  // dims 2kw, 2kw+1
-  const bool sum_wave = (wave & 1) == 0;
+  const bool exps_wave = wave >= 5;
+  const int hh = exps_wave ? wave - 5 : wave >> 1, kw = (wave & 1) * 64 + lane;  // dims 2kw, 2kw+1
+  const bool sum_wave = wave == 0 || wave == 3;
   const int bx = blockIdx.x;
   const int hp = (bx >> 3) & 1, rest = (bx & 7) | ((bx >> 4) << 3);
   const int kvh = rest >> 6, c = rest & 63;
@@ -420,32 +469,46 @@ __global__ __launch_bounds__(320, 1) void k_attn_chain(AttnArgs a) {
       // are ever outstanding, and loads complete in order)
       if (nt >= 3) wait_vm<63>(); else if (nt == 2) wait_vm<kTileOps>(); else wait_vm<0>();
     }
-    lds_barrier();
-    if (!producer && !sum_wave) tile_exps(sm, 0, L, hh, lane, carry);
-    for (int T = 0; T < nt; ++T) {
-      // tiles up to T+1 complete (V of T, scores of T+1); tile T+2 may pend
-      if (producer) {
+    // The producer keeps its DMA in flight across barriers (lds_barrier); the
+    // other waves have no vector-memory operations outstanding and use
+    // __syncthreads, whose waits the compiler tracks (an explicit wait that
+    // leaves DMA pending makes it drain every LDS read instead).
+    if (producer) lds_barrier(); else __syncthreads();
+    // One loop per role, each with one barrier per tile.
+    if (producer) {
+      for (int T = 0; T < nt; ++T) {
+        // tiles up to T+1 complete (V of T, scores of T+1); tile T+2 may pend
         if (T + 2 < nt) wait_vm<kTileOps>(); else wait_vm<0>();
-      }
-      lds_barrier();
-      if (producer) {
+        lds_barrier();
         if (T + kStages - 1 < nt) issue_tile(sm, vrow0, sc0, sstride, C, L, T + kStages - 1, lane);
-      } else if (sum_wave) {
-        run_tile<true>(sm, T, hh, kw, oa, ob, sum);
-      } else {
+      }
+    } else if (exps_wave) {
+      tile_exps(sm, 0, L, hh, lane, carry);
+      for (int T = 0; T < nt; ++T) {
+        __syncthreads();
         if (T + 1 < nt) tile_exps(sm, T + 1, L, hh, lane, carry);
-        run_tile<false>(sm, T, hh, kw, oa, ob, sum);
+      }
+    } else if (sum_wave) {
+      for (int T = 0; T < nt; ++T) {
+        __syncthreads();
+        run_tile<true>(sm, T, hh, kw, lane, oa, ob, sum);
+      }
+    } else {
+      for (int T = 0; T < nt; ++T) {
+        __syncthreads();
+        run_tile<false>(sm, T, hh, kw, lane, oa, ob, sum);
       }
     }
   }
   if (producer) return;
+  float* ml = a.part_ml + ((size_t)(h0 + hh) * kAttnMaxChains + c) * 2;
+  if (exps_wave) {
+    if (lane == 0) ml[0] = carry;
+    return;
+  }
   float* po = a.part_o + ((size_t)(h0 + hh) * kAttnMaxChains + c) * 256 + 2 * kw;
   *reinterpret_cast<float2*>(po) = make_float2(oa, ob);
-  if (lane == 0) {
-    float* ml = a.part_ml + ((size_t)(h0 + hh) * kAttnMaxChains + c) * 2;
-    if (sum_wave) ml[1] = sum;
-    else ml[0] = carry;
-  }
+  if (sum_wave && lane == 0) ml[1] = sum;
 }
 
 // ---- merge + gate ----
@@ -545,7 +608,7 @@ hipError_t launch_attn_scores(const AttnArgs& a, hipStream_t s) {
 
 hipError_t launch_attn_chain(const AttnArgs& a, hipStream_t s) {
   if (!attn_ok(a)) return hipErrorInvalidValue;
-  hipLaunchKernelGGL(k_attn_chain, dim3(kKvHeads * kAttnMaxChains * 2), dim3(320), 0, s, a);
+  hipLaunchKernelGGL(k_attn_chain, dim3(kKvHeads * kAttnMaxChains * 2), dim3(kChainThreads), 0, s, a);
   return hipGetLastError();
 }
 
