@@ -26,10 +26,11 @@ HBM_PEAK = 8.0e12
 GDN_STATE_BYTES = 18 * 2 * 16 * 128 * 128 * 4      # fp32 state read + write
 CONV_HISTORY_BYTES = 18 * 73728                      # history read + write (reference byte model)
 KV_BYTES_PER_POS = 6 * 2 * 2 * 256 * 2               # 6 layers x {K,V} x 2 heads x 256 x bf16
-# k_attn_chain per attended position: V rows of 2 heads (1024 B) + 8 fp32
-# scores (32 B); per launch: chain outputs and (max, sum) written.
-CHAIN_BYTES_PER_POS = 2 * 256 * 2 + 8 * 4
-CHAIN_FIXED_BYTES = 8 * 64 * (256 + 2) * 4
+# k_attn_fused per attended position: K and V rows of the 2 KV heads
+# (2048 B); per launch: q|gate, k and v projections read, the new K/V rows
+# written, chain outputs and (max, sum) written.
+FUSED_BYTES_PER_POS = 2 * 2 * 256 * 2
+FUSED_FIXED_BYTES = 8 * 512 * 2 + 2 * 2 * 256 * 2 + 2 * 2 * 256 * 2 + 8 * 64 * (256 + 2) * 4
 PROFILES = os.path.join(ROOT, "profiles")
 
 
@@ -130,14 +131,14 @@ def main():
         print(f"# ctx {ctx}: {tps:.1f} tok/s, {ms / args.steps * 1e3:.1f} us/step, "
               f"{b * tps / 1e9:.0f} GB/s ({b * tps / HBM_PEAK * 100:.1f}% of 8 TB/s)", file=sys.stderr, flush=True)
     head_ctx = max(contexts)
-    # dominant kernel: the per-chain online softmax of one attention layer at
-    # the headline context (it streams the layer's V cache and scores)
+    # dominant kernel: the fused scores + per-chain online softmax of one
+    # attention layer at the headline context (it streams the layer's K and V)
     eng.fill_synthetic(head_ctx - 1, seed=1, pending=1)
     # rotate over the six attention layers: every launch streams a cold cache
-    parts = {p: eng.time_attention(-1, args.attn_reps, p) for p in ("scores", "chains", "merge", "all")}
+    parts = {p: eng.time_attention(-1, args.attn_reps, p) for p in ("chains", "merge", "all")}
     chain_ms = parts["chains"]
     n_att = head_ctx  # attended positions, including the new one
-    chain_bytes = CHAIN_BYTES_PER_POS * n_att + CHAIN_FIXED_BYTES
+    chain_bytes = FUSED_BYTES_PER_POS * n_att + FUSED_FIXED_BYTES
     head_ms = eng.time_head(args.attn_reps)
     eng.close()
     copy_bytes = 1 << 30
@@ -172,13 +173,14 @@ def main():
             "head_kernel_us": round(head_ms * 1e3, 2),
         },
         "roofline": {
-            "kernel": f"k_attn_chain (per-chain online softmax over V, one attention layer, {n_att} positions)",
+            "kernel": f"k_attn_fused (scores + per-chain online softmax over K and V, one attention "
+                      f"layer, {n_att} positions)",
             "bound": "hbm",
             "achieved": round(chain_bytes / (chain_ms / 1e3) / 1e9, 1),
             "peak": 8000.0,
             "unit": "GB/s",
             "frac": round(chain_bytes / (chain_ms / 1e3) / HBM_PEAK, 4),
-            "traffic": committed_traffic("k_attn_chain", head_ctx),
+            "traffic": committed_traffic("k_attn_fused", head_ctx),
             "algorithmic_bytes": chain_bytes,
             "launch_us": round(chain_ms * 1e3, 2),
             "attention_layer_us": {k: round(v * 1e3, 2) for k, v in parts.items()},

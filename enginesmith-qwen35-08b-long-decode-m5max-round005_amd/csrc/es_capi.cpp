@@ -248,8 +248,7 @@ int es_attn_decode(const uint16_t* q_proj, const uint16_t* k_proj, const uint16_
   a.gated = gated;
   a.query_out = query_out;
   a.pos_val = position;
-  if (int rc = hip_status(es::launch_attn_scores(a, S(stream)), "es_attn_decode scores")) return rc;
-  if (int rc = hip_status(es::launch_attn_chain(a, S(stream)), "es_attn_decode chains")) return rc;
+  if (int rc = hip_status(es::launch_attn_fused(a, S(stream)), "es_attn_decode chains")) return rc;
   return hip_status(es::launch_attn_merge(a, S(stream)), "es_attn_decode merge");
 }
 

@@ -23,7 +23,12 @@ constexpr int kKindPrompt = 1;  // layers + advance (prompt consumption)
 
 }  // namespace
 
-int Engine::splits_for(int length) { return length < 8192 ? 32 : 256; }
+// The attention launch shape does not depend on the length, so one graph
+// serves every step; the value is the `blocks` the launch arguments carry.
+int Engine::splits_for(int length) {
+  (void)length;
+  return 64;
+}
 
 Engine* Engine::create(const void* blob, uint64_t bytes, int n_layers, int vocab, int capacity,
                        std::string* err) {
@@ -240,8 +245,7 @@ hipError_t Engine::enqueue_layers(hipStream_t s, int splits) {
       nm.m[2] = L.v; nm.y[2] = v_;
       if ((e = launch_norm_multi(nm, s)) != hipSuccess) return e;
       const AttnArgs a = attn_args(L, splits);
-      if ((e = launch_attn_scores(a, s)) != hipSuccess) return e;
-      if ((e = launch_attn_chain(a, s)) != hipSuccess) return e;
+      if ((e = launch_attn_fused(a, s)) != hipSuccess) return e;
       if ((e = launch_attn_merge(a, s)) != hipSuccess) return e;
       if ((e = launch_qmv(L.o, y_, h_, h_, nullptr, s)) != hipSuccess) return e;
     }
@@ -569,9 +573,8 @@ int Engine::time_decode(int steps, int warmup, double* ms_total, std::string* er
 
 hipError_t Engine::launch_attention_part(const AttnArgs& a, int which) {
   hipError_t e = hipSuccess;
-  if (which == 0 || which == 1) e = launch_attn_scores(a, stream_);
-  if (e == hipSuccess && (which == 0 || which == 2)) e = launch_attn_chain(a, stream_);
-  if (e == hipSuccess && (which == 0 || which == 3)) e = launch_attn_merge(a, stream_);
+  if (which == 0 || which == 1) e = launch_attn_fused(a, stream_);
+  if (e == hipSuccess && (which == 0 || which == 2)) e = launch_attn_merge(a, stream_);
   return e;
 }
 
@@ -583,7 +586,7 @@ int Engine::time_attention(int layer, int reps, int which, double* ms_avg, std::
   std::vector<int> att;
   for (int l = 0; l < shape_.n_layers; ++l)
     if (layers_[l].attention && (layer < 0 || l == layer)) att.push_back(l);
-  if (att.empty() || layer >= shape_.n_layers || reps <= 0 || which < 0 || which > 3) {
+  if (att.empty() || layer >= shape_.n_layers || reps <= 0 || which < 0 || which > 2) {
     if (err) *err = "invalid attention timing request";
     return 1;
   }

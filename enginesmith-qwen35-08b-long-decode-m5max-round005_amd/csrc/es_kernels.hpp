@@ -72,8 +72,8 @@ hipError_t launch_gdn_gate_out(const Q4& w, const uint16_t* y, const uint16_t* z
 // Decode attention follows the reference's two routes (model.rs:327-347):
 // below 1024 cached positions 32 interleaved position chains combined in
 // fp32 (sdpa_vector), from 1024 on 64 chains whose outputs are rounded to
-// bf16 before the gated merge (sdpa_vector_2pass_1 + split2_gate). Three
-// launches: scores, per-chain online softmax, merge + gate.
+// bf16 before the gated merge (sdpa_vector_2pass_1 + split2_gate). Two
+// launches: scores with the per-chain online softmax, then merge + gate.
 constexpr int kAttnRouteSplit = 1024;  // first length served by 64 chains
 constexpr int kAttnMaxChains = 64;
 struct AttnArgs {
@@ -88,8 +88,7 @@ struct AttnArgs {
   const float* inv_freq;    // [32] rotary inverse frequencies
   float* part_o;            // [8, 64, 256] unnormalised chain outputs
   float* part_ml;           // [8, 64, 2] chain (max, sum)
-  float* scores;            // [8, capacity] scaled q.k per position
-  int blocks;               // score blocks per KV head
+  int blocks;               // accepted for the C ABI (1..1024); no launch depends on it
   uint16_t* gated;          // [8, 256]
   uint16_t* query_out;      // optional [8, 256] roped queries
   const StepState* st;
@@ -97,8 +96,7 @@ struct AttnArgs {
 };
 size_t attn_scratch_bytes(int capacity);
 void attn_bind_scratch(AttnArgs& a, void* scratch);
-hipError_t launch_attn_scores(const AttnArgs& a, hipStream_t s);
-hipError_t launch_attn_chain(const AttnArgs& a, hipStream_t s);
+hipError_t launch_attn_fused(const AttnArgs& a, hipStream_t s);
 hipError_t launch_attn_merge(const AttnArgs& a, hipStream_t s);
 
 // ---- vocab head, k_head.hip ----

@@ -7,27 +7,25 @@
 //     then merged and gated (sdpa_vector_2pass_1 + attn_decode_split2_gate,
 //     attention_decode.metal:215-431, 830-891).
 //
-// k_attn_scores, grid (blocks, 2 KV heads) x 256: the prologue fuses
-//   attn_prepare_qkv_decode (attention.metal:262-313: q/k RMSNorm with bf16
-//   normalised value and bf16 gain product, RoPE on dims 0..63 with pairs
-//   (i, i+32)); the block whose chunk holds the new position also writes its
-//   K/V rows. Each block then streams a contiguous chunk of the K cache once
-//   for all four query heads of the group: 8 lanes per position, lane m holds
-//   dims 8m+64i .. +7 (i = 0..3, 128 coalesced bytes per 8 lanes), one fma
+// k_attn_fused, 256 blocks x 768 threads: block = (KV head, chain, query-head
+//   pair). The prologue fuses attn_prepare_qkv_decode (attention.metal:262-313:
+//   q/k RMSNorm with bf16 normalised value and bf16 gain product, RoPE on dims
+//   0..63 with pairs (i, i+32)); the blocks of the chain that holds the new
+//   position form its K/V rows, write them to the cache (query-head pair 0)
+//   and use them in place of the rows they stream. Two data-moving waves
+//   stage the chain's K and V rows in LDS by 16-byte global->LDS DMA, 32-step
+//   tiles, four deep. Four waves score each K tile for both heads
+//   (8 lanes per position, lane m holds dims 8m+64i .. +7 (i = 0..3), one fma
 //   chain per 8 dims, (p[m]+p[m+8])+(p[m+16]+p[m+24]) in the lane and a DPP
-//   tree over the 8 lanes. Scores go to an fp32 array [8, capacity].
-// k_attn_chain, 256 blocks x 448 threads: block = (KV head, chain, query-head
-//   pair), thread = two adjacent value dims of one head (four compute waves),
-//   plus one data-moving wave and one exps wave per head. V rows and scores
-//   are staged in
-//   LDS by 16-byte global->LDS DMA, four 64-step tiles deep. The exps waves
-//   turn the chain's scores into running max, factor and exp score one tile ahead
-//   (max scan by DPP, exp by the shared series), which reach the compute
-//   lanes by DPP row broadcast. Per step o = fma(e, v, o*factor)
-//   and sum = sum*factor + e; when every factor of a tile is exactly 1 the
-//   products by 1 are skipped, which changes no bit.
-//   The two blocks of a (KV head, chain) sit on the same XCD (block ids b and
-//   b+8) so the second read of each V row is an L2 hit.
+//   tree over the 8 lanes); two waves turn the scores into running max,
+//   factor and exp score one tile later (max scan by DPP, exp by the shared
+//   series), which reach the chain lanes by DPP row broadcast; four waves
+//   run the chain steps two tiles after the scores, per step
+//   o = fma(e, v, o*factor) and sum = sum*factor + e; when every factor of a
+//   tile is exactly 1 the products by 1 are skipped, which changes no bit.
+//   K and V are each read from HBM once; the two blocks of a (KV head, chain)
+//   sit on the same XCD (block ids b and b+8) so the second read of each row
+//   is an L2 hit.
 // k_attn_merge, grid (8 heads, 4 quarters) x 64: chain combination of either
 //   route, then gated = bf16(bf16(o) * sigmoid_bf(gate)) (attention.metal:133-151).
 #include "es_kernels.hpp"
@@ -80,155 +78,13 @@ __device__ __forceinline__ float chunk_dot(const float* q, const u32x4& k) {
   return s;
 }
 
-// Row stride of the score array: j-slots per chain, for the 32-chain route,
-// rounded up to whole 64-step tiles.
-__host__ __device__ __forceinline__ int score_stride(int capacity) {
-  return (((capacity + 31) / 32) + 63) & ~63;
-}
-
 __device__ __forceinline__ int route_chains(int n) { return n < kAttnRouteSplit ? 32 : 64; }
 
-constexpr int kRing = 4;  // K-row register slots per lane in k_attn_scores
+// ---- fused scores + per-chain online softmax ----
 
-__global__ __launch_bounds__(256, 2) void k_attn_scores(AttnArgs a) {
-  __shared__ float nrm[5][256];     // normalised q heads 0..3, new k
-  __shared__ float qs[4][256];      // roped q * 1/16
-  __shared__ u32x4 knew[32];        // new K row (roped, bf16)
-
-  // wave is uniform; readfirstlane lets the compiler keep the item loop scalar.
-  const int t = threadIdx.x, lane = t & 63, wave = __builtin_amdgcn_readfirstlane(t >> 6);
-  const int g = blockIdx.y, B = gridDim.x;
-  const int pos = load_pos(a.st, a.pos_val);
-  const int n = pos + 1;
-  const int C = route_chains(n);
-  // Work items (chain c, 8 steps from 8*j8): item i = j8*C + c covers
-  // positions c + C*(8*j8 + r), r = 0..7. Block b owns items [ib0, ib1).
-  const int jtot = (n + C - 1) / C;
-  const int items = C * ((jtot + 7) >> 3);
-  const int ipb = (items + B - 1) / B;
-  const int ib0 = blockIdx.x * ipb;
-  if (ib0 >= items) return;
-  const int ib1 = min(ib0 + ipb, items);
-  const int ipos = (pos / C >> 3) * C + pos % C;
-  const bool owner = ib0 <= ipos && ipos < ib1;  // holds the new position
-  const int grp = lane >> 3, m = lane & 7;
-  const uint16_t* kb = a.kcache + (size_t)g * a.capacity * 256 + 8 * m;
-  // Lane group grp takes step r = grp of the item; wave w takes items
-  // ib0 + w, ib0 + w + 4, ...
-  const int lc = C == 32 ? 5 : 6;  // log2 C
-  auto item_pos = [&](int i, int& p) {
-    p = (i & (C - 1)) + ((8 * (i >> lc) + grp) << lc);
-    return p < n;
-  };
-  // Prologue inputs, read before the K ring so that waiting for them does not
-  // wait for K (vector-memory counters complete in order).
-  const uint2 qx = *reinterpret_cast<const uint2*>(a.q_proj + (4 * g + wave) * 512 + lane * 4);
-  const uint2 qg = *reinterpret_cast<const uint2*>(a.q_gain + lane * 4);
-  const uint2 kx = *reinterpret_cast<const uint2*>(a.k_proj + g * 256 + lane * 4);
-  const uint2 kg = *reinterpret_cast<const uint2*>(a.k_gain + lane * 4);
-  const uint2 vx = *reinterpret_cast<const uint2*>(a.v_proj + g * 256 + lane * 4);
-  float inv[4];
-#pragma unroll
-  for (int x = 0; x < 4; ++x) inv[x] = a.inv_freq[((lane * 4) & 31) + x];
-  // Wave w takes items ib0 + w + 4*it, it = 0 .. nit-1. K rows stream
-  // through a ring of kRing register slots, kRing - 1 items in flight while
-  // one is computed; the first kRing - 1 are issued before the prologue so
-  // their latency overlaps it. Loads are unconditional: an item past the end
-  // reads row 0 and the new position's row (written by this kernel) is read
-  // but replaced by the LDS copy, so no branch holds a load back.
-  const int nit = ib1 - ib0 > wave ? (ib1 - ib0 - wave + 3) / 4 : 0;
-  u32x4 kr[kRing][4];
-  int pr[kRing];
-  bool okr[kRing];
-  auto issue = [&](int it, u32x4* dst, int& pp, bool& okk) {
-    okk = it < nit && item_pos(ib0 + wave + 4 * it, pp);
-    const u32x4* r = reinterpret_cast<const u32x4*>(kb + (size_t)(okk ? pp : 0) * 256);
-#pragma unroll
-    for (int x = 0; x < 4; ++x) dst[x] = r[8 * x];
-  };
-#pragma unroll
-  for (int u = 0; u < kRing - 1; ++u) issue(u, kr[u], pr[u], okr[u]);
-
-  // ---- prologue: q (and, in the owner block, the new k/v rows) ----
-  {
-    float o4[4];
-    head_norm4(qx, qg, o4);
-#pragma unroll
-    for (int x = 0; x < 4; ++x) nrm[wave][lane * 4 + x] = o4[x];
-    if (owner && wave == 0) {
-      head_norm4(kx, kg, o4);
-#pragma unroll
-      for (int x = 0; x < 4; ++x) nrm[4][lane * 4 + x] = o4[x];
-    }
-  }
-  __syncthreads();
-  {
-    float r[4];
-#pragma unroll
-    for (int x = 0; x < 4; ++x) r[x] = rope_at(nrm[wave], lane * 4 + x, pos, inv[x]);
-    if (a.query_out && blockIdx.x == 0) {
-      uint16_t* qo = a.query_out + (4 * g + wave) * 256 + lane * 4;
-      *reinterpret_cast<uint2*>(qo) = make_uint2(pack_bf2(r[0], r[1]), pack_bf2(r[2], r[3]));
-    }
-#pragma unroll
-    for (int x = 0; x < 4; ++x) qs[wave][lane * 4 + x] = r[x] * 0.0625f;
-    if (owner && wave == 1) {
-      float kr[4];
-#pragma unroll
-      for (int x = 0; x < 4; ++x) kr[x] = rope_at(nrm[4], lane * 4 + x, pos, inv[x]);
-      const uint32_t k0 = pack_bf2(kr[0], kr[1]);
-      const uint32_t k1 = pack_bf2(kr[2], kr[3]);
-      uint32_t* kw = reinterpret_cast<uint32_t*>(knew);
-      kw[lane * 2] = k0;
-      kw[lane * 2 + 1] = k1;
-      const size_t ci = ((size_t)g * a.capacity + pos) * 256 + lane * 4;
-      *reinterpret_cast<uint2*>(a.kcache + ci) = make_uint2(k0, k1);
-      *reinterpret_cast<uint2*>(a.vcache + ci) = vx;
-    }
-  }
-  __syncthreads();
-
-  // q for this lane's dims: 4 heads x 4 chunks x 8 dims.
-  float q[4][4][8];
-#pragma unroll
-  for (int hh = 0; hh < 4; ++hh)
-#pragma unroll
-    for (int x = 0; x < 4; ++x)
-#pragma unroll
-      for (int j = 0; j < 8; ++j) q[hh][x][j] = qs[hh][64 * x + 8 * m + j];
-
-  const int sstride = score_stride(a.capacity);
-  float* sc = a.scores + (size_t)(4 * g + (m & 3)) * kAttnMaxChains * sstride;
-  for (int it0 = 0; it0 < nit; it0 += kRing) {
-#pragma unroll
-    for (int u = 0; u < kRing; ++u) {
-      const int it = it0 + u;  // items past nit compute on row 0 and store nothing
-      const int nx = (u + kRing - 1) % kRing;  // slot freed by the previous item
-      issue(it + kRing - 1, kr[nx], pr[nx], okr[nx]);
-      u32x4 kc[4];
-#pragma unroll
-      for (int x = 0; x < 4; ++x) kc[x] = okr[u] && pr[u] == pos ? knew[m + 8 * x] : kr[u][x];
-      float s[4];
-#pragma unroll
-      for (int hh = 0; hh < 4; ++hh) {
-        const float p0 = chunk_dot(q[hh][0], kc[0]);
-        const float p1 = chunk_dot(q[hh][1], kc[1]);
-        const float p2 = chunk_dot(q[hh][2], kc[2]);
-        const float p3 = chunk_dot(q[hh][3], kc[3]);
-        s[hh] = tree8((p0 + p1) + (p2 + p3));
-      }
-      const int hm = m & 3;
-      const float mine = hm == 0 ? s[0] : hm == 1 ? s[1] : hm == 2 ? s[2] : s[3];
-      const int p = pr[u];
-      if (okr[u] && m < 4) sc[(size_t)(p & (C - 1)) * sstride + (p >> lc)] = mine;
-    }
-  }
-}
-
-// ---- per-chain online softmax ----
-
-constexpr int kTile = 64;    // chain steps per tile
-constexpr int kStages = 4;   // V tiles in LDS (3 in flight while one is used)
+constexpr int kTile = 32;     // chain steps per tile
+constexpr int kStages = 4;    // K and V tiles in LDS, each ring four deep
+constexpr int kTileOps = 16;  // DMA operations per tile and ring (2 rows each)
 
 template <int CTRL, int ROWS>
 __device__ __forceinline__ float dpp_src(float x, float old) {
@@ -251,12 +107,17 @@ __device__ __forceinline__ float readlane63(float x) {
   return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, x), 63));
 }
 
-struct __attribute__((aligned(16))) ChainSmem {
+struct __attribute__((aligned(16))) FusedSmem {
+  uint16_t k[kStages][kTile][256];  // K rows of a tile, as loaded
   uint16_t v[kStages][kTile][256];  // V rows of a tile, as loaded
-  float s[kStages][2][kTile];       // scores of a tile, both heads
-  float e[2][2][kTile];             // [buffer][head][step] exp scores
+  float s[2][2][kTile];             // [buffer][head][step] scores
+  float e[2][2][kTile];             // exp scores
   float f[2][2][kTile];             // factors
   int slow[2][2];                   // some factor of the tile differs from 1
+  float nrm[3][256];                // prologue: normalised q of both heads, new k
+  float qs[2][256];                 // roped q x 1/16 of both heads
+  u32x4 knew[32];                   // new K row (roped, bf16)
+  u32x4 vnew[32];                   // new V row
 };
 
 typedef __attribute__((address_space(3))) void* lds_ptr_t;
@@ -279,44 +140,77 @@ __device__ __forceinline__ void wait_vm() {
   __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
 }
 
-// Issue tile T from the producer wave: 64 V rows as 32 DMA of 1 KB (lanes
-// 0..31 one row, 32..63 the next) and the tile's 2 x 64 scores as one DMA of
-// 32 x 16 B (33 vector-memory operations). Rows past the chain's end re-read
-// its last row (in bounds; their slots are masked by e = 0).
-constexpr int kTileOps = 33;
-__device__ __forceinline__ void issue_tile(ChainSmem& sm, const uint16_t* vrow0, const float* sc0,
-                                           int sstride, int C, int L, int T, int lane) {
-  const int st = T % kStages;
+// Wait until tile t has landed when `later` (0..2) tiles of the same ring
+// were issued after it.
+__device__ __forceinline__ void wait_tiles(int later) {
+  if (later >= 2) wait_vm<2 * kTileOps>();
+  else if (later == 1) wait_vm<kTileOps>();
+  else wait_vm<0>();
+}
+
+// Issue tile t of one ring (K or V rows of the chain) from a producer wave:
+// 32 rows as 16 DMA of 1 KB (lanes 0..31 one row, 32..63 the next). Rows
+// past the chain's end re-read its last row (in bounds; their scores are
+// masked and their exp scores are 0).
+__device__ __forceinline__ void issue_rows(uint16_t (*ring)[kTile][256], const uint16_t* row0, int C,
+                                           int L, int t, int lane) {
+  uint16_t(*dst)[256] = ring[t % kStages];
 #pragma unroll 4
-  for (int x = 0; x < 32; ++x) {
+  for (int x = 0; x < kTile / 2; ++x) {
     const int r = 2 * x;
-    const int j = min(T * kTile + r + (lane >> 5), L - 1);
-    const uint16_t* g = vrow0 + (size_t)j * C * 256 + (lane & 31) * 8;
-    __builtin_amdgcn_global_load_lds(g, (lds_ptr_t)&sm.v[st][r][0], 16, 0, 0);
-  }
-  if (lane < 32) {
-    const int head = lane >> 4, part = lane & 15;
-    const float* g = sc0 + (size_t)head * kAttnMaxChains * sstride + T * kTile + part * 4;
-    __builtin_amdgcn_global_load_lds(g, (lds_ptr_t)&sm.s[st][0][0], 16, 0, 0);
+    const int j = min(t * kTile + r + (lane >> 5), L - 1);
+    const uint16_t* g = row0 + (size_t)j * C * 256 + (lane & 31) * 8;
+    __builtin_amdgcn_global_load_lds(g, (lds_ptr_t)&dst[r][0], 16, 0, 0);
   }
 }
 
-// Exp scores and factors of tile T for one head from its staged scores.
-__device__ __forceinline__ void tile_exps(ChainSmem& sm, int T, int L, int head, int lane,
+// Overwrite row i of a staged tile with the row computed in this launch
+// (the cache row may still hold the old value when the DMA read it).
+__device__ __forceinline__ void patch_row(uint16_t* row, const u32x4* src, int lane) {
+  if (lane < 32) reinterpret_cast<u32x4*>(row)[lane] = src[lane];
+}
+
+// Scores of tile t for both heads of the block: 8 lanes per position, lane m
+// holds dims 8m+64x .. +7 (x = 0..3) of the K row; one fma chain per 8 dims,
+// (p[m]+p[m+8])+(p[m+16]+p[m+24]) in the lane and a DPP tree over the 8
+// lanes. The four compute waves cover the tile's 32 positions.
+__device__ __forceinline__ void tile_scores(FusedSmem& sm, int t, int pidx, int m,
+                                            const float (&q)[2][4][8]) {
+  const u32x4* row = reinterpret_cast<const u32x4*>(&sm.k[t % kStages][pidx][0]);
+  u32x4 kc[4];
+#pragma unroll
+  for (int x = 0; x < 4; ++x) kc[x] = row[m + 8 * x];
+  float s[2];
+#pragma unroll
+  for (int hh = 0; hh < 2; ++hh) {
+    const float p0 = chunk_dot(q[hh][0], kc[0]);
+    const float p1 = chunk_dot(q[hh][1], kc[1]);
+    const float p2 = chunk_dot(q[hh][2], kc[2]);
+    const float p3 = chunk_dot(q[hh][3], kc[3]);
+    s[hh] = tree8((p0 + p1) + (p2 + p3));
+  }
+  if (m < 2) sm.s[t & 1][m][pidx] = m == 0 ? s[0] : s[1];
+}
+
+// Exp scores and factors of tile t for one head from its scores (lanes 0..31
+// hold the tile's steps; lanes past the tile or the chain read -inf).
+__device__ __forceinline__ void tile_exps(FusedSmem& sm, int t, int L, int head, int lane,
                                           float& carry) {
   const float ninf = -__builtin_inff();
-  const float s = T * kTile + lane < L ? sm.s[T % kStages][head][lane] : ninf;
+  const float s = lane < kTile && t * kTile + lane < L ? sm.s[t & 1][head][lane] : ninf;
   const float mt = fmaxf(carry, wave_max_scan(s));
   const float pv = dpp_src<0x138, 0xf>(mt, carry);  // wave_shr:1, lane 0 <- carry
   const float f = es_exp(pv - mt), e = es_exp(s - mt);
-  sm.e[T & 1][head][lane] = e;
-  sm.f[T & 1][head][lane] = f;
-  sm.slow[T & 1][head] = __any(f != 1.0f);  // wave-uniform, stored by every lane
+  if (lane < kTile) {
+    sm.e[t & 1][head][lane] = e;
+    sm.f[t & 1][head][lane] = f;
+  }
+  sm.slow[t & 1][head] = __any(f != 1.0f);  // wave-uniform, stored by every lane
   carry = readlane63(mt);
 }
 
 // Exp scores and factors reach the compute waves through DPP: each lane
-// holds e[16r + (lane & 15)] for r = 0..3 (one 4-byte LDS read per r), and
+// holds e[16r + (lane & 15)] for r = 0, 1 (one 4-byte LDS read per r), and
 // step s = 16r + k uses row_newbcast:k, which gives every lane of a 16-lane
 // row the value of that row's lane k, as the first operand of the
 // arithmetic. The registers read this way are only ever written by LDS loads,
@@ -374,20 +268,20 @@ __device__ __forceinline__ void chain_group(const uint32_t* w, float er, float f
 #undef ES_STEP
 }
 
-// Groups G .. 7 of a tile: compute group G, then issue the loads of group
+// Groups G .. 3 of a tile: compute group G, then issue the loads of group
 // G + AHEAD into the slot it frees. LDS reads complete in order and at most
 // 15 may be outstanding (the counter's width), so a fast tile keeps three
-// groups in flight (plus two reads of exp scores) and a slow tile, which also
+// groups in flight (plus one read of exp scores) and a slow tile, which also
 // reads factors, two.
 template <int G, bool SLOW, bool SUM>
 __device__ __forceinline__ void chain_groups(const uint32_t* vw, int kw, const float* er,
                                              const float* fr, uint32_t (&w)[4][8], float& oa,
                                              float& ob, float& sum) {
-  if constexpr (G < 8) {
+  if constexpr (G < kTile / 8) {
     constexpr int ahead = SLOW ? 2 : 3;
     chain_group<G, SLOW, SUM>(w[G % 4], er[G / 2], fr[G / 2], oa, ob, sum);
     issue_fence();
-    if constexpr (G + ahead < 8) {
+    if constexpr (G + ahead < kTile / 8) {
       load_group(vw, kw, G + ahead, w[(G + ahead) % 4]);
       issue_fence();
     }
@@ -395,19 +289,18 @@ __device__ __forceinline__ void chain_groups(const uint32_t* vw, int kw, const f
   }
 }
 
-// 64 steps of the two adjacent dims owned by this thread for one head; SUM
-// waves also keep the head's sum. Steps past the chain's end have e = 0 and
-// f = 1 and change nothing (o is never -0, V rows are finite).
+// The tile's steps for the two adjacent dims owned by this thread for one
+// head; SUM waves also keep the head's sum. Steps past the chain's end have
+// e = 0 and f = 1 and change nothing (o is never -0, V rows are finite).
 template <bool SLOW, bool SUM>
-__device__ __forceinline__ void chain_tile(const ChainSmem& sm, int T, int hh, int kw, int lane,
+__device__ __forceinline__ void chain_tile(const FusedSmem& sm, int t, int hh, int kw, int lane,
                                            float& oa, float& ob, float& sum) {
-  const int st = T % kStages, b = T & 1;
-  const uint32_t* vw = reinterpret_cast<const uint32_t*>(&sm.v[st][0][0]);
-  const float* ep = sm.e[b][hh] + (lane & 15);
-  const float* fp = sm.f[b][hh] + (lane & 15);
-  float er[4], fr[4];
+  const uint32_t* vw = reinterpret_cast<const uint32_t*>(&sm.v[t % kStages][0][0]);
+  const float* ep = sm.e[t & 1][hh] + (lane & 15);
+  const float* fp = sm.f[t & 1][hh] + (lane & 15);
+  float er[2], fr[2];
 #pragma unroll
-  for (int r = 0; r < 4; ++r) {
+  for (int r = 0; r < 2; ++r) {
     er[r] = ep[16 * r];
     fr[r] = SLOW ? fp[16 * r] : 1.0f;
   }
@@ -421,32 +314,29 @@ __device__ __forceinline__ void chain_tile(const ChainSmem& sm, int T, int hh, i
 }
 
 template <bool SUM>
-__device__ __forceinline__ void run_tile(const ChainSmem& sm, int T, int hh, int kw, int lane,
+__device__ __forceinline__ void run_tile(const FusedSmem& sm, int t, int hh, int kw, int lane,
                                          float& oa, float& ob, float& sum) {
-  if (sm.slow[T & 1][hh])
-    chain_tile<true, SUM>(sm, T, hh, kw, lane, oa, ob, sum);
+  if (sm.slow[t & 1][hh])
+    chain_tile<true, SUM>(sm, t, hh, kw, lane, oa, ob, sum);
   else
-    chain_tile<false, SUM>(sm, T, hh, kw, lane, oa, ob, sum);
+    chain_tile<false, SUM>(sm, t, hh, kw, lane, oa, ob, sum);
 }
 
-// Block = (KV head, chain, query-head pair): compute waves 0,1 own head 0 and
-// 2,3 head 1, two adjacent value dims per thread. Wave 4 only moves data
-// (global->LDS DMA), so no compute wave waits on memory counters, and waves
-// 5 and 6 only turn head 0's and head 1's scores into exps, one tile ahead,
-// so that work runs beside the value steps instead of before them. Waves 0
-// and 3 also keep their head's sum (the SIMDs that host no exps wave). Per
-// tile T: the producer waits until tiles up to T+1 are in LDS; barrier; the
-// producer issues tile T+3 into the stage tile T-1 used; the exps waves form
-// the exps of tile T+1; the compute waves run tile T.
-constexpr int kChainThreads = 7 * 64;
+// Block = (KV head, chain, query-head pair), 12 waves, three per SIMD. Waves
+// 0..3 run the chain for head (wave & 1), two adjacent value dims per thread
+// (waves 0 and 1 also keep their head's sum); waves 4..7 score the tiles, 8
+// lanes per position; wave 8 streams the chain's K rows and wave 9 its V rows
+// into LDS by global->LDS DMA; waves 10 and 11 turn head 0's and head 1's
+// scores into exps. Each SIMD hosts one chain wave and one scoring wave, so
+// one's LDS latency is covered by the other's arithmetic. Iteration I (one
+// barrier each): scores of tile I, exps of tile I-1, chain steps of tile
+// I-2; K tile I+3 and V tile I+1 are issued into the stages freed by tiles
+// I-1 and I-3.
+constexpr int kFusedThreads = 12 * 64;
 
-__global__ __launch_bounds__(kChainThreads, 1) void k_attn_chain(AttnArgs a) {
-  __shared__ ChainSmem sm;
+__global__ __launch_bounds__(kFusedThreads, 1) void k_attn_fused(AttnArgs a) {
+  __shared__ FusedSmem sm;
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
-  const bool producer = wave == 4;
-  const bool exps_wave = wave >= 5;
-  const int hh = exps_wave ? wave - 5 : wave >> 1, kw = (wave & 1) * 64 + lane;  // dims 2kw, 2kw+1
-  const bool sum_wave = wave == 0 || wave == 3;
   const int bx = blockIdx.x;
   const int hp = (bx >> 3) & 1, rest = (bx & 7) | ((bx >> 4) << 3);
   const int kvh = rest >> 6, c = rest & 63;
@@ -455,60 +345,122 @@ __global__ __launch_bounds__(kChainThreads, 1) void k_attn_chain(AttnArgs a) {
   const int C = route_chains(n);
   if (c >= C) return;
   const int L = n > c ? (n - 1 - c) / C + 1 : 0;
+  const int nt = (L + kTile - 1) / kTile;
   const int h0 = 4 * kvh + 2 * hp;
+  const bool holder = pos % C == c;  // this chain's last step is the new position
+  const int jpos = pos / C, tpos = jpos / kTile, ipos = jpos % kTile;
+  const uint16_t* krow0 = a.kcache + ((size_t)kvh * a.capacity + c) * 256;
+  const uint16_t* vrow0 = a.vcache + ((size_t)kvh * a.capacity + c) * 256;
+
+  // ---- prologue: producers start streaming; the others form q (and, in
+  // the holder blocks, the new K/V rows) ----
+  if (wave == 8) {
+    for (int tt = 0; tt < 3 && tt < nt; ++tt) issue_rows(sm.k, krow0, C, L, tt, lane);
+  } else if (wave == 9) {
+    if (nt > 0) issue_rows(sm.v, vrow0, C, L, 0, lane);
+  } else if (wave < 4) {
+    uint2 xv, gv;
+    if (wave < 2) {
+      xv = *reinterpret_cast<const uint2*>(a.q_proj + (h0 + wave) * 512 + lane * 4);
+      gv = *reinterpret_cast<const uint2*>(a.q_gain + lane * 4);
+    } else {
+      xv = *reinterpret_cast<const uint2*>((wave == 2 ? a.k_proj : a.v_proj) + kvh * 256 + lane * 4);
+      gv = *reinterpret_cast<const uint2*>(a.k_gain + lane * 4);
+    }
+    if (wave < 3) {
+      float o4[4];
+      head_norm4(xv, gv, o4);
+#pragma unroll
+      for (int x = 0; x < 4; ++x) sm.nrm[wave][lane * 4 + x] = o4[x];
+    } else {
+      reinterpret_cast<uint2*>(sm.vnew)[lane] = xv;
+      if (holder && hp == 0)
+        *reinterpret_cast<uint2*>(a.vcache + ((size_t)kvh * a.capacity + pos) * 256 + lane * 4) = xv;
+    }
+  }
+  if (wave == 8 || wave == 9) lds_barrier(); else __syncthreads();
+  if (wave < 3) {
+    float inv[4];
+#pragma unroll
+    for (int x = 0; x < 4; ++x) inv[x] = a.inv_freq[((lane * 4) & 31) + x];
+    float r[4];
+#pragma unroll
+    for (int x = 0; x < 4; ++x) r[x] = rope_at(sm.nrm[wave], lane * 4 + x, pos, inv[x]);
+    if (wave < 2) {
+      if (a.query_out && c == 0) {
+        uint16_t* qo = a.query_out + (h0 + wave) * 256 + lane * 4;
+        *reinterpret_cast<uint2*>(qo) = make_uint2(pack_bf2(r[0], r[1]), pack_bf2(r[2], r[3]));
+      }
+#pragma unroll
+      for (int x = 0; x < 4; ++x) sm.qs[wave][lane * 4 + x] = r[x] * 0.0625f;
+    } else {
+      const uint2 kp = make_uint2(pack_bf2(r[0], r[1]), pack_bf2(r[2], r[3]));
+      reinterpret_cast<uint2*>(sm.knew)[lane] = kp;
+      if (holder && hp == 0)
+        *reinterpret_cast<uint2*>(a.kcache + ((size_t)kvh * a.capacity + pos) * 256 + lane * 4) = kp;
+    }
+  }
+  if (wave == 8 || wave == 9) lds_barrier(); else __syncthreads();
+
   float oa = 0.0f, ob = 0.0f, sum = 0.0f;
   float carry = kFiniteMin;  // exps waves: running max of their head
-  if (L > 0) {
-    const int nt = (L + kTile - 1) / kTile;
-    const int sstride = score_stride(a.capacity);
-    const uint16_t* vrow0 = a.vcache + ((size_t)kvh * a.capacity + c) * 256;
-    const float* sc0 = a.scores + ((size_t)h0 * kAttnMaxChains + c) * sstride;
-    if (producer) {
-      for (int T = 0; T < kStages - 1 && T < nt; ++T) issue_tile(sm, vrow0, sc0, sstride, C, L, T, lane);
-      // tile 0 complete; tiles 1 and 2 may stay pending (at most 63 operations
-      // are ever outstanding, and loads complete in order)
-      if (nt >= 3) wait_vm<63>(); else if (nt == 2) wait_vm<kTileOps>(); else wait_vm<0>();
+  // One loop per role, each with one barrier per iteration. The producers
+  // keep DMA in flight across barriers (lds_barrier); the other waves have no
+  // vector-memory operations outstanding and use __syncthreads, whose waits
+  // the compiler tracks.
+  if (wave == 8) {
+    for (int I = 0; I < nt + 2; ++I) {
+      if (I < nt) {
+        wait_tiles(min(2, nt - 1 - I));  // K tile I landed
+        if (holder && I == tpos) patch_row(&sm.k[I % kStages][ipos][0], sm.knew, lane);
+      }
+      lds_barrier();
+      if (I + 3 < nt) issue_rows(sm.k, krow0, C, L, I + 3, lane);
     }
-    // The producer keeps its DMA in flight across barriers (lds_barrier); the
-    // other waves have no vector-memory operations outstanding and use
-    // __syncthreads, whose waits the compiler tracks (an explicit wait that
-    // leaves DMA pending makes it drain every LDS read instead).
-    if (producer) lds_barrier(); else __syncthreads();
-    // One loop per role, each with one barrier per tile.
-    if (producer) {
-      for (int T = 0; T < nt; ++T) {
-        // tiles up to T+1 complete (V of T, scores of T+1); tile T+2 may pend
-        if (T + 2 < nt) wait_vm<kTileOps>(); else wait_vm<0>();
-        lds_barrier();
-        if (T + kStages - 1 < nt) issue_tile(sm, vrow0, sc0, sstride, C, L, T + kStages - 1, lane);
+  } else if (wave == 9) {
+    for (int I = 0; I < nt + 2; ++I) {
+      if (I >= 2) {
+        wait_tiles(min(2, nt - 1 - (I - 2)));  // V tile I-2 landed
+        if (holder && I - 2 == tpos) patch_row(&sm.v[(I - 2) % kStages][ipos][0], sm.vnew, lane);
       }
-    } else if (exps_wave) {
-      tile_exps(sm, 0, L, hh, lane, carry);
-      for (int T = 0; T < nt; ++T) {
-        __syncthreads();
-        if (T + 1 < nt) tile_exps(sm, T + 1, L, hh, lane, carry);
-      }
-    } else if (sum_wave) {
-      for (int T = 0; T < nt; ++T) {
-        __syncthreads();
-        run_tile<true>(sm, T, hh, kw, lane, oa, ob, sum);
-      }
-    } else {
-      for (int T = 0; T < nt; ++T) {
-        __syncthreads();
-        run_tile<false>(sm, T, hh, kw, lane, oa, ob, sum);
+      lds_barrier();
+      if (I + 1 < nt) issue_rows(sm.v, vrow0, C, L, I + 1, lane);
+    }
+  } else if (wave >= 10) {
+    const int head = wave - 10;
+    for (int I = 0; I < nt + 2; ++I) {
+      __syncthreads();
+      if (I >= 1 && I <= nt) tile_exps(sm, I - 1, L, head, lane, carry);
+    }
+  } else if (wave >= 4) {
+    const int pidx = (wave - 4) * 8 + (lane >> 3), m = lane & 7;
+    float q[2][4][8];
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+#pragma unroll
+      for (int x = 0; x < 4; ++x)
+#pragma unroll
+        for (int j = 0; j < 8; ++j) q[h][x][j] = sm.qs[h][64 * x + 8 * m + j];
+    for (int I = 0; I < nt + 2; ++I) {
+      __syncthreads();
+      if (I < nt) tile_scores(sm, I, pidx, m, q);
+    }
+  } else {
+    const int hh = wave & 1, kw = (wave >> 1) * 64 + lane;  // dims 2kw, 2kw+1
+    const bool sum_wave = wave < 2;
+    for (int I = 0; I < nt + 2; ++I) {
+      __syncthreads();
+      if (I >= 2) {
+        if (sum_wave) run_tile<true>(sm, I - 2, hh, kw, lane, oa, ob, sum);
+        else run_tile<false>(sm, I - 2, hh, kw, lane, oa, ob, sum);
       }
     }
-  }
-  if (producer) return;
-  float* ml = a.part_ml + ((size_t)(h0 + hh) * kAttnMaxChains + c) * 2;
-  if (exps_wave) {
-    if (lane == 0) ml[0] = carry;
+    float* po = a.part_o + ((size_t)(h0 + hh) * kAttnMaxChains + c) * 256 + 2 * kw;
+    *reinterpret_cast<float2*>(po) = make_float2(oa, ob);
+    if (sum_wave && lane == 0) a.part_ml[((size_t)(h0 + hh) * kAttnMaxChains + c) * 2 + 1] = sum;
     return;
   }
-  float* po = a.part_o + ((size_t)(h0 + hh) * kAttnMaxChains + c) * 256 + 2 * kw;
-  *reinterpret_cast<float2*>(po) = make_float2(oa, ob);
-  if (sum_wave && lane == 0) ml[1] = sum;
+  if (wave >= 10 && lane == 0) a.part_ml[((size_t)(h0 + wave - 10) * kAttnMaxChains + c) * 2] = carry;
 }
 
 // ---- merge + gate ----
@@ -583,7 +535,7 @@ __global__ __launch_bounds__(64) void k_attn_merge(AttnArgs a) {
 
 bool attn_ok(const AttnArgs& a) {
   return a.q_proj && a.k_proj && a.v_proj && a.q_gain && a.k_gain && a.kcache && a.vcache &&
-         a.inv_freq && a.part_o && a.part_ml && a.scores && a.gated && a.blocks >= 1 &&
+         a.inv_freq && a.part_o && a.part_ml && a.gated && a.blocks >= 1 &&
          a.blocks <= 1024 && a.capacity > 0 &&
          (a.st || (a.pos_val >= 0 && a.pos_val < a.capacity));
 }
@@ -591,24 +543,18 @@ bool attn_ok(const AttnArgs& a) {
 }  // namespace
 
 size_t attn_scratch_bytes(int capacity) {
-  return (size_t)kQHeads * kAttnMaxChains * (256 + 2 + score_stride(capacity)) * sizeof(float);
+  (void)capacity;  // the chain states do not grow with the cache
+  return (size_t)kQHeads * kAttnMaxChains * (256 + 2) * sizeof(float);
 }
 
 void attn_bind_scratch(AttnArgs& a, void* scratch) {
   a.part_o = static_cast<float*>(scratch);
   a.part_ml = a.part_o + (size_t)kQHeads * kAttnMaxChains * 256;
-  a.scores = a.part_ml + (size_t)kQHeads * kAttnMaxChains * 2;
 }
 
-hipError_t launch_attn_scores(const AttnArgs& a, hipStream_t s) {
+hipError_t launch_attn_fused(const AttnArgs& a, hipStream_t s) {
   if (!attn_ok(a)) return hipErrorInvalidValue;
-  hipLaunchKernelGGL(k_attn_scores, dim3(a.blocks, kKvHeads), dim3(256), 0, s, a);
-  return hipGetLastError();
-}
-
-hipError_t launch_attn_chain(const AttnArgs& a, hipStream_t s) {
-  if (!attn_ok(a)) return hipErrorInvalidValue;
-  hipLaunchKernelGGL(k_attn_chain, dim3(kKvHeads * kAttnMaxChains * 2), dim3(kChainThreads), 0, s, a);
+  hipLaunchKernelGGL(k_attn_fused, dim3(kKvHeads * kAttnMaxChains * 2), dim3(kFusedThreads), 0, s, a);
   return hipGetLastError();
 }
 

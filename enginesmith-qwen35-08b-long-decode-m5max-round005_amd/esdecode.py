@@ -315,7 +315,7 @@ class Engine:
         check(lib().es_engine_time_decode(self.h, steps, warmup, ctypes.byref(ms)))
         return ms.value
 
-    ATTN_PARTS = {"all": 0, "scores": 1, "chains": 2, "merge": 3}
+    ATTN_PARTS = {"all": 0, "chains": 1, "merge": 2}
 
     def time_attention(self, layer: int, reps: int, part: str = "all") -> float:
         """Average ms of one attention layer's launches (or of one of them)."""

@@ -142,8 +142,8 @@ int es_gdn_gate_out_proj(const es_q4* out_proj, const uint16_t* y, const uint16_
 int es_rope_inv_freq(float* host_out32);
 
 /* Scratch bytes es_attn_decode needs for a cache of `capacity` rows. Layout
- * (fp32): chain outputs [8,64,256], chain (max, sum) [8,64,2], scores
- * [8,capacity]. */
+ * (fp32): chain outputs [8,64,256], chain (max, sum) [8,64,2]; the size does
+ * not depend on the capacity. */
 size_t es_attn_scratch_bytes(int capacity);
 
 /* attn_prepare_qkv_decode (attention.metal:262-313) + decode attention with
@@ -154,9 +154,9 @@ size_t es_attn_scratch_bytes(int capacity);
  * 830-891). q_proj [8,512] (query|gate), k_proj/v_proj [2,256]; writes K/V
  * row `position` of kcache/vcache [2, capacity, 256] and
  * gated [8,256] = bf16(bf16(attn) * sigmoid_bf(gate)). Attends to positions
- * 0..position. `blocks` (1..1024) is the score launch's blocks per KV head,
- * a work split that changes no result. query_out (optional) receives the
- * roped queries [8,256]. */
+ * 0..position. `blocks` must be 1..1024 and changes nothing (the launch
+ * shape is fixed: one block per KV head, chain and query-head pair).
+ * query_out (optional) receives the roped queries [8,256]. */
 int es_attn_decode(const uint16_t* q_proj, const uint16_t* k_proj, const uint16_t* v_proj,
                    const uint16_t* q_gain, const uint16_t* k_gain, uint16_t* kcache,
                    uint16_t* vcache, int capacity, int position, const float* inv_freq,
@@ -236,12 +236,12 @@ int es_engine_fill_synthetic(es_engine* e, int length, uint64_t seed, uint32_t p
 
 /* Timing with HIP events on the engine stream. */
 int es_engine_time_decode(es_engine* e, int steps, int warmup, double* ms_total);
-/* which: 0 = all three attention launches, 1 = scores, 2 = chains, 3 = merge.
+/* which: 0 = both attention launches, 1 = scores with the chains, 2 = merge.
  * layer < 0 rotates over every attention layer (cold KV caches, as in a
  * decode step); layer >= 0 repeats that layer. */
 int es_engine_time_attention(es_engine* e, int layer, int reps, int which, double* ms_avg);
 int es_engine_time_head(es_engine* e, int reps, double* ms_avg);
-/* Score blocks per KV head the engine uses at attention length `length`. */
+/* The `blocks` value the engine passes to the attention launch (constant). */
 int es_engine_splits_for(int length);
 
 #ifdef __cplusplus
