@@ -143,6 +143,8 @@ int Engine::init(const void* blob, uint64_t bytes, std::string* err) {
   logits_ = static_cast<uint16_t*>(alloc((size_t)shape_.vocab * 2));
   head_part_ = static_cast<float*>(alloc((size_t)head_blocks(shape_.vocab) * 2 * sizeof(float)));
   attn_scratch_ = alloc(attn_scratch_bytes(capacity_));
+  proj_part_ = static_cast<float*>(alloc((size_t)kGdnHeads * kHidden * sizeof(float)));
+  hmid_ = static_cast<uint16_t*>(alloc(1024 * 2));
   inv_freq_ = static_cast<float*>(alloc(32 * sizeof(float)));
   st_ = static_cast<StepState*>(alloc(sizeof(StepState)));
   prompt_ = static_cast<uint32_t*>(alloc((size_t)capacity_ * 4));
@@ -150,7 +152,8 @@ int Engine::init(const void* blob, uint64_t bytes, std::string* err) {
   forced_ = static_cast<uint32_t*>(alloc((size_t)capacity_ * 4));
   for (void* p : {(void*)h_, (void*)z_, (void*)ab_, (void*)y_, (void*)q_, (void*)k_, (void*)v_,
                   (void*)act_, (void*)logits_, (void*)head_part_,
-                  attn_scratch_, (void*)inv_freq_, (void*)st_, (void*)prompt_,
+                  attn_scratch_, (void*)proj_part_, (void*)hmid_, (void*)inv_freq_, (void*)st_,
+                  (void*)prompt_,
                   (void*)out_, (void*)forced_}) {
     if (!p) {
       if (err) *err = "device allocation of scratch failed";
@@ -204,8 +207,12 @@ AttnArgs Engine::attn_args(const LayerDev& L, int splits) {
   return a;
 }
 
-// Kernel order of encode_forward with rows == 1 (model.rs:228-307): per GDN
-// layer 5 launches, per attention layer 6, embedding fused into layer 0.
+// Kernel order of encode_forward with rows == 1 (model.rs:228-307), per
+// layer: GDN = input norm + projections, recurrence + gated norm + out_proj
+// head partials, residual + post norm + gate/up, down + residual (4
+// launches); attention = input norm + q/k/v, fused attention, merge + gate +
+// o_proj head partials, residual + post norm + gate/up, down + residual (5).
+// The embedding is fused into layer 0's first launch.
 hipError_t Engine::enqueue_layers(hipStream_t s, int splits) {
   hipError_t e;
   for (int l = 0; l < shape_.n_layers; ++l) {
@@ -233,10 +240,16 @@ hipError_t Engine::enqueue_layers(hipStream_t s, int splits) {
       g.a_log = L.a_log;
       g.dt_bias = L.dt_bias;
       g.state = L.state;
-      g.y = y_;
       g.st = st_;
-      if ((e = launch_gdn_recur(g, s)) != hipSuccess) return e;
-      if ((e = launch_gdn_gate_out(L.out, y_, z_, L.gdn_norm, h_, nullptr, s)) != hipSuccess)
+      GdnOutArgs go{};
+      go.r = g;
+      go.z = z_;
+      go.norm_w = L.gdn_norm;
+      go.out = L.out;
+      go.part = proj_part_;
+      if ((e = launch_gdn_recur_out(go, s)) != hipSuccess) return e;
+      if ((e = launch_norm_gate_up_parts(L.gate, L.up, h_, proj_part_, kGdnHeads, hmid_,
+                                         L.post_norm, act_, s)) != hipSuccess)
         return e;
     } else {
       nm.count = 3;
@@ -246,12 +259,13 @@ hipError_t Engine::enqueue_layers(hipStream_t s, int splits) {
       if ((e = launch_norm_multi(nm, s)) != hipSuccess) return e;
       const AttnArgs a = attn_args(L, splits);
       if ((e = launch_attn_fused(a, s)) != hipSuccess) return e;
-      if ((e = launch_attn_merge(a, s)) != hipSuccess) return e;
-      if ((e = launch_qmv(L.o, y_, h_, h_, nullptr, s)) != hipSuccess) return e;
+      if ((e = launch_attn_merge_out(a, L.o, proj_part_, s)) != hipSuccess) return e;
+      if ((e = launch_norm_gate_up_parts(L.gate, L.up, h_, proj_part_, kQHeads, hmid_,
+                                         L.post_norm, act_, s)) != hipSuccess)
+        return e;
     }
-    if ((e = launch_norm_gate_up(L.gate, L.up, h_, L.post_norm, nullptr, act_, s)) != hipSuccess)
-      return e;
-    if ((e = launch_qmv(L.down, act_, h_, h_, nullptr, s)) != hipSuccess) return e;
+    // MLP down projection; its residual is the stream after the mixer (hmid_)
+    if ((e = launch_qmv(L.down, act_, hmid_, h_, nullptr, s)) != hipSuccess) return e;
   }
   return hipSuccess;
 }

@@ -113,7 +113,9 @@ class Engine {
   uint16_t* act_ = nullptr;     // [3584]
   uint16_t* logits_ = nullptr;  // [vocab]
   float* head_part_ = nullptr;
-  void* attn_scratch_ = nullptr;  // chain outputs, chain (max, sum), scores
+  void* attn_scratch_ = nullptr;  // chain outputs, chain (max, sum)
+  float* proj_part_ = nullptr;    // [16, 1024] head partials of out_proj / o_proj
+  uint16_t* hmid_ = nullptr;      // [1024] residual after the attention / GDN mixer
   float* inv_freq_ = nullptr;
   StepState* st_ = nullptr;
   uint32_t* prompt_ = nullptr;  // [capacity]

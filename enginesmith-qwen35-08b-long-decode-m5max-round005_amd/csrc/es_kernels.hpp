@@ -35,6 +35,13 @@ hipError_t launch_norm_gate_up(const Q4& gate, const Q4& up, const uint16_t* x,
                                const uint16_t* gain, uint16_t* norm_out, uint16_t* act,
                                hipStream_t s);
 
+// Engine path: h_new = bf16(h_old + bf16(pairwise sum of nparts head
+// partials [nparts, 1024])) (8: o_proj, 16: GDN out_proj), then as above
+// on h_new. h_new must not alias h_old.
+hipError_t launch_norm_gate_up_parts(const Q4& gate, const Q4& up, const uint16_t* h_old,
+                                     const float* part, int nparts, uint16_t* h_new,
+                                     const uint16_t* gain, uint16_t* act, hipStream_t s);
+
 // y = bf16(W x) or, with residual, y = bf16(residual + bf16(W x)). x bf16[K].
 // K == 1024 or 1024 < K <= 4096 with K % 64 == 0. y may alias residual.
 hipError_t launch_qmv(const Q4& w, const uint16_t* x, const uint16_t* residual, uint16_t* y,
@@ -60,6 +67,18 @@ struct GdnRecurArgs {
   int pos_val;
 };
 hipError_t launch_gdn_recur(const GdnRecurArgs& a, hipStream_t s);
+
+// Engine path: recurrence + gated RMSNorm + out_proj partials per head
+// (part[h][r] = the head's 128 columns of row r, the four slice partials
+// combined pairwise); the next launch adds the 16 partials pairwise.
+struct GdnOutArgs {
+  GdnRecurArgs r;           // y, qkv_out, g_out, beta_out unused
+  const uint16_t* z;        // [2048] output-gate projection
+  const uint16_t* norm_w;   // [128]
+  Q4 out;                   // out_proj [1024, 2048]
+  float* part;              // [16, 1024]
+};
+hipError_t launch_gdn_recur_out(const GdnOutArgs& a, hipStream_t s);
 
 // Gated RMSNorm of y by z (per 128-wide head) feeding out_proj (K=2048) with
 // the residual add: h = bf16(h + bf16(W gated)). gated_out (optional) receives
@@ -98,6 +117,10 @@ size_t attn_scratch_bytes(int capacity);
 void attn_bind_scratch(AttnArgs& a, void* scratch);
 hipError_t launch_attn_fused(const AttnArgs& a, hipStream_t s);
 hipError_t launch_attn_merge(const AttnArgs& a, hipStream_t s);
+// Engine path: merge + gate, then o_proj partials per head (part[h][r] = the
+// head's 256 columns of row r, its eight slice partials combined pairwise);
+// the next launch adds the 8 partials pairwise.
+hipError_t launch_attn_merge_out(const AttnArgs& a, const Q4& o, float* part, hipStream_t s);
 
 // ---- vocab head, k_head.hip ----
 struct HeadArgs {

@@ -474,43 +474,38 @@ __device__ __forceinline__ float tree_reg32(float* v) {
   return v[0];
 }
 
-__global__ __launch_bounds__(64) void k_attn_merge(AttnArgs a) {
-  __shared__ float fac[kAttnMaxChains];
-  __shared__ float total;
-  const int lane = threadIdx.x, h = blockIdx.x;
-  const int d = blockIdx.y * 64 + lane;
-  const int pos = load_pos(a.st, a.pos_val);
-  const bool two_pass = pos + 1 >= kAttnRouteSplit;
+// Chain factors of head h for the merge, by one 64-lane wave: fac[l] =
+// exp(max_l - max) and *total = the weighted sum of the chain sums
+// (attention_decode.metal:858-862 for the long route).
+__device__ __forceinline__ void merge_factors(const AttnArgs& a, int h, int lane, bool two_pass,
+                                              float* fac, float* total) {
   const float* ml = a.part_ml + (size_t)h * kAttnMaxChains * 2;
-  const float* po = a.part_o + (size_t)h * kAttnMaxChains * 256 + d;
-  float v[kAttnMaxChains];
-  // Chain outputs first: independent loads in flight while the factors form.
-#pragma unroll
-  for (int c = 0; c < 32; ++c) v[c] = po[(size_t)c * 256];
   if (two_pass) {
-#pragma unroll
-    for (int c = 32; c < 64; ++c) v[c] = po[(size_t)c * 256];
     const float mx = ml[2 * lane];
     const float F = es_exp(mx - wave_max(mx));
     fac[lane] = F;
     // lane l < 32: (0 + F_l s_l) + F_{l+32} s_{l+32}, then pairwise over lanes
-    // (attention_decode.metal:858-862).
     const float prod = F * ml[2 * lane + 1];
     const float hi = __shfl_down(prod, 32, 64);
     float s = 0.0f;
     s = s + prod;
     s = s + hi;
     s = tree32(s);
-    if (lane == 0) total = s;
+    if (lane == 0) *total = s;
   } else {
     const float mx = lane < 32 ? ml[2 * lane] : kFiniteMin;
     const float F = es_exp(mx - wave_max(mx));
     if (lane < 32) fac[lane] = F;
     const float s = tree32(ml[2 * (lane & 31) + 1] * F);
-    if (lane == 0) total = s;
+    if (lane == 0) *total = s;
   }
-  __syncthreads();
-  const float sum = total;
+}
+
+// Merged, normalised and gated value of dim d of head h: bf16(bf16(o) *
+// sigmoid_bf(gate)) with o = (sum of factor-weighted chain outputs) / total;
+// v holds the 64 chain outputs of the dim (loaded by the caller).
+__device__ __forceinline__ uint32_t merge_dim(const AttnArgs& a, int h, int d, bool two_pass,
+                                              const float* fac, float sum, float* v) {
   float o;
   if (two_pass) {
     float w[32];
@@ -530,7 +525,75 @@ __global__ __launch_bounds__(64) void k_attn_merge(AttnArgs a) {
   o = sum == 0.0f ? o : o / sum;
   const float attention = rbf(o);
   const float gate = sigmoid_bf(bf2f(a.q_proj[h * 512 + 256 + d]));
-  a.gated[h * 256 + d] = (uint16_t)f2bf(attention * gate);
+  return f2bf(attention * gate);
+}
+
+__device__ __forceinline__ void load_chain_outputs(const AttnArgs& a, int h, int d, bool two_pass,
+                                                   float* v) {
+  const float* po = a.part_o + (size_t)h * kAttnMaxChains * 256 + d;
+#pragma unroll
+  for (int c = 0; c < 32; ++c) v[c] = po[(size_t)c * 256];
+  if (two_pass) {
+#pragma unroll
+    for (int c = 32; c < 64; ++c) v[c] = po[(size_t)c * 256];
+  }
+}
+
+__global__ __launch_bounds__(64) void k_attn_merge(AttnArgs a) {
+  __shared__ float fac[kAttnMaxChains];
+  __shared__ float total;
+  const int lane = threadIdx.x, h = blockIdx.x;
+  const int d = blockIdx.y * 64 + lane;
+  const int pos = load_pos(a.st, a.pos_val);
+  const bool two_pass = pos + 1 >= kAttnRouteSplit;
+  float v[kAttnMaxChains];
+  // Chain outputs first: independent loads in flight while the factors form.
+  load_chain_outputs(a, h, d, two_pass, v);
+  merge_factors(a, h, lane, two_pass, fac, &total);
+  __syncthreads();
+  a.gated[h * 256 + d] = (uint16_t)merge_dim(a, h, d, two_pass, fac, total, v);
+}
+
+// Engine path: merge + gate of head h (every one of the 8 blocks of the head
+// forms all 256 dims) and the head's share of o_proj for output rows
+// 128*rg .. +127: per row the eight 32-column slice partials combined by
+// tree8. The 64-slice tree of a K=2048 row pairs adjacent slices first, so the
+// row's full sum is the pairwise tree8 of the 8 head partials, formed by the
+// next launch, bit for bit.
+__global__ __launch_bounds__(256) void k_attn_merge_out(AttnArgs a, Q4 o, float* part) {
+  __shared__ float fac[kAttnMaxChains];
+  __shared__ float total;
+  __shared__ float gx[256 + 8];  // gated output, slice s at gx[33 s ..]
+  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+  const int h = blockIdx.x, rg = blockIdx.y;  // a head's blocks share an XCD
+  const int sl = t & 7, gs = 8 * h + sl;  // K slice of this lane
+  u32x4 oc[4];
+  uint32_t osv[4], obv[4];
+#pragma unroll
+  for (int p = 0; p < 4; ++p) {
+    const size_t row = (size_t)rg * 128 + 32 * p + (t >> 3);
+    oc[p] = *reinterpret_cast<const u32x4*>(o.w + row * 256 + gs * 4);
+    osv[p] = o.s[row * 32 + gs / 2];
+    obv[p] = o.b[row * 32 + gs / 2];
+  }
+  const int pos = load_pos(a.st, a.pos_val);
+  const bool two_pass = pos + 1 >= kAttnRouteSplit;
+  float v[kAttnMaxChains];
+  load_chain_outputs(a, h, t, two_pass, v);
+  if (wave == 0) merge_factors(a, h, lane, two_pass, fac, &total);
+  __syncthreads();
+  gx[t + (t >> 5)] = bf2f(merge_dim(a, h, t, two_pass, fac, total, v));
+  __syncthreads();
+  float xv[32], xr[32];
+#pragma unroll
+  for (int q = 0; q < 32; ++q) xv[q] = gx[sl * 33 + q];
+  const float xs = prep_slice(xv, xr);
+#pragma unroll
+  for (int p = 0; p < 4; ++p) {
+    const int row = rg * 128 + 32 * p + (t >> 3);
+    const float pp = tree8(q4_slice(oc[p], osv[p], obv[p], xr, xs));
+    if (sl == 0) part[(size_t)h * 1024 + row] = pp;
+  }
 }
 
 bool attn_ok(const AttnArgs& a) {
@@ -555,6 +618,13 @@ void attn_bind_scratch(AttnArgs& a, void* scratch) {
 hipError_t launch_attn_fused(const AttnArgs& a, hipStream_t s) {
   if (!attn_ok(a)) return hipErrorInvalidValue;
   hipLaunchKernelGGL(k_attn_fused, dim3(kKvHeads * kAttnMaxChains * 2), dim3(kFusedThreads), 0, s, a);
+  return hipGetLastError();
+}
+
+hipError_t launch_attn_merge_out(const AttnArgs& a, const Q4& o, float* part, hipStream_t s) {
+  if (!attn_ok(a) || !o.w || !o.s || !o.b || o.n != kHidden || o.k != 2048 || !part)
+    return hipErrorInvalidValue;
+  hipLaunchKernelGGL(k_attn_merge_out, dim3(kQHeads, 8), dim3(256), 0, s, a, o, part);
   return hipGetLastError();
 }
 

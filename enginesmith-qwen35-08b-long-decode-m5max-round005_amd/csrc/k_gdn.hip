@@ -136,6 +136,145 @@ __global__ __launch_bounds__(256) void k_gdn_recur(GdnRecurArgs a) {
   reinterpret_cast<float4*>(sp)[1] = make_float4(S[4], S[5], S[6], S[7]);
 }
 
+// Recurrence + gated RMSNorm + the head's share of out_proj, one launch per
+// layer for the engine. Grid: 16 heads x 8 row-groups (block id = 16 rg + h,
+// so a head's blocks share an XCD and its state is read once into that XCD's
+// L2), 512 threads. Every
+// block runs the whole head's recurrence (its 128 value rows, 4 passes of 32
+// rows, 16 lanes per row and 8 keys per lane, the same arithmetic and order as
+// k_gdn_recur) so it holds all 128 readouts, writes back only its own 16 state
+// rows (all blocks compute the same values), forms the gated norm of the head
+// (gdn.metal:238-254, 8 channels per lane, tree16) and the out_proj partial of
+// output rows 128*rg .. +127 over the head's 128 columns: per row the four
+// 32-column slice partials of k_gdn_gate_out combined by tree4. Because the
+// 64-slice tree of a K=2048 row pairs adjacent slices first, the row's full
+// sum is the pairwise tree16 of these 16 head partials, formed by the next
+// launch, bit for bit.
+__global__ __launch_bounds__(512) void k_gdn_recur_out(GdnOutArgs a) {
+  __shared__ float qk[256];
+  __shared__ float vv[128];
+  __shared__ float red[4];
+  __shared__ float gates[2];
+  __shared__ float yv[128];
+  __shared__ float xg[128 + 4];  // gated output, slice s at xg[33 s ..]
+  __shared__ float ginv;
+  const GdnRecurArgs& r = a.r;
+  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+  const int h = blockIdx.x, rg = blockIdx.y;
+  const int j = t & 15;
+
+  // ---- loads first (state of 4 rows per thread, out_proj slice, conv taps, z)
+  float S[4][8];
+#pragma unroll
+  for (int p = 0; p < 4; ++p) {
+    const float* sp = r.state + ((size_t)(h * 128 + p * 32 + (t >> 4))) * 128 + 8 * j;
+    const float4 lo = reinterpret_cast<const float4*>(sp)[0];
+    const float4 hi = reinterpret_cast<const float4*>(sp)[1];
+    S[p][0] = lo.x; S[p][1] = lo.y; S[p][2] = lo.z; S[p][3] = lo.w;
+    S[p][4] = hi.x; S[p][5] = hi.y; S[p][6] = hi.z; S[p][7] = hi.w;
+  }
+  const int orow = rg * 128 + (t >> 2), osl = 4 * h + (t & 3);  // output row, K slice
+  const u32x4 oc = *reinterpret_cast<const u32x4*>(a.out.w + (size_t)orow * 256 + osl * 4);
+  const uint32_t osv = a.out.s[(size_t)orow * 32 + osl / 2];
+  const uint32_t obv = a.out.b[(size_t)orow * 32 + osl / 2];
+  // conv channels: q (t < 128), k (t < 256), v (t < 384)
+  const int c = t < 128 ? h * 128 + t : t < 256 ? 2048 + h * 128 + (t - 128) : 4096 + h * 128 + (t - 256);
+  RingTaps rt;
+  if (t < 384) ring_load(r.ring, r.conv_w, c, rt);
+  // gated norm inputs: element t (t < 128) of z and of the norm weight
+  uint32_t zb = 0u, wb = 0u;
+  if (t < 128) {
+    zb = a.z[h * 128 + t];
+    wb = a.norm_w[t];
+  }
+  const int pos = load_pos(r.st, r.pos_val);
+
+  // ---- conv + SiLU, q/k L2 norm, gates (as k_gdn_recur)
+  float v = 0.0f;
+  if (t < 384) v = conv_silu(rt, pos);
+  if (t < 256) {
+    const float ss = tree64(v * v);
+    if (lane == 0) red[wave] = ss;
+  } else if (t < 384) {
+    vv[t - 256] = v;
+  } else if (t == 384) {
+    const float ax = rbf(bf2f(r.ab[h]) + bf2f(r.dt_bias[h]));
+    gates[0] = es_exp(-es_exp(r.a_log[h]) * softplus_bf(ax));
+    gates[1] = sigmoid_bf(bf2f(r.ab[16 + h]));
+  }
+  __syncthreads();
+  if (t < 256) {
+    const float tot = t < 128 ? red[0] + red[1] : red[2] + red[3];
+    const float inv = 1.0f / sqrtf(tot / 128.0f + 1.0e-6f / 128.0f);
+    const float scale = t < 128 ? 0.0078125f : rbf(0.08838834764831845f);
+    qk[t] = rbf(rbf(v * inv) * scale);
+  }
+  __syncthreads();
+
+  // ---- recurrence of the head's 128 value rows
+  const float g = gates[0], beta = gates[1];
+  float kk[8], qq[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    kk[i] = qk[128 + 8 * j + i];
+    qq[i] = qk[8 * j + i];
+  }
+#pragma unroll
+  for (int p = 0; p < 4; ++p) {
+    const int row = p * 32 + (t >> 4);
+    float mem = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      S[p][i] = S[p][i] * g;
+      mem = fmaf(S[p][i], kk[i], mem);
+    }
+    mem = tree16(mem);
+    const float delta = (vv[row] - mem) * beta;
+    float out = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      S[p][i] = fmaf(kk[i], delta, S[p][i]);
+      out = fmaf(S[p][i], qq[i], out);
+    }
+    out = tree16(out);
+    if (j == 0) yv[row] = bf2f(f2bf(out));
+    if ((row >> 4) == rg) {
+      float* sp = r.state + ((size_t)(h * 128 + row)) * 128 + 8 * j;
+      reinterpret_cast<float4*>(sp)[0] = make_float4(S[p][0], S[p][1], S[p][2], S[p][3]);
+      reinterpret_cast<float4*>(sp)[1] = make_float4(S[p][4], S[p][5], S[p][6], S[p][7]);
+    }
+  }
+  __syncthreads();
+
+  // ---- gated RMSNorm of the head (as k_gdn_gate_out): sum of squares as 16
+  // lanes x 8 channels (fma chain, tree16), then one channel per thread
+  if (t < 16) {
+    float ss = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) ss = fmaf(yv[t * 8 + i], yv[t * 8 + i], ss);
+    ss = tree16(ss);
+    if (t == 0) ginv = 1.0f / sqrtf(ss / 128.0f + 1e-6f);
+  }
+  __syncthreads();
+  if (t < 128) {
+    const float norm = rbf(rbf(yv[t] * ginv) * bf2f(wb));
+    const float gz = bf2f(zb);
+    const float sy = 1.0f / (1.0f + es_exp(fabsf(gz)));
+    const float sig = gz < 0.0f ? sy : 1.0f - sy;
+    xg[t + (t >> 5)] = rbf((gz * sig) * norm);
+  }
+  __syncthreads();
+
+  // ---- out_proj partial: 4 lanes per output row, one 32-column slice each
+  float xv[32], xr[32];
+  const int sl = t & 3;
+#pragma unroll
+  for (int q = 0; q < 32; ++q) xv[q] = xg[sl * 33 + q];
+  const float xs = prep_slice(xv, xr);
+  const float part = tree4(q4_slice(oc, osv, obv, xr, xs));
+  if (sl == 0) a.part[(size_t)h * 1024 + orow] = part;
+}
+
 }  // namespace
 
 hipError_t launch_gdn_recur(const GdnRecurArgs& a, hipStream_t s) {
@@ -143,6 +282,16 @@ hipError_t launch_gdn_recur(const GdnRecurArgs& a, hipStream_t s) {
     return hipErrorInvalidValue;
   if (!a.st && a.pos_val < 0) return hipErrorInvalidValue;
   hipLaunchKernelGGL(k_gdn_recur, dim3(8, kGdnHeads), dim3(256), 0, s, a);
+  return hipGetLastError();
+}
+
+hipError_t launch_gdn_recur_out(const GdnOutArgs& a, hipStream_t s) {
+  const GdnRecurArgs& r = a.r;
+  if (!r.ring || !r.conv_w || !r.ab || !r.a_log || !r.dt_bias || !r.state || !a.z || !a.norm_w ||
+      !a.part || !a.out.w || !a.out.s || !a.out.b || a.out.n != kHidden || a.out.k != 2048)
+    return hipErrorInvalidValue;
+  if (!r.st && r.pos_val < 0) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(k_gdn_recur_out, dim3(kGdnHeads, 8), dim3(512), 0, s, a);
   return hipGetLastError();
 }
 

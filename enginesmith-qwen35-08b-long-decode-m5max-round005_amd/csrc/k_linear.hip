@@ -190,6 +190,98 @@ __global__ __launch_bounds__(256) void k_norm_gate_up(Q4 gate, Q4 up, const uint
   }
 }
 
+// Pairwise sum of N head partials in index order (the upper levels of the
+// 64-slice row tree).
+template <int N>
+__device__ __forceinline__ float pair_sum(const float* v) {
+  if constexpr (N == 1) {
+    return v[0];
+  } else {
+    return pair_sum<N / 2>(v) + pair_sum<N / 2>(v + N / 2);
+  }
+}
+
+// As k_norm_gate_up, but the input is formed here from the previous
+// projection's head partials: h = bf16(h_old + bf16(pair_sum(partials)))
+// (the residual epilogue of the K=2048 projection), written to h_new by block
+// 0 for the next launch's residual. Thread t forms elements 4t..4t+3; they
+// pass through LDS so every lane also has its 32-element slice.
+template <int NP, int NPART>
+__global__ __launch_bounds__(256) void k_norm_gate_up_parts(Q4 gate, Q4 up, const uint16_t* h_old,
+                                                            const float* part, uint16_t* h_new,
+                                                            const uint16_t* gain, uint16_t* act) {
+  __shared__ float hs[kNormLds];
+  __shared__ float norm_lds[kNormLds];
+  const int t = threadIdx.x;
+  const int lane = t & 63, wave = t >> 6, half = lane >> 5, sl = lane & 31;
+  const int base = (blockIdx.x * 4 + wave) * (2 * NP);
+  u32x4 cg[NP], cu[NP];
+  uint32_t sg[NP], bg[NP], su[NP], bu[NP];
+  int rr[NP];
+#pragma unroll
+  for (int p = 0; p < NP; ++p) {
+    const int r = base + 2 * p + half;
+    rr[p] = r;
+    const int rl = r < gate.n ? r : 0;
+    cg[p] = *reinterpret_cast<const u32x4*>(gate.w + (size_t)rl * 128 + sl * 4);
+    cu[p] = *reinterpret_cast<const u32x4*>(up.w + (size_t)rl * 128 + sl * 4);
+    sg[p] = gate.s[(size_t)rl * 16 + sl / 2];
+    bg[p] = gate.b[(size_t)rl * 16 + sl / 2];
+    su[p] = up.s[(size_t)rl * 16 + sl / 2];
+    bu[p] = up.b[(size_t)rl * 16 + sl / 2];
+  }
+  const uint2 ho = reinterpret_cast<const uint2*>(h_old)[t];
+  const uint2 g4 = reinterpret_cast<const uint2*>(gain)[t];
+  float4 pv[NPART];
+#pragma unroll
+  for (int k = 0; k < NPART; ++k) pv[k] = reinterpret_cast<const float4*>(part + k * kHidden)[t];
+  issue_fence();
+  float hn[4];
+  {
+    const float hf[4] = {bf_lo(ho.x), bf_hi(ho.x), bf_lo(ho.y), bf_hi(ho.y)};
+    float c[NPART];
+#pragma unroll
+    for (int k = 0; k < NPART; ++k) c[k] = pv[k].x;
+    hn[0] = bf2f(f2bf(hf[0] + rbf(pair_sum<NPART>(c))));
+#pragma unroll
+    for (int k = 0; k < NPART; ++k) c[k] = pv[k].y;
+    hn[1] = bf2f(f2bf(hf[1] + rbf(pair_sum<NPART>(c))));
+#pragma unroll
+    for (int k = 0; k < NPART; ++k) c[k] = pv[k].z;
+    hn[2] = bf2f(f2bf(hf[2] + rbf(pair_sum<NPART>(c))));
+#pragma unroll
+    for (int k = 0; k < NPART; ++k) c[k] = pv[k].w;
+    hn[3] = bf2f(f2bf(hf[3] + rbf(pair_sum<NPART>(c))));
+  }
+  const uint2 x4 = make_uint2(pack_bf2(hn[0], hn[1]), pack_bf2(hn[2], hn[3]));
+  if (blockIdx.x == 0) reinterpret_cast<uint2*>(h_new)[t] = x4;
+  *reinterpret_cast<float4*>(hs + (t >> 3) * 36 + (t & 7) * 4) = make_float4(hn[0], hn[1], hn[2], hn[3]);
+  __syncthreads();
+  float xv[32];
+  {
+    const float4* r = reinterpret_cast<const float4*>(hs + sl * 36);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const float4 q = r[i];
+      xv[4 * i] = q.x; xv[4 * i + 1] = q.y; xv[4 * i + 2] = q.z; xv[4 * i + 3] = q.w;
+    }
+  }
+  float xn[32];
+  norm_block_1024(xv, x4, g4, norm_lds, xn);
+  float xr[32];
+  const float xs = prep_slice(xn, xr);
+#pragma unroll
+  for (int p = 0; p < NP; ++p) {
+    const float g = tree32(q4_slice(cg[p], sg[p], bg[p], xr, xs));
+    const float u = tree32(q4_slice(cu[p], su[p], bu[p], xr, xs));
+    if (sl == 0 && rr[p] < gate.n) {
+      const float gb = rbf(g), ub = rbf(u);
+      const float silu = rbf(gb * sigmoid_bf(gb));
+      act[rr[p]] = (uint16_t)f2bf(silu * ub);
+    }
+  }
+}
+
 // Plain / residual QMV for K == 1024 (half-wave rows).
 template <int P, bool ADD>
 __global__ __launch_bounds__(256) void k_qmv_narrow(Q4 m, const uint16_t* x,
@@ -434,6 +526,25 @@ hipError_t launch_norm_gate_up(const Q4& gate, const Q4& up, const uint16_t* x,
   const int blocks = (gate.n + rows_per_block - 1) / rows_per_block;
   hipLaunchKernelGGL(k_norm_gate_up<kGateUpNP>, dim3(blocks), dim3(256), 0, s, gate, up, x, gain,
                      norm_out, act);
+  return hipGetLastError();
+}
+
+hipError_t launch_norm_gate_up_parts(const Q4& gate, const Q4& up, const uint16_t* h_old,
+                                     const float* part, int nparts, uint16_t* h_new,
+                                     const uint16_t* gain, uint16_t* act, hipStream_t s) {
+  if (!q4_ok(gate) || !q4_ok(up) || gate.k != kHidden || up.k != kHidden || gate.n != up.n ||
+      !h_old || !part || !h_new || h_new == h_old || !gain || !act)
+    return hipErrorInvalidValue;
+  const int rows_per_block = 4 * 2 * kGateUpNP;
+  const int blocks = (gate.n + rows_per_block - 1) / rows_per_block;
+  if (nparts == 16)
+    hipLaunchKernelGGL((k_norm_gate_up_parts<kGateUpNP, 16>), dim3(blocks), dim3(256), 0, s, gate, up,
+                       h_old, part, h_new, gain, act);
+  else if (nparts == 8)
+    hipLaunchKernelGGL((k_norm_gate_up_parts<kGateUpNP, 8>), dim3(blocks), dim3(256), 0, s, gate, up,
+                       h_old, part, h_new, gain, act);
+  else
+    return hipErrorInvalidValue;
   return hipGetLastError();
 }
 
