@@ -251,6 +251,10 @@ __device__ __forceinline__ void unpack_bf16x32(const Raw64& r, float* out) {
     }
 }
 
+// Cache-policy operand of the global->LDS and buffer load builtins that sets
+// the non-temporal (streaming) hint on gfx950.
+constexpr int kLoadNonTemporal = 2;
+
 // Keeps the machine scheduler from moving instructions across this point, so
 // loads issued above it are in flight before the arithmetic below starts.
 __device__ __forceinline__ void issue_fence() { __builtin_amdgcn_sched_barrier(0); }

@@ -151,7 +151,9 @@ __device__ __forceinline__ void wait_tiles(int later) {
 // Issue tile t of one ring (K or V rows of the chain) from a producer wave:
 // 32 rows as 16 DMA of 1 KB (lanes 0..31 one row, 32..63 the next). Rows
 // past the chain's end re-read its last row (in bounds; their scores are
-// masked and their exp scores are 0).
+// masked and their exp scores are 0). The reads are non-temporal: the KV
+// stream is far larger than the on-package cache and would otherwise evict
+// the weights the small kernels read again next step.
 __device__ __forceinline__ void issue_rows(uint16_t (*ring)[kTile][256], const uint16_t* row0, int C,
                                            int L, int t, int lane) {
   uint16_t(*dst)[256] = ring[t % kStages];
@@ -160,7 +162,7 @@ __device__ __forceinline__ void issue_rows(uint16_t (*ring)[kTile][256], const u
     const int r = 2 * x;
     const int j = min(t * kTile + r + (lane >> 5), L - 1);
     const uint16_t* g = row0 + (size_t)j * C * 256 + (lane & 31) * 8;
-    __builtin_amdgcn_global_load_lds(g, (lds_ptr_t)&dst[r][0], 16, 0, 0);
+    __builtin_amdgcn_global_load_lds(g, (lds_ptr_t)&dst[r][0], 16, 0, kLoadNonTemporal);
   }
 }
 

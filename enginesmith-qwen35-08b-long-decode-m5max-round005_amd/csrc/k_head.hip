@@ -39,7 +39,9 @@ struct HeadBatch {
 
 // Buffer resources over the codes, scales and biases of the table: rows past
 // the vocabulary are out of range and read as zero, so no row is clamped, and
-// the per-row offsets are immediates on one per-lane base offset.
+// the per-row offsets are immediates on one per-lane base offset. The table
+// (143 MB, read once per step) is read non-temporally so it does not evict
+// the layer weights from the on-package cache.
 struct HeadRsrc {
   __amdgpu_buffer_rsrc_t w, s, b;
 };
@@ -49,9 +51,9 @@ __device__ __forceinline__ void head_load(const HeadRsrc& rs, int voff_c, int vo
 #pragma unroll
   for (int p = 0; p < kPassBatch; ++p) {
     const int dr = it * 2 * kPassBatch + 2 * p;  // rows past the lane's first row
-    hb.c[p] = __builtin_amdgcn_raw_buffer_load_b128(rs.w, voff_c + dr * 512, 0, 0);
-    hb.s[p] = __builtin_amdgcn_raw_buffer_load_b16(rs.s, voff_s + dr * 32, 0, 0);
-    hb.b[p] = __builtin_amdgcn_raw_buffer_load_b16(rs.b, voff_s + dr * 32, 0, 0);
+    hb.c[p] = __builtin_amdgcn_raw_buffer_load_b128(rs.w, voff_c + dr * 512, 0, kLoadNonTemporal);
+    hb.s[p] = __builtin_amdgcn_raw_buffer_load_b16(rs.s, voff_s + dr * 32, 0, kLoadNonTemporal);
+    hb.b[p] = __builtin_amdgcn_raw_buffer_load_b16(rs.b, voff_s + dr * 32, 0, kLoadNonTemporal);
   }
 }
 

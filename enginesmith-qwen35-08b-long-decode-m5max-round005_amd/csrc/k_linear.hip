@@ -73,35 +73,34 @@ struct MultiDev {
 
 template <int P, bool EMBED>
 __global__ __launch_bounds__(256) void k_norm_multi(MultiDev a) {
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, half = lane >> 5, sl = lane & 31;
+  const int lane = threadIdx.x & 63, half = lane >> 5, sl = lane & 31;
+  // A wave's 2P rows lie in one matrix (every matrix has a multiple of 2P
+  // rows), so the matrix and its pointers are wave-uniform (scalar registers).
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int wrow0 = (blockIdx.x * 4 + wave) * (2 * P);
+  const bool wvalid = wrow0 < a.total;
+  int m = 0, local0 = wvalid ? wrow0 : 0;
+#pragma unroll
+  for (int i = 0; i < 3; ++i) {
+    if (m == i && i + 1 < a.count && local0 >= a.m[i].n) {
+      local0 -= a.m[i].n;
+      m = i + 1;
+    }
+  }
+  const Q4 q = m == 0 ? a.m[0] : m == 1 ? a.m[1] : m == 2 ? a.m[2] : a.m[3];
   // Weight loads first: they do not depend on the input, so their latency
-  // overlaps the input load and the normalisation below.
-  const int base = (blockIdx.x * 4 + wave) * (2 * P);
+  // overlaps the input load and the normalisation below. They are
+  // non-temporal: the input projections (94 MB per step) are left out of the
+  // on-package cache so that the other layer weights (about 200 MB) stay in it
+  // from one step to the next.
   u32x4 c[P];
   uint32_t sv[P], bv[P];
-  int mi[P], lr[P];
 #pragma unroll
   for (int p = 0; p < P; ++p) {
-    const int r = base + 2 * p + half;
-    // Row r of the concatenation -> (matrix m, local row), without branches so
-    // that every load below is issued before the first wait.
-    int local = r < a.total ? r : 0;
-    int m = 0;
-#pragma unroll
-    for (int i = 0; i < 3; ++i) {
-      const bool adv = m == i && i + 1 < a.count && local >= a.m[i].n;
-      local = adv ? local - a.m[i].n : local;
-      m = adv ? i + 1 : m;
-    }
-    const Q4& q = a.m[0];
-    const uint32_t* w = m == 0 ? q.w : m == 1 ? a.m[1].w : m == 2 ? a.m[2].w : a.m[3].w;
-    const uint16_t* s = m == 0 ? q.s : m == 1 ? a.m[1].s : m == 2 ? a.m[2].s : a.m[3].s;
-    const uint16_t* b = m == 0 ? q.b : m == 1 ? a.m[1].b : m == 2 ? a.m[2].b : a.m[3].b;
-    mi[p] = r < a.total ? m : -1;
-    lr[p] = local;
-    c[p] = *reinterpret_cast<const u32x4*>(w + (size_t)local * 128 + sl * 4);
-    sv[p] = s[(size_t)local * 16 + sl / 2];
-    bv[p] = b[(size_t)local * 16 + sl / 2];
+    const int local = local0 + 2 * p + half;
+    c[p] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(q.w + (size_t)local * 128 + sl * 4));
+    sv[p] = __builtin_nontemporal_load(q.s + (size_t)local * 16 + sl / 2);
+    bv[p] = __builtin_nontemporal_load(q.b + (size_t)local * 16 + sl / 2);
   }
 
   __shared__ float norm_lds[kNormLds];
@@ -130,15 +129,12 @@ __global__ __launch_bounds__(256) void k_norm_multi(MultiDev a) {
   float xr[32];
   const float xs = prep_slice(xn, xr);
 
-  uint16_t* y0 = a.y[0];
-  if (a.ring0) y0 += (size_t)((a.st ? pos_raw : a.pos_val) & 3) * a.m[0].n;
+  uint16_t* y = m == 0 ? a.y[0] : m == 1 ? a.y[1] : m == 2 ? a.y[2] : a.y[3];
+  if (m == 0 && a.ring0) y += (size_t)((a.st ? pos_raw : a.pos_val) & 3) * a.m[0].n;
 #pragma unroll
   for (int p = 0; p < P; ++p) {
     const float part = tree32(q4_slice(c[p], sv[p], bv[p], xr, xs));
-    if (sl == 0 && mi[p] >= 0) {
-      uint16_t* y = mi[p] == 0 ? y0 : mi[p] == 1 ? a.y[1] : mi[p] == 2 ? a.y[2] : a.y[3];
-      y[lr[p]] = (uint16_t)f2bf(part);
-    }
+    if (sl == 0 && wvalid) y[local0 + 2 * p + half] = (uint16_t)f2bf(part);
   }
 }
 
@@ -487,7 +483,8 @@ hipError_t launch_norm_multi(const NormMultiArgs& a, hipStream_t s) {
   MultiDev d{};
   int total = 0;
   for (int i = 0; i < a.count; ++i) {
-    if (!q4_ok(a.m[i]) || a.m[i].k != kHidden || !a.y[i]) return hipErrorInvalidValue;
+    if (!q4_ok(a.m[i]) || a.m[i].k != kHidden || !a.y[i] || a.m[i].n % (2 * kMultiP) != 0)
+      return hipErrorInvalidValue;
     d.m[i] = a.m[i];
     d.y[i] = a.y[i];
     total += a.m[i].n;

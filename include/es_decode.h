@@ -91,7 +91,7 @@ int es_q4_matvec_add(const es_q4* w, const uint16_t* x, const uint16_t* residual
 /* qmv_multi_g8_norm (linear_input_norm.metal:13-119) with the rms_norm_bf16
  * arithmetic (linear.metal:300-331): u = bf16(bf16(x*rsqrt(mean(x^2)+1e-6))*gain)
  * over 1024 columns, then y[i] = bf16(W_i u) for count (1..4) matrices of
- * k = 1024. norm_out (optional) receives u. */
+ * k = 1024, each with a multiple of 8 rows. norm_out (optional) receives u. */
 int es_q4_rmsnorm_matvec_multi(const es_q4* w, int count, const uint16_t* x, const uint16_t* gain,
                                uint16_t* norm_out, uint16_t* const* y, void* stream);
 

@@ -84,6 +84,20 @@ def test_rmsnorm_multi_gdn_projections():
         assert_bits_equal(o.numpy(np.uint16), O.q4_matvec(c, s, b, u), what=f"multi n={n}")
 
 
+def test_rmsnorm_multi_rejects_row_count_not_multiple_of_8():
+    """A wave's 8 rows must lie in one matrix, so every row count is a multiple of 8."""
+    r = rng(13)
+    mats = [random_q4(r, n, 1024) for n in (16, 12)]
+    dev = [E.DeviceQ4(*m) for m in mats]
+    arr = (E.Q4 * 2)(*[d.struct for d in dev])
+    outs = [E.DeviceBuffer(n * 2) for n in (16, 12)]
+    ptrs = (E.c_void_p * 2)(*[o.ptr for o in outs])
+    dx = E.DeviceBuffer.from_numpy(bf16(r.normal(0, 1, 1024)))
+    dg = E.DeviceBuffer.from_numpy(bf16(np.ones(1024)))
+    rc = E.lib().es_q4_rmsnorm_matvec_multi(arr, 2, dx.ptr, dg.ptr, None, ptrs, None)
+    assert rc == E.ES_ERR_INVALID
+
+
 def test_gdn_in_proj_ring_slot():
     r = rng(12)
     x = bf16(r.normal(0, 1, 1024))
