@@ -287,15 +287,22 @@ hipError_t Engine::enqueue_step(hipStream_t s, int splits, bool with_head) {
   return launch_advance(st_, prompt_, s);
 }
 
-hipGraphExec_t Engine::graph(int kind, int splits, std::string* err) {
+// A graph holds `steps` consecutive steps of one kind. Every step reads its
+// position and token from the device-side step state and advances it, so the
+// same graph serves any starting position. Within one graph the steps follow
+// each other as ordinary kernel boundaries; between graph launches the runtime
+// adds a gap of about 9 us and the first kernel starts with cold caches.
+hipGraphExec_t Engine::graph(int kind, int splits, int steps, std::string* err) {
   for (auto& g : graphs_)
-    if (g.kind == kind && g.splits == splits) return g.exec;
-  GraphEntry ge{kind, splits, nullptr, nullptr};
+    if (g.kind == kind && g.splits == splits && g.steps == steps) return g.exec;
+  GraphEntry ge{kind, splits, steps, nullptr, nullptr};
   if (hipStreamBeginCapture(stream_, hipStreamCaptureModeThreadLocal) != hipSuccess) {
     if (err) *err = "hipStreamBeginCapture failed";
     return nullptr;
   }
-  const hipError_t qe = enqueue_step(stream_, splits, kind == kKindDecode);
+  hipError_t qe = hipSuccess;
+  for (int i = 0; i < steps && qe == hipSuccess; ++i)
+    qe = enqueue_step(stream_, splits, kind == kKindDecode);
   const hipError_t ce = hipStreamEndCapture(stream_, &ge.g);
   if (qe != hipSuccess || ce != hipSuccess) {
     if (err) *err = std::string("graph capture failed: ") + hipGetErrorString(qe != hipSuccess ? qe : ce);
@@ -318,9 +325,25 @@ int Engine::upload_state(int pos, int step, uint32_t token, std::string* err) {
   return 0;
 }
 
+int Engine::launch_steps(int kind, int first_pos, int n, std::string* err) {
+  int done = 0;
+  while (done < n) {
+    const int pos = first_pos + done;
+    const int splits = splits_for(pos + 1);
+    int steps = 1;
+    if (n - done >= kGraphSteps && splits_for(pos + kGraphSteps) == splits) steps = kGraphSteps;
+    hipGraphExec_t ex = graph(kind, splits, steps, err);
+    if (!ex) return 2;
+    ES_HIP(hipGraphLaunch(ex, stream_), "hipGraphLaunch");
+    done += steps;
+  }
+  return 0;
+}
+
 // Launch `count` steps of one kind starting at absolute position first_pos.
 // At most kAhead steps are in flight between cancellation checks
-// (model.rs:127-139 keeps 16 outstanding).
+// (model.rs:127-139 keeps 16 outstanding). Forced tokens and per-step logits
+// need host work between steps, so those runs launch one graph per step.
 int Engine::run_steps(int kind, int first_pos, int count, const uint32_t* forced_dev,
                       uint16_t* logits_out, std::string* err) {
   constexpr int kAhead = 16;
@@ -332,9 +355,15 @@ int Engine::run_steps(int kind, int first_pos, int count, const uint32_t* forced
       return 3;
     }
     const int batch = std::min(kAhead, count - launched);
+    if (!forced_dev && !logits_out) {
+      if (int rc = launch_steps(kind, first_pos + launched, batch, err)) return rc;
+      launched += batch;
+      ES_HIP(hipStreamSynchronize(stream_), "step sync");
+      continue;
+    }
     for (int i = 0; i < batch; ++i) {
       const int pos = first_pos + launched + i;
-      hipGraphExec_t ex = graph(kind, splits_for(pos + 1), err);
+      hipGraphExec_t ex = graph(kind, splits_for(pos + 1), 1, err);
       if (!ex) return 2;
       if (forced_dev) {
         ES_HIP(launch_set_token(st_, forced_dev + launched + i, stream_), "set token");
@@ -554,23 +583,17 @@ int Engine::time_decode(int steps, int warmup, double* ms_total, std::string* er
     return 1;
   }
   if (int rc = upload_state(position_, 0, pending_, err)) return rc;
-  for (int i = 0; i < warmup; ++i) {
-    hipGraphExec_t ex = graph(kKindDecode, splits_for(position_ + i + 1), err);
-    if (!ex) return 2;
-    ES_HIP(hipGraphLaunch(ex, stream_), "launch");
-  }
-  // capture every graph the timed steps need before the clock starts
-  for (int i = 0; i < steps; ++i)
-    if (!graph(kKindDecode, splits_for(position_ + warmup + i + 1), err)) return 2;
+  // capture the graphs before the clock starts (the warmup uses the same ones)
+  if (!graph(kKindDecode, splits_for(position_ + 1), 1, err)) return 2;
+  if (steps >= kGraphSteps && !graph(kKindDecode, splits_for(position_ + 1), kGraphSteps, err))
+    return 2;
+  if (int rc = launch_steps(kKindDecode, position_, warmup, err)) return rc;
   ES_HIP(hipStreamSynchronize(stream_), "warmup sync");
   hipEvent_t e0, e1;
   ES_HIP(hipEventCreate(&e0), "event");
   ES_HIP(hipEventCreate(&e1), "event");
   ES_HIP(hipEventRecord(e0, stream_), "record");
-  for (int i = 0; i < steps; ++i) {
-    hipGraphExec_t ex = graph(kKindDecode, splits_for(position_ + warmup + i + 1), err);
-    ES_HIP(hipGraphLaunch(ex, stream_), "launch");
-  }
+  if (int rc = launch_steps(kKindDecode, position_ + warmup, steps, err)) return rc;
   ES_HIP(hipEventRecord(e1, stream_), "record");
   ES_HIP(hipEventSynchronize(e1), "event sync");
   float ms = 0.0f;

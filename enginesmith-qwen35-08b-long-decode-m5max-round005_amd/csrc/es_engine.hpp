@@ -86,7 +86,11 @@ class Engine {
   void reset_state();
   hipError_t enqueue_layers(hipStream_t s, int splits);
   hipError_t enqueue_step(hipStream_t s, int splits, bool with_head);
-  hipGraphExec_t graph(int kind, int splits, std::string* err);
+  hipGraphExec_t graph(int kind, int splits, int steps, std::string* err);
+  // Enqueue `n` steps of one kind from absolute position first_pos: whole
+  // kGraphSteps-step graphs, then single-step graphs for the rest.
+  int launch_steps(int kind, int first_pos, int n, std::string* err);
+  static constexpr int kGraphSteps = 16;
   int run_steps(int kind, int first_pos, int count, const uint32_t* forced_dev,
                 uint16_t* logits_out, std::string* err);
   int upload_state(int pos, int step, uint32_t token, std::string* err);
@@ -125,6 +129,7 @@ class Engine {
   struct GraphEntry {
     int kind;
     int splits;
+    int steps;
     hipGraph_t g;
     hipGraphExec_t exec;
   };

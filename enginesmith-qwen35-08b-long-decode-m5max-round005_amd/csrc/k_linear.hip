@@ -43,8 +43,10 @@ __device__ __forceinline__ void norm_slice_1024(const float* xv, const Raw64& ga
   for (int j = 0; j < 32; ++j) xn[j] = rbf(rbf(xv[j] * inv) * gv[j]);
 }
 
-// Dequantised embedding slice (embedding_q4, linear.metal:20-23).
-__device__ __forceinline__ void embed_slice(const Q4& e, uint32_t tok, int sl, float* xv) {
+// Dequantised embedding slice (embedding_q4, linear.metal:20-23). The table
+// is taken by value: a reference into the kernel-argument struct made the
+// compiler copy the whole struct (272 B) to per-thread scratch memory.
+__device__ __forceinline__ void embed_slice(Q4 e, uint32_t tok, int sl, float* xv) {
   if (tok >= (uint32_t)e.n) tok = 0;  // ids come from validated prompts or the head's argmax
   const u32x4 c = *reinterpret_cast<const u32x4*>(e.w + (size_t)tok * 128 + sl * 4);
   const float sc = bf2f(e.s[(size_t)tok * 16 + sl / 2]);

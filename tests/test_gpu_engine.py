@@ -90,6 +90,28 @@ def test_continuation_equals_monolithic(small):
     assert parts == whole
 
 
+def test_graph_batches_equal_one_step_launches(small):
+    """Steps replayed 16 to a graph (prompt and decode) leave the same tokens,
+    GDN state and KV rows as the same steps launched one graph per step
+    (forced decode of the generated stream)."""
+    eng, _, _ = small
+    r = rng(46)
+    prompt = r.integers(0, SMALL["vocab"], 40).tolist()  # 39 prompt steps: 2 batches of 16 + 7
+    gen = eng.generate(prompt, 37, reset=True)           # 2 batches of 16 + 5
+    end = eng.position
+    ring_a, state_a = eng.read_gdn(0)
+    kv_a = eng.read_kv(3, 0, end - 40, 40)
+    first = eng.generate(prompt, 1, reset=True)
+    assert first[0] == gen[0]
+    am = eng.forced_decode(gen[:-1])
+    assert am.tolist() == gen[1:]
+    assert eng.position == end
+    ring_b, state_b = eng.read_gdn(0)
+    assert np.array_equal(ring_a, ring_b)
+    assert np.array_equal(state_a.view(np.uint32), state_b.view(np.uint32))
+    assert np.array_equal(eng.read_kv(3, 0, end - 40, 40), kv_a)
+
+
 def test_reset_isolation(small):
     eng, _, _ = small
     r = rng(44)
