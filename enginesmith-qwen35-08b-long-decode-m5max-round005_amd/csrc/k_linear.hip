@@ -90,21 +90,13 @@ __global__ __launch_bounds__(256) void k_norm_multi(MultiDev a) {
     }
   }
   const Q4 q = m == 0 ? a.m[0] : m == 1 ? a.m[1] : m == 2 ? a.m[2] : a.m[3];
-  // Weight loads first: they do not depend on the input, so their latency
-  // overlaps the input load and the normalisation below. They are
-  // non-temporal: the input projections (94 MB per step) are left out of the
-  // on-package cache so that the other layer weights (about 200 MB) stay in it
-  // from one step to the next.
-  u32x4 c[P];
-  uint32_t sv[P], bv[P];
-#pragma unroll
-  for (int p = 0; p < P; ++p) {
-    const int local = local0 + 2 * p + half;
-    c[p] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(q.w + (size_t)local * 128 + sl * 4));
-    sv[p] = __builtin_nontemporal_load(q.s + (size_t)local * 16 + sl / 2);
-    bv[p] = __builtin_nontemporal_load(q.b + (size_t)local * 16 + sl / 2);
-  }
-
+  // Input, gain and position loads first, then the weights. Loads complete
+  // in issue order, so the normalisation (which needs only the input) runs
+  // while the weights are still arriving; issued the other way round it
+  // would wait for every weight load. The weights are non-temporal: the
+  // input projections (94 MB per step) are left out of the on-package cache
+  // so that the other layer weights (about 200 MB) stay in it from one step
+  // to the next.
   __shared__ float norm_lds[kNormLds];
   const Raw64 graw = EMBED ? load_raw64(a.gain + sl * 32) : Raw64{};
   const uint2 x4 = EMBED ? uint2{0u, 0u} : reinterpret_cast<const uint2*>(a.x)[threadIdx.x];
@@ -114,14 +106,24 @@ __global__ __launch_bounds__(256) void k_norm_multi(MultiDev a) {
   asm volatile("v_mov_b32 %0, 0" : "=v"(zero));
   const int* pos_src = a.st ? &a.st->pos : reinterpret_cast<const int*>(a.gain);
   const int pos_raw = pos_src[zero];
+  const Raw64 xraw = EMBED ? Raw64{} : load_raw64(a.x + sl * 32);
+  issue_fence();
+  u32x4 c[P];
+  uint32_t sv[P], bv[P];
+#pragma unroll
+  for (int p = 0; p < P; ++p) {
+    const int local = local0 + 2 * p + half;
+    c[p] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(q.w + (size_t)local * 128 + sl * 4));
+    sv[p] = __builtin_nontemporal_load(q.s + (size_t)local * 16 + sl / 2);
+    bv[p] = __builtin_nontemporal_load(q.b + (size_t)local * 16 + sl / 2);
+  }
+  issue_fence();
   float xv[32];
   if (EMBED) {
     const uint32_t tok = a.st ? a.st->token : a.token_val;
     embed_slice(a.embed, tok, sl, xv);
     if (a.h_out && blockIdx.x == 0 && threadIdx.x < 32) store_bf16x32(a.h_out + sl * 32, xv);
   } else {
-    const Raw64 xraw = load_raw64(a.x + sl * 32);
-    issue_fence();
     unpack_bf16x32(xraw, xv);
   }
   float xn[32];
@@ -149,6 +151,13 @@ __global__ __launch_bounds__(256) void k_norm_gate_up(Q4 gate, Q4 up, const uint
                                                       uint16_t* act) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, half = lane >> 5, sl = lane & 31;
   const int base = (blockIdx.x * 4 + wave) * (2 * NP);
+  // Input and gain first, then the weights (loads complete in issue order:
+  // the normalisation runs while the weights arrive).
+  __shared__ float norm_lds[kNormLds];
+  const Raw64 xraw = load_raw64(x + sl * 32);
+  const uint2 x4 = reinterpret_cast<const uint2*>(x)[threadIdx.x];
+  const uint2 g4 = reinterpret_cast<const uint2*>(gain)[threadIdx.x];
+  issue_fence();
   u32x4 cg[NP], cu[NP];
   uint32_t sg[NP], bg[NP], su[NP], bu[NP];
   int rr[NP];
@@ -164,10 +173,6 @@ __global__ __launch_bounds__(256) void k_norm_gate_up(Q4 gate, Q4 up, const uint
     su[p] = up.s[(size_t)rl * 16 + sl / 2];
     bu[p] = up.b[(size_t)rl * 16 + sl / 2];
   }
-  __shared__ float norm_lds[kNormLds];
-  const Raw64 xraw = load_raw64(x + sl * 32);
-  const uint2 x4 = reinterpret_cast<const uint2*>(x)[threadIdx.x];
-  const uint2 g4 = reinterpret_cast<const uint2*>(gain)[threadIdx.x];
   issue_fence();
   float xv[32];
   unpack_bf16x32(xraw, xv);
@@ -213,6 +218,15 @@ __global__ __launch_bounds__(256) void k_norm_gate_up_parts(Q4 gate, Q4 up, cons
   const int t = threadIdx.x;
   const int lane = t & 63, wave = t >> 6, half = lane >> 5, sl = lane & 31;
   const int base = (blockIdx.x * 4 + wave) * (2 * NP);
+  // The residual, gain and partials first, then the weights (loads complete
+  // in issue order: the partial sum and the normalisation run while the
+  // weights arrive).
+  const uint2 ho = reinterpret_cast<const uint2*>(h_old)[t];
+  const uint2 g4 = reinterpret_cast<const uint2*>(gain)[t];
+  float4 pv[NPART];
+#pragma unroll
+  for (int k = 0; k < NPART; ++k) pv[k] = reinterpret_cast<const float4*>(part + k * kHidden)[t];
+  issue_fence();
   u32x4 cg[NP], cu[NP];
   uint32_t sg[NP], bg[NP], su[NP], bu[NP];
   int rr[NP];
@@ -228,11 +242,6 @@ __global__ __launch_bounds__(256) void k_norm_gate_up_parts(Q4 gate, Q4 up, cons
     su[p] = up.s[(size_t)rl * 16 + sl / 2];
     bu[p] = up.b[(size_t)rl * 16 + sl / 2];
   }
-  const uint2 ho = reinterpret_cast<const uint2*>(h_old)[t];
-  const uint2 g4 = reinterpret_cast<const uint2*>(gain)[t];
-  float4 pv[NPART];
-#pragma unroll
-  for (int k = 0; k < NPART; ++k) pv[k] = reinterpret_cast<const float4*>(part + k * kHidden)[t];
   issue_fence();
   float hn[4];
   {
@@ -331,6 +340,11 @@ __global__ __launch_bounds__(256) void k_qmv_wide(Q4 m, const uint16_t* x,
   const int wpr = m.k >> 3, gpr = m.k >> 6;
   const int s1 = v1 ? lane : 0, s2 = v2 ? lane + 64 : 0;
   const int base = (blockIdx.x * 4 + wave) * P;
+  // Input first, then the weights (loads complete in issue order: the
+  // input's slice sums and scaling run while the weights arrive).
+  const Raw64 xa = load_raw64(x + s1 * 32);
+  const Raw64 xb = load_raw64(x + s2 * 32);
+  issue_fence();
   u32x4 c1[P], c2[P];
   uint32_t sa[P], ba[P], sb[P], bb[P];
 #pragma unroll
@@ -351,8 +365,6 @@ __global__ __launch_bounds__(256) void k_qmv_wide(Q4 m, const uint16_t* x,
     const int r = base + p;
     res[p] = ADD ? residual[r < m.n ? r : 0] : 0u;
   }
-  const Raw64 xa = load_raw64(x + s1 * 32);
-  const Raw64 xb = load_raw64(x + s2 * 32);
   issue_fence();
   float xv[32], xr1[32], xr2[32];
   float xs1 = 0.0f, xs2 = 0.0f;
