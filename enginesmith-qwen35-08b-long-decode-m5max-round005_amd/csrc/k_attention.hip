@@ -479,15 +479,20 @@ __device__ __forceinline__ float tree_reg32(float* v) {
 // Chain factors of head h for the merge, by one 64-lane wave: fac[l] =
 // exp(max_l - max) and *total = the weighted sum of the chain sums
 // (attention_decode.metal:858-862 for the long route).
-__device__ __forceinline__ void merge_factors(const AttnArgs& a, int h, int lane, bool two_pass,
-                                              float* fac, float* total) {
+// The (max, sum) pair of chain `lane` (lane & 31 on the short route).
+__device__ __forceinline__ float2 load_chain_ml(const AttnArgs& a, int h, int lane, bool two_pass) {
   const float* ml = a.part_ml + (size_t)h * kAttnMaxChains * 2;
+  return reinterpret_cast<const float2*>(ml)[two_pass ? lane : (lane & 31)];
+}
+
+__device__ __forceinline__ void merge_factors(float2 mlv, int lane, bool two_pass, float* fac,
+                                              float* total) {
   if (two_pass) {
-    const float mx = ml[2 * lane];
+    const float mx = mlv.x;
     const float F = es_exp(mx - wave_max(mx));
     fac[lane] = F;
     // lane l < 32: (0 + F_l s_l) + F_{l+32} s_{l+32}, then pairwise over lanes
-    const float prod = F * ml[2 * lane + 1];
+    const float prod = F * mlv.y;
     const float hi = __shfl_down(prod, 32, 64);
     float s = 0.0f;
     s = s + prod;
@@ -495,10 +500,10 @@ __device__ __forceinline__ void merge_factors(const AttnArgs& a, int h, int lane
     s = tree32(s);
     if (lane == 0) *total = s;
   } else {
-    const float mx = lane < 32 ? ml[2 * lane] : kFiniteMin;
+    const float mx = lane < 32 ? mlv.x : kFiniteMin;
     const float F = es_exp(mx - wave_max(mx));
     if (lane < 32) fac[lane] = F;
-    const float s = tree32(ml[2 * (lane & 31) + 1] * F);
+    const float s = tree32(mlv.y * F);
     if (lane == 0) *total = s;
   }
 }
@@ -506,8 +511,9 @@ __device__ __forceinline__ void merge_factors(const AttnArgs& a, int h, int lane
 // Merged, normalised and gated value of dim d of head h: bf16(bf16(o) *
 // sigmoid_bf(gate)) with o = (sum of factor-weighted chain outputs) / total;
 // v holds the 64 chain outputs of the dim (loaded by the caller).
-__device__ __forceinline__ uint32_t merge_dim(const AttnArgs& a, int h, int d, bool two_pass,
-                                              const float* fac, float sum, float* v) {
+// gate_raw: bf16 gate of the dim (q_proj[h*512 + 256 + d]).
+__device__ __forceinline__ uint32_t merge_dim(uint32_t gate_raw, bool two_pass, const float* fac,
+                                              float sum, float* v) {
   float o;
   if (two_pass) {
     float w[32];
@@ -526,7 +532,7 @@ __device__ __forceinline__ uint32_t merge_dim(const AttnArgs& a, int h, int d, b
   }
   o = sum == 0.0f ? o : o / sum;
   const float attention = rbf(o);
-  const float gate = sigmoid_bf(bf2f(a.q_proj[h * 512 + 256 + d]));
+  const float gate = sigmoid_bf(bf2f(gate_raw));
   return f2bf(attention * gate);
 }
 
@@ -548,12 +554,16 @@ __global__ __launch_bounds__(64) void k_attn_merge(AttnArgs a) {
   const int d = blockIdx.y * 64 + lane;
   const int pos = load_pos(a.st, a.pos_val);
   const bool two_pass = pos + 1 >= kAttnRouteSplit;
+  // (max, sum) pairs, chain outputs and the gate in flight together; the
+  // factors form as soon as the first arrive.
+  const float2 mlv = load_chain_ml(a, h, lane, two_pass);
   float v[kAttnMaxChains];
-  // Chain outputs first: independent loads in flight while the factors form.
   load_chain_outputs(a, h, d, two_pass, v);
-  merge_factors(a, h, lane, two_pass, fac, &total);
+  const uint32_t gate_raw = a.q_proj[h * 512 + 256 + d];
+  issue_fence();
+  merge_factors(mlv, lane, two_pass, fac, &total);
   __syncthreads();
-  a.gated[h * 256 + d] = (uint16_t)merge_dim(a, h, d, two_pass, fac, total, v);
+  a.gated[h * 256 + d] = (uint16_t)merge_dim(gate_raw, two_pass, fac, total, v);
 }
 
 // Engine path: merge + gate of head h (every one of the 8 blocks of the head
@@ -569,6 +579,16 @@ __global__ __launch_bounds__(256) void k_attn_merge_out(AttnArgs a, Q4 o, float*
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
   const int h = blockIdx.x, rg = blockIdx.y;  // a head's blocks share an XCD
   const int sl = t & 7, gs = 8 * h + sl;  // K slice of this lane
+  const int pos = load_pos(a.st, a.pos_val);
+  const bool two_pass = pos + 1 >= kAttnRouteSplit;
+  // Loads in the order they are needed (they complete in issue order): the
+  // (max, sum) pairs, the chain outputs and the gate, then the o_proj slice.
+  float2 mlv = make_float2(0.0f, 0.0f);
+  if (wave == 0) mlv = load_chain_ml(a, h, lane, two_pass);
+  float v[kAttnMaxChains];
+  load_chain_outputs(a, h, t, two_pass, v);
+  const uint32_t gate_raw = a.q_proj[h * 512 + 256 + t];
+  issue_fence();
   u32x4 oc[4];
   uint32_t osv[4], obv[4];
 #pragma unroll
@@ -578,13 +598,10 @@ __global__ __launch_bounds__(256) void k_attn_merge_out(AttnArgs a, Q4 o, float*
     osv[p] = o.s[row * 32 + gs / 2];
     obv[p] = o.b[row * 32 + gs / 2];
   }
-  const int pos = load_pos(a.st, a.pos_val);
-  const bool two_pass = pos + 1 >= kAttnRouteSplit;
-  float v[kAttnMaxChains];
-  load_chain_outputs(a, h, t, two_pass, v);
-  if (wave == 0) merge_factors(a, h, lane, two_pass, fac, &total);
+  issue_fence();
+  if (wave == 0) merge_factors(mlv, lane, two_pass, fac, &total);
   __syncthreads();
-  gx[t + (t >> 5)] = bf2f(merge_dim(a, h, t, two_pass, fac, total, v));
+  gx[t + (t >> 5)] = bf2f(merge_dim(gate_raw, two_pass, fac, total, v));
   __syncthreads();
   float xv[32], xr[32];
 #pragma unroll

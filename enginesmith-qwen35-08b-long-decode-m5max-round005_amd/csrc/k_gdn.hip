@@ -163,7 +163,23 @@ __global__ __launch_bounds__(512) void k_gdn_recur_out(GdnOutArgs a) {
   const int h = blockIdx.x, rg = blockIdx.y;
   const int j = t & 15;
 
-  // ---- loads first (state of 4 rows per thread, out_proj slice, conv taps, z)
+  // ---- loads, in the order they are needed (loads complete in issue
+  // order): conv taps and gate inputs for the prologue, then the state of 4
+  // rows per thread, z and the norm weight, then the out_proj slice
+  const int pos = load_pos(r.st, r.pos_val);
+  // conv channels: q (t < 128), k (t < 256), v (t < 384)
+  const int c = t < 128 ? h * 128 + t : t < 256 ? 2048 + h * 128 + (t - 128) : 4096 + h * 128 + (t - 256);
+  RingTaps rt;
+  if (t < 384) ring_load(r.ring, r.conv_w, c, rt);
+  uint32_t ga = 0u, gd = 0u, gb = 0u;
+  float gl = 0.0f;
+  if (t == 384) {
+    ga = r.ab[h];
+    gd = r.dt_bias[h];
+    gl = r.a_log[h];
+    gb = r.ab[16 + h];
+  }
+  issue_fence();
   float S[4][8];
 #pragma unroll
   for (int p = 0; p < 4; ++p) {
@@ -173,21 +189,17 @@ __global__ __launch_bounds__(512) void k_gdn_recur_out(GdnOutArgs a) {
     S[p][0] = lo.x; S[p][1] = lo.y; S[p][2] = lo.z; S[p][3] = lo.w;
     S[p][4] = hi.x; S[p][5] = hi.y; S[p][6] = hi.z; S[p][7] = hi.w;
   }
-  const int orow = rg * 128 + (t >> 2), osl = 4 * h + (t & 3);  // output row, K slice
-  const u32x4 oc = *reinterpret_cast<const u32x4*>(a.out.w + (size_t)orow * 256 + osl * 4);
-  const uint32_t osv = a.out.s[(size_t)orow * 32 + osl / 2];
-  const uint32_t obv = a.out.b[(size_t)orow * 32 + osl / 2];
-  // conv channels: q (t < 128), k (t < 256), v (t < 384)
-  const int c = t < 128 ? h * 128 + t : t < 256 ? 2048 + h * 128 + (t - 128) : 4096 + h * 128 + (t - 256);
-  RingTaps rt;
-  if (t < 384) ring_load(r.ring, r.conv_w, c, rt);
   // gated norm inputs: element t (t < 128) of z and of the norm weight
   uint32_t zb = 0u, wb = 0u;
   if (t < 128) {
     zb = a.z[h * 128 + t];
     wb = a.norm_w[t];
   }
-  const int pos = load_pos(r.st, r.pos_val);
+  const int orow = rg * 128 + (t >> 2), osl = 4 * h + (t & 3);  // output row, K slice
+  const u32x4 oc = *reinterpret_cast<const u32x4*>(a.out.w + (size_t)orow * 256 + osl * 4);
+  const uint32_t osv = a.out.s[(size_t)orow * 32 + osl / 2];
+  const uint32_t obv = a.out.b[(size_t)orow * 32 + osl / 2];
+  issue_fence();
 
   // ---- conv + SiLU, q/k L2 norm, gates (as k_gdn_recur)
   float v = 0.0f;
@@ -198,9 +210,9 @@ __global__ __launch_bounds__(512) void k_gdn_recur_out(GdnOutArgs a) {
   } else if (t < 384) {
     vv[t - 256] = v;
   } else if (t == 384) {
-    const float ax = rbf(bf2f(r.ab[h]) + bf2f(r.dt_bias[h]));
-    gates[0] = es_exp(-es_exp(r.a_log[h]) * softplus_bf(ax));
-    gates[1] = sigmoid_bf(bf2f(r.ab[16 + h]));
+    const float ax = rbf(bf2f(ga) + bf2f(gd));
+    gates[0] = es_exp(-es_exp(gl) * softplus_bf(ax));
+    gates[1] = sigmoid_bf(bf2f(gb));
   }
   __syncthreads();
   if (t < 256) {
