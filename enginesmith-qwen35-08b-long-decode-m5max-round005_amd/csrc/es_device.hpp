@@ -147,6 +147,21 @@ __device__ __forceinline__ float dpp_half_mirror(float v) {
 __device__ __forceinline__ float dpp_mirror(float v) {
   return __builtin_amdgcn_update_dpp(0.0f, v, 0x140, 0xf, 0xf, false);
 }
+// Exchanges between 16-lane rows by the gfx950 row-swap instructions
+// (v_permlane16_swap_b32, v_permlane32_swap_b32: VALU operations, where a
+// shuffle goes through the LDS crossbar). Swapping a value with a copy of
+// itself leaves in every lane the row-ordered pair (v[l & ~16], v[l | 16])
+// (resp. (v[l & ~32], v[l | 32])); its sum or max equals v + v[l ^ 16]
+// (v + v[l ^ 32]) bit for bit, since addition and max are commutative.
+// Callers run them with the whole wave active.
+__device__ __forceinline__ float2 rows_xor16(float v) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return make_float2(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float2 rows_xor32(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return make_float2(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
 __device__ __forceinline__ float tree4(float v) {
   v = v + dpp_xor1(v);
   v = v + dpp_xor2(v);
@@ -160,13 +175,13 @@ __device__ __forceinline__ float tree16(float v) {
 }
 __device__ __forceinline__ float tree32(float v) {
   v = tree16(v);
-  v = v + __shfl_xor(v, 16, 64);
-  return v;
+  const float2 p = rows_xor16(v);
+  return p.x + p.y;
 }
 __device__ __forceinline__ float tree64(float v) {
   v = tree32(v);
-  v = v + __shfl_xor(v, 32, 64);
-  return v;
+  const float2 p = rows_xor32(v);
+  return p.x + p.y;
 }
 __device__ __forceinline__ float row16_max(float v) {
   v = fmaxf(v, dpp_xor1(v));
@@ -175,10 +190,15 @@ __device__ __forceinline__ float row16_max(float v) {
   v = fmaxf(v, dpp_mirror(v));
   return v;
 }
+// Each lane keeps its own value as the first operand of the max (as with a
+// shuffle), so a +0/-0 tie resolves exactly as it did lane by lane.
 __device__ __forceinline__ float wave_max(float v) {
   v = row16_max(v);
-  v = fmaxf(v, __shfl_xor(v, 16, 64));
-  v = fmaxf(v, __shfl_xor(v, 32, 64));
+  const int lane = threadIdx.x & 63;
+  float2 p = rows_xor16(v);
+  v = (lane & 16) ? fmaxf(p.y, p.x) : fmaxf(p.x, p.y);
+  p = rows_xor32(v);
+  v = (lane & 32) ? fmaxf(p.y, p.x) : fmaxf(p.x, p.y);
   return v;
 }
 

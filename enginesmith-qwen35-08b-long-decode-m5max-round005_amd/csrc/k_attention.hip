@@ -493,7 +493,7 @@ __device__ __forceinline__ void merge_factors(float2 mlv, int lane, bool two_pas
     fac[lane] = F;
     // lane l < 32: (0 + F_l s_l) + F_{l+32} s_{l+32}, then pairwise over lanes
     const float prod = F * mlv.y;
-    const float hi = __shfl_down(prod, 32, 64);
+    const float hi = rows_xor32(prod).y;  // lane l < 32: prod of lane l + 32
     float s = 0.0f;
     s = s + prod;
     s = s + hi;
