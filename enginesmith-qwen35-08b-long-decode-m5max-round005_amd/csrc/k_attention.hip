@@ -50,16 +50,22 @@ __device__ __forceinline__ void head_norm4(const uint2 xv, const uint2 gv, float
 }
 
 // Rotary component d of a normalised head (attention.metal:55-70):
-// d < 32: fma(lo, c, -(hi*s)); 32 <= d < 64: fma(lo, s, hi*c).
-// inv is inv_freq[d & 31] (read by the caller, only used for d < 64).
-__device__ __forceinline__ float rope_at(const float* nrm, int d, int pos, float inv) {
-  if (d >= 64) return nrm[d];
-  const int pair = d & 31;
+// d < 32: fma(lo, c, -(hi*s)); 32 <= d < 64: fma(lo, s, hi*c), where lo and
+// hi are dims d & 31 and (d & 31) + 32. own is dim d, partner dim d ^ 32;
+// inv is inv_freq[d & 31] (only used for d < 64).
+__device__ __forceinline__ float rope_at(float own, float partner, int d, int pos, float inv) {
+  if (d >= 64) return own;
   const float angle = (float)pos * inv;
   float s, c;
   es_sincos(angle, &s, &c);
-  const float lo = nrm[pair], hi = nrm[pair + 32];
+  const float lo = d < 32 ? own : partner, hi = d < 32 ? partner : own;
   return rbf(d < 32 ? fmaf(lo, c, -(hi * s)) : fmaf(lo, s, hi * c));
+}
+
+// Value of lane l ^ 8 inside each 16-lane row (DPP row rotate by 8). With 4
+// dims per lane, dim d ^ 32 of a head (d < 64) sits in lane ^ 8.
+__device__ __forceinline__ float dpp_row_ror8(float v) {
+  return __builtin_amdgcn_update_dpp(0.0f, v, 0x128, 0xf, 0xf, false);
 }
 
 __device__ __forceinline__ float tree8(float v) {
@@ -114,7 +120,6 @@ struct __attribute__((aligned(16))) FusedSmem {
   float e[2][2][kTile];             // exp scores
   float f[2][2][kTile];             // factors
   int slow[2][2];                   // some factor of the tile differs from 1
-  float nrm[3][256];                // prologue: normalised q of both heads, new k
   float qs[2][256];                 // roped q x 1/16 of both heads
   u32x4 knew[32];                   // new K row (roped, bf16)
   u32x4 vnew[32];                   // new V row
@@ -361,7 +366,10 @@ __global__ __launch_bounds__(kFusedThreads, 1) void k_attn_fused(AttnArgs a) {
   } else if (wave == 9) {
     if (nt > 0) issue_rows(sm.v, vrow0, C, L, 0, lane);
   } else if (wave < 4) {
+    // One barrier: RoPE takes the partner dims (d ^ 32, in lane ^ 8) by DPP,
+    // so q and the new K row go to LDS straight after the norm.
     uint2 xv, gv;
+    float inv[4] = {0.0f, 0.0f, 0.0f, 0.0f};
     if (wave < 2) {
       xv = *reinterpret_cast<const uint2*>(a.q_proj + (h0 + wave) * 512 + lane * 4);
       gv = *reinterpret_cast<const uint2*>(a.q_gain + lane * 4);
@@ -370,36 +378,34 @@ __global__ __launch_bounds__(kFusedThreads, 1) void k_attn_fused(AttnArgs a) {
       gv = *reinterpret_cast<const uint2*>(a.k_gain + lane * 4);
     }
     if (wave < 3) {
-      float o4[4];
+#pragma unroll
+      for (int x = 0; x < 4; ++x) inv[x] = a.inv_freq[((lane * 4) & 31) + x];
+    }
+    issue_fence();
+    if (wave < 3) {
+      float o4[4], p4[4], r[4];
       head_norm4(xv, gv, o4);
 #pragma unroll
-      for (int x = 0; x < 4; ++x) sm.nrm[wave][lane * 4 + x] = o4[x];
+      for (int x = 0; x < 4; ++x) p4[x] = dpp_row_ror8(o4[x]);
+#pragma unroll
+      for (int x = 0; x < 4; ++x) r[x] = rope_at(o4[x], p4[x], lane * 4 + x, pos, inv[x]);
+      if (wave < 2) {
+        if (a.query_out && c == 0) {
+          uint16_t* qo = a.query_out + (h0 + wave) * 256 + lane * 4;
+          *reinterpret_cast<uint2*>(qo) = make_uint2(pack_bf2(r[0], r[1]), pack_bf2(r[2], r[3]));
+        }
+#pragma unroll
+        for (int x = 0; x < 4; ++x) sm.qs[wave][lane * 4 + x] = r[x] * 0.0625f;
+      } else {
+        const uint2 kp = make_uint2(pack_bf2(r[0], r[1]), pack_bf2(r[2], r[3]));
+        reinterpret_cast<uint2*>(sm.knew)[lane] = kp;
+        if (holder && hp == 0)
+          *reinterpret_cast<uint2*>(a.kcache + ((size_t)kvh * a.capacity + pos) * 256 + lane * 4) = kp;
+      }
     } else {
       reinterpret_cast<uint2*>(sm.vnew)[lane] = xv;
       if (holder && hp == 0)
         *reinterpret_cast<uint2*>(a.vcache + ((size_t)kvh * a.capacity + pos) * 256 + lane * 4) = xv;
-    }
-  }
-  if (wave == 8 || wave == 9) lds_barrier(); else __syncthreads();
-  if (wave < 3) {
-    float inv[4];
-#pragma unroll
-    for (int x = 0; x < 4; ++x) inv[x] = a.inv_freq[((lane * 4) & 31) + x];
-    float r[4];
-#pragma unroll
-    for (int x = 0; x < 4; ++x) r[x] = rope_at(sm.nrm[wave], lane * 4 + x, pos, inv[x]);
-    if (wave < 2) {
-      if (a.query_out && c == 0) {
-        uint16_t* qo = a.query_out + (h0 + wave) * 256 + lane * 4;
-        *reinterpret_cast<uint2*>(qo) = make_uint2(pack_bf2(r[0], r[1]), pack_bf2(r[2], r[3]));
-      }
-#pragma unroll
-      for (int x = 0; x < 4; ++x) sm.qs[wave][lane * 4 + x] = r[x] * 0.0625f;
-    } else {
-      const uint2 kp = make_uint2(pack_bf2(r[0], r[1]), pack_bf2(r[2], r[3]));
-      reinterpret_cast<uint2*>(sm.knew)[lane] = kp;
-      if (holder && hp == 0)
-        *reinterpret_cast<uint2*>(a.kcache + ((size_t)kvh * a.capacity + pos) * 256 + lane * 4) = kp;
     }
   }
   if (wave == 8 || wave == 9) lds_barrier(); else __syncthreads();
