@@ -6,6 +6,7 @@
 #include <cstring>
 #include <string>
 
+#include "es_checkpoint.hpp"
 #include "es_engine.hpp"
 #include "es_kernels.hpp"
 #include "es_weights.hpp"
@@ -303,11 +304,35 @@ int es_weights_tensor_info(int n_layers, int vocab, int index, char* name, int n
   return ES_OK;
 }
 
+int es_weights_tensor_shape(int n_layers, int vocab, int index, int64_t* dims, int max_dims) {
+  if (n_layers < 1 || vocab < 1) return fail(ES_ERR_INVALID, "bad model shape");
+  const auto t = es::weight_layout({n_layers, vocab}, nullptr);
+  if (index < 0 || index >= (int)t.size()) return fail(ES_ERR_INVALID, "tensor index out of range");
+  const int nd = (int)t[index].shape.size();
+  if (!dims || max_dims < nd) return fail(ES_ERR_INVALID, "es_weights_tensor_shape: dims too short");
+  for (int i = 0; i < nd; ++i) dims[i] = t[index].shape[i];
+  return nd;
+}
+
 int es_weights_random(int n_layers, int vocab, uint64_t seed, void* blob, size_t bytes,
                       int threads) {
   if (n_layers < 1 || vocab < 1) return fail(ES_ERR_INVALID, "bad model shape");
   if (!es::weights_random({n_layers, vocab}, seed, blob, bytes, threads))
     return fail(ES_ERR_INVALID, "es_weights_random: blob too small");
+  return ES_OK;
+}
+
+int es_checkpoint_config(const char* model_dir, int* n_layers, int* vocab) {
+  if (!model_dir || !n_layers || !vocab) return fail(ES_ERR_INVALID, "es_checkpoint_config: null argument");
+  std::string err;
+  if (!es::checkpoint_config(model_dir, n_layers, vocab, &err)) return fail(ES_ERR_INVALID, err);
+  return ES_OK;
+}
+
+int es_checkpoint_load(const char* model_dir, int n_layers, int vocab, void* blob, size_t bytes) {
+  if (!model_dir || n_layers < 1 || vocab < 1) return fail(ES_ERR_INVALID, "es_checkpoint_load: bad arguments");
+  std::string err;
+  if (!es::checkpoint_load(model_dir, n_layers, vocab, blob, bytes, &err)) return fail(ES_ERR_INVALID, err);
   return ES_OK;
 }
 

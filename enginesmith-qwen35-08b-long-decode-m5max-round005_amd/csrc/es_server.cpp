@@ -4,8 +4,10 @@
 // JSON object per line, keys sorted as serde_json writes them.
 //
 // Usage: es_server --model DIR
-// DIR holds es_model.json {"seed": S, "n_layers": L, "vocab": V[, "capacity": C]}
-// describing a seeded random-init model.
+// DIR is a checkpoint directory (config.json and *.safetensors, loaded and
+// checked as Weights::load does, weights.rs:11-53), or, when it has no
+// config.json, holds es_model.json {"seed": S, "n_layers": L, "vocab": V
+// [, "capacity": C]} describing a seeded random-init model.
 #include <atomic>
 #include <condition_variable>
 #include <cstdio>
@@ -23,161 +25,13 @@
 #include <vector>
 
 #include "es_decode.h"
+#include "es_json.hpp"
 
 namespace {
 
-// ---- minimal JSON value + parser ----
-struct Json {
-  enum Kind { Null, Bool, Num, Str, Arr, Obj } kind = Null;
-  bool b = false;
-  double num = 0;
-  bool is_int = false;
-  long long i = 0;
-  bool neg = false;
-  std::string s;            // string value, or raw text of a number
-  std::vector<Json> arr;
-  std::map<std::string, Json> obj;
-  const Json* get(const std::string& k) const {
-    auto it = obj.find(k);
-    return it == obj.end() ? nullptr : &it->second;
-  }
-};
+using es::Json;
+using es::parse_json;
 
-struct Parser {
-  const char* p;
-  const char* e;
-  std::string err;
-  void ws() {
-    while (p < e && (*p == ' ' || *p == '\t' || *p == '\n' || *p == '\r')) ++p;
-  }
-  bool fail(const char* m) {
-    if (err.empty()) err = m;
-    return false;
-  }
-  bool lit(const char* w) {
-    size_t n = std::strlen(w);
-    if ((size_t)(e - p) < n || std::strncmp(p, w, n) != 0) return fail("invalid literal");
-    p += n;
-    return true;
-  }
-  bool str(std::string& out) {
-    if (p >= e || *p != '"') return fail("expected string");
-    ++p;
-    while (p < e && *p != '"') {
-      if (*p == '\\') {
-        ++p;
-        if (p >= e) return fail("bad escape");
-        char c = *p++;
-        switch (c) {
-          case '"': out += '"'; break;
-          case '\\': out += '\\'; break;
-          case '/': out += '/'; break;
-          case 'b': out += '\b'; break;
-          case 'f': out += '\f'; break;
-          case 'n': out += '\n'; break;
-          case 'r': out += '\r'; break;
-          case 't': out += '\t'; break;
-          case 'u': {
-            if (e - p < 4) return fail("bad unicode escape");
-            unsigned v = (unsigned)std::strtoul(std::string(p, p + 4).c_str(), nullptr, 16);
-            p += 4;
-            if (v < 0x80) out += (char)v;
-            else if (v < 0x800) { out += (char)(0xC0 | (v >> 6)); out += (char)(0x80 | (v & 0x3F)); }
-            else { out += (char)(0xE0 | (v >> 12)); out += (char)(0x80 | ((v >> 6) & 0x3F)); out += (char)(0x80 | (v & 0x3F)); }
-            break;
-          }
-          default: return fail("bad escape");
-        }
-      } else {
-        out += *p++;
-      }
-    }
-    if (p >= e) return fail("unterminated string");
-    ++p;
-    return true;
-  }
-  bool number(Json& v) {
-    const char* st = p;
-    if (p < e && *p == '-') ++p;
-    bool frac = false;
-    while (p < e && ((*p >= '0' && *p <= '9') || *p == '.' || *p == 'e' || *p == 'E' || *p == '+' || *p == '-')) {
-      if (*p == '.' || *p == 'e' || *p == 'E') frac = true;
-      ++p;
-    }
-    if (p == st) return fail("expected value");
-    v.kind = Json::Num;
-    v.s.assign(st, p);
-    v.num = std::strtod(v.s.c_str(), nullptr);
-    v.neg = v.s[0] == '-';
-    v.is_int = !frac;
-    if (v.is_int) v.i = std::strtoll(v.s.c_str(), nullptr, 10);
-    return true;
-  }
-  bool value(Json& v, int depth) {
-    if (depth > 64) return fail("nesting too deep");
-    ws();
-    if (p >= e) return fail("unexpected end");
-    char c = *p;
-    if (c == '{') {
-      ++p;
-      v.kind = Json::Obj;
-      ws();
-      if (p < e && *p == '}') { ++p; return true; }
-      while (true) {
-        ws();
-        std::string k;
-        if (!str(k)) return false;
-        ws();
-        if (p >= e || *p != ':') return fail("expected ':'");
-        ++p;
-        Json child;
-        if (!value(child, depth + 1)) return false;
-        v.obj[k] = std::move(child);
-        ws();
-        if (p < e && *p == ',') { ++p; continue; }
-        if (p < e && *p == '}') { ++p; return true; }
-        return fail("expected ',' or '}'");
-      }
-    }
-    if (c == '[') {
-      ++p;
-      v.kind = Json::Arr;
-      ws();
-      if (p < e && *p == ']') { ++p; return true; }
-      while (true) {
-        Json child;
-        if (!value(child, depth + 1)) return false;
-        v.arr.push_back(std::move(child));
-        ws();
-        if (p < e && *p == ',') { ++p; continue; }
-        if (p < e && *p == ']') { ++p; return true; }
-        return fail("expected ',' or ']'");
-      }
-    }
-    if (c == '"') {
-      v.kind = Json::Str;
-      return str(v.s);
-    }
-    if (c == 't') { v.kind = Json::Bool; v.b = true; return lit("true"); }
-    if (c == 'f') { v.kind = Json::Bool; v.b = false; return lit("false"); }
-    if (c == 'n') { v.kind = Json::Null; return lit("null"); }
-    return number(v);
-  }
-};
-
-bool parse_json(const std::string& text, Json& out, std::string& err) {
-  Parser ps{text.data(), text.data() + text.size(), {}};
-  if (!ps.value(out, 0)) {
-    err = ps.err;
-    return false;
-  }
-  ps.ws();
-  if (ps.p != ps.e) {
-    err = "trailing characters";
-    return false;
-  }
-  return true;
-}
 
 void write_json(std::ostream& o, const Json& v) {
   switch (v.kind) {
@@ -283,22 +137,33 @@ int main(int argc, char** argv) {
   }
   if (model_dir.empty()) return die("--model MODEL_DIR required");
   std::string text, err;
-  if (!read_file(model_dir + "/es_model.json", text))
-    return die("no es_model.json in " + model_dir + " (checkpoint loading is not supported)");
-  Json cfg;
-  if (!parse_json(text, cfg, err) || cfg.kind != Json::Obj) return die("invalid es_model.json: " + err);
-  auto num = [&](const char* k, long long def) -> long long {
-    const Json* v = cfg.get(k);
-    return v && v->kind == Json::Num ? v->i : def;
-  };
-  const int n_layers = (int)num("n_layers", 24), vocab = (int)num("vocab", 248320);
-  const int capacity = (int)num("capacity", 262144);
-  const unsigned long long seed = (unsigned long long)num("seed", 0);
-  const size_t bytes = es_weights_total_bytes(n_layers, vocab);
-  if (!bytes) return die("unsupported model configuration");
-  std::vector<uint8_t> blob(bytes);
-  if (es_weights_random(n_layers, vocab, seed, blob.data(), bytes, 0) != ES_OK)
-    return die(es_last_error());
+  int n_layers = 24, vocab = 248320, capacity = 262144;  // model.rs:8-9
+  std::vector<uint8_t> blob;
+  size_t bytes = 0;
+  if (read_file(model_dir + "/config.json", text) || !read_file(model_dir + "/es_model.json", text)) {
+    // checkpoint directory (Model::load, model.rs:38-79)
+    if (es_checkpoint_config(model_dir.c_str(), &n_layers, &vocab) != ES_OK) return die(es_last_error());
+    bytes = es_weights_total_bytes(n_layers, vocab);
+    blob.resize(bytes);
+    if (es_checkpoint_load(model_dir.c_str(), n_layers, vocab, blob.data(), bytes) != ES_OK)
+      return die(es_last_error());
+  } else {
+    Json cfg;
+    if (!parse_json(text, cfg, err) || cfg.kind != Json::Obj) return die("invalid es_model.json: " + err);
+    auto num = [&](const char* k, long long def) -> long long {
+      const Json* v = cfg.get(k);
+      return v && v->kind == Json::Num ? v->i : def;
+    };
+    n_layers = (int)num("n_layers", 24);
+    vocab = (int)num("vocab", 248320);
+    capacity = (int)num("capacity", 262144);
+    const unsigned long long seed = (unsigned long long)num("seed", 0);
+    bytes = es_weights_total_bytes(n_layers, vocab);
+    if (!bytes) return die("unsupported model configuration");
+    blob.resize(bytes);
+    if (es_weights_random(n_layers, vocab, seed, blob.data(), bytes, 0) != ES_OK)
+      return die(es_last_error());
+  }
   es_engine* engine = es_engine_create(blob.data(), bytes, n_layers, vocab, capacity);
   if (!engine) return die(es_last_error());
   std::vector<uint8_t>().swap(blob);

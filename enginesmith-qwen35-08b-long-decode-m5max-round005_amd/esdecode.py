@@ -73,6 +73,9 @@ _SIGNATURES = {
     "es_weights_tensor_info": (c_int, [c_int, c_int, c_int, c_char_p, c_int, POINTER(c_uint64), POINTER(c_uint64),
                                        POINTER(c_int)]),
     "es_weights_random": (c_int, [c_int, c_int, c_uint64, c_void_p, c_size_t, c_int]),
+    "es_weights_tensor_shape": (c_int, [c_int, c_int, c_int, POINTER(ctypes.c_int64), c_int]),
+    "es_checkpoint_config": (c_int, [c_char_p, POINTER(c_int), POINTER(c_int)]),
+    "es_checkpoint_load": (c_int, [c_char_p, c_int, c_int, c_void_p, c_size_t]),
     "es_engine_create": (c_void_p, [c_void_p, c_size_t, c_int, c_int, c_int]),
     "es_engine_destroy": (None, [c_void_p]),
     "es_engine_generate": (c_int, [c_void_p, c_void_p, c_int, c_int, c_int, c_void_p]),
@@ -224,6 +227,33 @@ def random_weights(n_layers: int, vocab: int, seed: int, threads: int = 0) -> np
     total = weights_total_bytes(n_layers, vocab)
     blob = np.empty(total, dtype=np.uint8)
     check(lib().es_weights_random(n_layers, vocab, seed, _ptr(blob), total, threads))
+    return blob
+
+
+def weights_shapes(n_layers: int, vocab: int) -> list:
+    """Checkpoint shape of every tensor, in blob order."""
+    dims = (ctypes.c_int64 * 8)()
+    out = []
+    for i in range(lib().es_weights_tensor_count(n_layers)):
+        nd = lib().es_weights_tensor_shape(n_layers, vocab, i, dims, 8)
+        if nd < 0:
+            check(nd)
+        out.append(tuple(int(dims[j]) for j in range(nd)))
+    return out
+
+
+def checkpoint_config(model_dir: str) -> tuple:
+    """(n_layers, vocab) of a checkpoint directory's config.json (Weights::load checks)."""
+    n, v = c_int(), c_int()
+    check(lib().es_checkpoint_config(os.fsencode(model_dir), ctypes.byref(n), ctypes.byref(v)))
+    return n.value, v.value
+
+
+def load_checkpoint(model_dir: str, n_layers: int, vocab: int) -> np.ndarray:
+    """Weight blob filled from the directory's *.safetensors files."""
+    total = weights_total_bytes(n_layers, vocab)
+    blob = np.empty(total, dtype=np.uint8)
+    check(lib().es_checkpoint_load(os.fsencode(model_dir), n_layers, vocab, _ptr(blob), total))
     return blob
 
 

@@ -187,9 +187,28 @@ size_t es_weights_total_bytes(int n_layers, int vocab);
 int es_weights_tensor_count(int n_layers);
 int es_weights_tensor_info(int n_layers, int vocab, int index, char* name, int name_len,
                            uint64_t* offset, uint64_t* bytes, int* dtype);
+/* Checkpoint shape of tensor `index` (model.rs:41-78; conv1d is [6144,4,1]):
+ * writes up to max_dims sizes and returns the number of dims, or a negative
+ * ES_ERR_* code. */
+int es_weights_tensor_shape(int n_layers, int vocab, int index, int64_t* dims, int max_dims);
 /* Seeded random-init model (Q4 of N(0,0.02) weights, see es_weights.hpp). */
 int es_weights_random(int n_layers, int vocab, uint64_t seed, void* blob, size_t bytes,
                       int threads);
+
+/* Checkpoint directory (Weights::load, weights.rs:11-15): config.json's
+ * text_config must have hidden_size 1024, num_hidden_layers 24 and
+ * vocab_size 248320, else ES_ERR_INVALID "unsupported model configuration".
+ * Writes the model shape (24, 248320). */
+int es_checkpoint_config(const char* model_dir, int* n_layers, int* vocab);
+/* Fills a weight blob (es_weights_total_bytes(n_layers, vocab) bytes, host
+ * memory) from every *.safetensors file of model_dir, checked as
+ * Weights::load / take / linear / done do (weights.rs:16-53, model.rs:38-79):
+ * only language_model.model.* tensors, dtypes U32/F32/BF16, byte ranges
+ * inside the file and equal to the shape's size, no duplicates, exactly the
+ * model's text tensor count (694 for 24 layers), each tensor present with the
+ * model's shape and dtype. Errors carry the reference's messages
+ * ("missing <name>", "wrong shape/dtype for <name>", ...). */
+int es_checkpoint_load(const char* model_dir, int n_layers, int vocab, void* blob, size_t bytes);
 
 /* ------------------------------------------------------------------ */
 /* Engine (Model::load / generate / cancelled, model.rs:28-180)        */

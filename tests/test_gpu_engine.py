@@ -186,3 +186,39 @@ def test_protocol_server(small, tmp_path):
         if p.poll() is None:
             p.kill()
             p.wait()
+
+
+def test_protocol_server_serves_a_checkpoint_directory(tmp_path):
+    """es_server --model DIR on a checkpoint directory (config.json + two
+    safetensors files, Weights::load's format) answers exactly as the engine
+    built from the same weights in memory."""
+    from checkpoint_files import write_checkpoint, write_config
+    d = tmp_path / "ckpt"
+    blob = E.random_weights(24, 248320, seed=21, threads=16)
+    write_checkpoint(str(d), blob, 24, 248320, files=2)
+    write_config(str(d))
+    prompt = [7, 70, 700, 7000, 70000]
+    eng = E.Engine(blob, 24, 248320, capacity=4096)
+    try:
+        expect = eng.generate(prompt, 5, reset=True)
+    finally:
+        eng.close()
+    del blob
+    p = subprocess.Popen([E.SERVER_PATH, "--model", str(d)], stdin=subprocess.PIPE, stdout=subprocess.PIPE,
+                         stderr=subprocess.PIPE, text=True)
+    try:
+        def ask(req):
+            p.stdin.write(json.dumps(req) + "\n")
+            p.stdin.flush()
+            return p.stdout.readline()
+
+        assert ask({"id": 1, "op": "hello"}) == '{"id":1,"ok":true,"protocol":1}\n'
+        assert json.loads(ask({"id": 2, "op": "generate", "prompt": prompt, "max_tokens": 5, "reset": True})) == \
+            {"id": 2, "ok": True, "tokens": expect}
+        p.stdin.close()
+        assert p.wait(timeout=60) == 0
+    finally:
+        if p.poll() is None:
+            p.kill()
+            p.wait()
+
