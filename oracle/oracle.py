@@ -297,6 +297,21 @@ class OracleModel:
             a[...] = 0
         self.position = 0
 
+    def snapshot(self):
+        """Copy of the state a later step reads back (GDN histories and states,
+        position). KV rows need no copy: a step writes its own row before it
+        attends, so rows past the restored position are rewritten before use."""
+        return ({l: a.copy() for l, a in self.history.items()}, {l: a.copy() for l, a in self.state.items()},
+                self.position)
+
+    def restore(self, snap):
+        hist, state, pos = snap
+        for l, a in hist.items():
+            self.history[l][...] = a
+        for l, a in state.items():
+            self.state[l][...] = a
+        self.position = pos
+
     def step(self, token: int, want_head: bool = True, want_logits: bool = False):
         logits = np.empty(self.vocab, dtype=np.uint16) if want_logits else None
         tok = lib().eo_model_step(ctypes.byref(self.m), ctypes.byref(self.st), int(token), self.position,

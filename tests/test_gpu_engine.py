@@ -222,3 +222,83 @@ def test_protocol_server_serves_a_checkpoint_directory(tmp_path):
             p.kill()
             p.wait()
 
+
+
+CONTROL_LENGTHS = [1, 2, 15, 16, 17, 31, 32, 33, 63, 64, 65, 1023, 1024, 1025]
+
+
+def test_control_prompts_pass_the_harness_gates():
+    """Short control prompts at the lengths where tiled and chunked kernels
+    usually break (docs/protocol.md:64-65), here around the 16-step graphs,
+    the 32-position tiles, the 64 chains and the 1024-position route switch:
+    prefixes of one random prompt, each generated from a reset and judged
+    teacher-forced against the oracle with the harness's gates. The oracle
+    walks the prompt once and branches at each length (snapshot / restore)."""
+    from judge import gates, judge_from
+    blob = E.random_weights(SMALL["n_layers"], SMALL["vocab"], seed=31)
+    eng = E.Engine(blob, SMALL["n_layers"], SMALL["vocab"], capacity=1100)
+    orc = O.OracleModel(E.tensor_views(blob, **SMALL), SMALL["n_layers"], SMALL["vocab"], capacity=1100)
+    prompt = rng(47).integers(0, SMALL["vocab"], max(CONTROL_LENGTHS)).tolist()
+    cases = []
+    try:
+        orc.reset()
+        consumed = 0  # prompt tokens the oracle has consumed
+        for n in CONTROL_LENGTHS:
+            toks = eng.generate(prompt[:n], 8, reset=True)
+            while consumed < n - 1:
+                orc.step(prompt[consumed], want_head=False)
+                consumed += 1
+            snap = orc.snapshot()
+            m = judge_from(orc, prompt[n - 1], toks)
+            orc.restore(snap)
+            print(f"prompt {n}: {len(m)} mismatches {m}", flush=True)
+            cases.append((len(toks), m))
+    finally:
+        eng.close()
+    assert gates(cases) == []
+
+
+def test_protocol_state_suite(tmp_path):
+    """The reference's protocol state checks (source/NOTES.md:157-160) through
+    the server: at prompt lengths 1, 31 and 1023, 32 tokens requested whole
+    equal 1 + 31 requested in two parts with a hello and a rejected request
+    between them (state kept across both), and an unrelated request before a
+    reset leaves no trace (reset isolation)."""
+    d = tmp_path / "model"
+    d.mkdir()
+    (d / "es_model.json").write_text(json.dumps(dict(seed=8, capacity=2048, **SMALL)))
+    p = subprocess.Popen([E.SERVER_PATH, "--model", str(d)], stdin=subprocess.PIPE, stdout=subprocess.PIPE,
+                         stderr=subprocess.PIPE, text=True)
+    r = rng(48)
+    rid = 0
+
+    def ask(op, **kw):
+        nonlocal rid
+        rid += 1
+        p.stdin.write(json.dumps(dict(id=rid, op=op, **kw)) + "\n")
+        p.stdin.flush()
+        rep = json.loads(p.stdout.readline())
+        assert rep["id"] == rid
+        return rep
+
+    try:
+        assert ask("hello") == {"id": 1, "ok": True, "protocol": 1}
+        for n in (1, 31, 1023):
+            prompt = r.integers(0, SMALL["vocab"], n).tolist()
+            other = r.integers(0, SMALL["vocab"], 17).tolist()
+            whole = ask("generate", prompt=prompt, max_tokens=32, reset=True)["tokens"]
+            assert len(whole) == 32 and all(0 <= t < SMALL["vocab"] for t in whole)
+            first = ask("generate", prompt=prompt, max_tokens=1, reset=True)["tokens"]
+            assert ask("hello")["protocol"] == 1
+            bad = ask("generate", prompt=[1], max_tokens=3, reset=False)
+            assert bad["ok"] is False and bad["error"] == "continuation prompt must be empty"
+            rest = ask("generate", prompt=[], max_tokens=31, reset=False)["tokens"]
+            assert first + rest == whole, f"split request differs at prompt length {n}"
+            ask("generate", prompt=other, max_tokens=5, reset=True)
+            assert ask("generate", prompt=prompt, max_tokens=32, reset=True)["tokens"] == whole
+        p.stdin.close()
+        assert p.wait(timeout=60) == 0
+    finally:
+        if p.poll() is None:
+            p.kill()
+            p.wait()
