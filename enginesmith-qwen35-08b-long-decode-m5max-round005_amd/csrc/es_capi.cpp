@@ -138,6 +138,15 @@ int es_q4_matvec_add(const es_q4* w, const uint16_t* x, const uint16_t* residual
   return hip_status(es::launch_qmv(m, x, residual, y, nullptr, S(stream)), "es_q4_matvec_add");
 }
 
+int es_q4_gemm(const es_q4* w, const uint16_t* x, int rows, const uint16_t* residual, uint16_t* y,
+               void* stream) {
+  es::Q4 m;
+  if (!to_q4(w, &m) || !x || !y) return fail(ES_ERR_INVALID, "es_q4_gemm: null argument");
+  if (rows < 1 || m.k % 64 != 0) return fail(ES_ERR_INVALID, "es_q4_gemm: rows >= 1 and k % 64 == 0 required");
+  if (x == y) return fail(ES_ERR_INVALID, "es_q4_gemm: x must not alias y");
+  return hip_status(es::launch_q4_gemm(m, x, rows, residual, y, S(stream)), "es_q4_gemm");
+}
+
 int es_q4_rmsnorm_matvec_multi(const es_q4* w, int count, const uint16_t* x, const uint16_t* gain,
                                uint16_t* norm_out, uint16_t* const* y, void* stream) {
   if (count < 1 || count > 4 || !w || !y || !x) return fail(ES_ERR_INVALID, "es_q4_rmsnorm_matvec_multi: bad count/pointers");

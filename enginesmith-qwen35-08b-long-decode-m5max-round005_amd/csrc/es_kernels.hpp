@@ -122,6 +122,13 @@ hipError_t launch_attn_merge(const AttnArgs& a, hipStream_t s);
 // the next launch adds the 8 partials pairwise.
 hipError_t launch_attn_merge_out(const AttnArgs& a, const Q4& o, float* part, hipStream_t s);
 
+// ---- batched prefill, k_prefill.hip ----
+// Y[m,N] = bf16(X[m,K] . W^T) with W dequantised to bf16 per weight, fp32
+// accumulation (qmm_q4_nax); with residual: Y = bf16(R + bf16(X . W^T)).
+// K a multiple of 64. Y may alias R.
+hipError_t launch_q4_gemm(const Q4& w, const uint16_t* x, int m, const uint16_t* residual, uint16_t* y,
+                          hipStream_t s);
+
 // ---- vocab head, k_head.hip ----
 struct HeadArgs {
   Q4 embed;                 // tied table [vocab, 1024]

@@ -73,6 +73,7 @@ _SIGNATURES = {
     "es_weights_tensor_info": (c_int, [c_int, c_int, c_int, c_char_p, c_int, POINTER(c_uint64), POINTER(c_uint64),
                                        POINTER(c_int)]),
     "es_weights_random": (c_int, [c_int, c_int, c_uint64, c_void_p, c_size_t, c_int]),
+    "es_q4_gemm": (c_int, [POINTER(Q4), c_void_p, c_int, c_void_p, c_void_p, c_void_p]),
     "es_weights_tensor_shape": (c_int, [c_int, c_int, c_int, POINTER(ctypes.c_int64), c_int]),
     "es_checkpoint_config": (c_int, [c_char_p, POINTER(c_int), POINTER(c_int)]),
     "es_checkpoint_load": (c_int, [c_char_p, c_int, c_int, c_void_p, c_size_t]),

@@ -88,6 +88,14 @@ int es_q4_matvec(const es_q4* w, const uint16_t* x, uint16_t* y, float* y_f32, v
 int es_q4_matvec_add(const es_q4* w, const uint16_t* x, const uint16_t* residual, uint16_t* y,
                      void* stream);
 
+/* Row-batched LINEAR (prefill, rows > 1; model.rs:189-199 routes it to
+ * qmm_q4_nax, linear_nax.metal:1096-1140): y[r,n] = bf16(sum_k x[r,k] *
+ * bf16(scale*q + bias)) with fp32 accumulation, or with residual (may alias
+ * y) bf16(residual[r,n] + that). x is [rows, k], y [rows, n]; k % 64 == 0;
+ * x must not alias y. */
+int es_q4_gemm(const es_q4* w, const uint16_t* x, int rows, const uint16_t* residual, uint16_t* y,
+               void* stream);
+
 /* qmv_multi_g8_norm (linear_input_norm.metal:13-119) with the rms_norm_bf16
  * arithmetic (linear.metal:300-331): u = bf16(bf16(x*rsqrt(mean(x^2)+1e-6))*gain)
  * over 1024 columns, then y[i] = bf16(W_i u) for count (1..4) matrices of

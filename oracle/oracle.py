@@ -140,6 +140,37 @@ def q4_matvec(codes, scales, biases, x, want_f32=False):
     return (y, yf) if want_f32 else y
 
 
+# ---- row-batched linear (prefill) ----
+def q4_dequant_bf16(codes, scales, biases):
+    """qmm_q4_nax's staged weights (linear_nax.metal:1118-1123): each weight
+    dequantised as bf16(fp32(scale) * q + fp32(bias)). scale * q is exact in
+    fp32 (8-bit by 4-bit significands), so the sum is rounded once, as a fused
+    multiply-add would round it. Returns fp32 values of the bf16 weights [n, k]."""
+    n, k8 = codes.shape
+    k = k8 * 8
+    shifts = np.arange(8, dtype=np.uint32) * 4
+    q = ((codes[:, :, None] >> shifts[None, None, :]) & 15).reshape(n, k).astype(np.float32)
+    s = np.repeat(bf16_to_f32(scales), 64, axis=1)
+    b = np.repeat(bf16_to_f32(biases), 64, axis=1)
+    return bf16_to_f32(f32_to_bf16(s * q + b))
+
+
+def q4_gemm(codes, scales, biases, x, residual=None):
+    """Row-batched linear of the prefill path (qmm_q4_nax, linear_nax.metal:
+    1096-1140; model.rs:189-199): y[r] = bf16(sum_k x[r,k] * w[n,k]) over the
+    bf16-dequantised weights, the sum taken in fp64 and rounded to fp32 before
+    the bf16 round (the kernel accumulates in fp32 in its own order, so
+    results agree to within the fp32 rounding of the sum); with a residual,
+    bf16(residual + bf16(sum)). x: [rows, k] bf16 bits."""
+    w = q4_dequant_bf16(codes, scales, biases).astype(np.float64)
+    xf = bf16_to_f32(np.asarray(x, dtype=np.uint16)).astype(np.float64)
+    acc = (xf @ w.T).astype(np.float32)
+    y = f32_to_bf16(acc)
+    if residual is not None:
+        y = f32_to_bf16(bf16_to_f32(np.asarray(residual, dtype=np.uint16)) + bf16_to_f32(y))
+    return y
+
+
 def q4_matvec_add(codes, scales, biases, x, residual):
     n, k8 = codes.shape
     y = np.empty(n, dtype=np.uint16)

@@ -1,0 +1,68 @@
+"""GPU parity of the batched prefill kernels (encode_forward with rows > 1,
+model.rs:228-350) against the oracle's restatements. The prefill GEMM
+accumulates in fp32 on MFMA in its own order, so its bf16 outputs agree with
+the oracle's fp64 sums to within one bf16 ulp on the few elements whose fp32
+value lies at a rounding boundary (tolerance stated per test)."""
+import numpy as np
+import pytest
+
+import esdecode as E
+import oracle as O
+from helpers import assert_bf16_close, bf16, f32, random_q4, rng
+
+pytestmark = pytest.mark.gpu
+
+GEMM_SHAPES = [(1, 16, 1024), (17, 1024, 1024), (128, 128, 64), (300, 6144, 1024), (257, 1024, 3584),
+               (2048, 512, 1024), (64, 1000, 2048), (130, 16, 1024)]
+
+
+@pytest.mark.parametrize("m,n,k", GEMM_SHAPES)
+def test_q4_gemm(m, n, k):
+    print(f"case q4_gemm m={m} n={n} k={k}", flush=True)
+    r = rng(2000 + m + n + k)
+    codes, scales, biases = random_q4(r, n, k)
+    x = bf16(r.normal(0, 1, (m, k)))
+    W = E.DeviceQ4(codes, scales, biases)
+    dx = E.DeviceBuffer.from_numpy(x)
+    dy = E.DeviceBuffer(m * n * 2)
+    E.check(E.lib().es_q4_gemm(W.struct, dx.ptr, m, None, dy.ptr, None))
+    E.synchronize()
+    got = dy.numpy(np.uint16).reshape(m, n)
+    want = O.q4_gemm(codes, scales, biases, x)
+    # tolerance: fp32 accumulation order only; <= 1 bf16 ulp on <= 1% of outputs
+    assert_bf16_close(got, want, max_ulp=1, max_frac=0.01, what=f"gemm {m}x{n}x{k}")
+
+
+@pytest.mark.parametrize("k", [1024, 3584])
+def test_q4_gemm_residual_in_place(k):
+    r = rng(3000 + k)
+    m, n = 200, 1024
+    codes, scales, biases = random_q4(r, n, k)
+    x = bf16(r.normal(0, 1, (m, k)))
+    res = bf16(r.normal(0, 1, (m, n)))
+    W = E.DeviceQ4(codes, scales, biases)
+    dx = E.DeviceBuffer.from_numpy(x)
+    dh = E.DeviceBuffer.from_numpy(res)
+    E.check(E.lib().es_q4_gemm(W.struct, dx.ptr, m, dh.ptr, dh.ptr, None))  # y aliases residual
+    E.synchronize()
+    want = O.q4_gemm(codes, scales, biases, x, residual=res)
+    got = dh.numpy(np.uint16).reshape(m, n)
+    # tolerance: one bf16 ulp of the GEMM term (the residual add after it can
+    # cancel, so a 1-ulp difference there is many ulps of the sum) plus one
+    # ulp of the sum; at most 1% of the outputs differ
+    y = f32(O.q4_gemm(codes, scales, biases, x)).astype(np.float64)
+    sum_ = f32(want).astype(np.float64)
+    ulp = lambda v: 2.0 ** (np.floor(np.log2(np.maximum(np.abs(v), 1e-30))) - 7)
+    d = np.abs(f32(got).astype(np.float64) - sum_)
+    assert np.all(d <= ulp(y) + ulp(sum_)), f"gemm add k={k}: max excess {np.max(d - ulp(y) - ulp(sum_))}"
+    assert np.mean(got != want) <= 0.01
+
+
+def test_q4_gemm_rejects_bad_arguments():
+    r = rng(4)
+    codes, scales, biases = random_q4(r, 8, 64)
+    W = E.DeviceQ4(codes, scales, biases)
+    dx = E.DeviceBuffer(4096)
+    dy = E.DeviceBuffer(4096)
+    assert E.lib().es_q4_gemm(W.struct, dx.ptr, 0, None, dy.ptr, None) != E.ES_OK
+    assert E.lib().es_q4_gemm(W.struct, dx.ptr, 1, None, dx.ptr, None) != E.ES_OK

@@ -130,3 +130,41 @@ def test_swiglu_rounding_sequence():
     gd = f32(g).astype(np.float64)
     exact = bf16((gd / (1 + np.exp(-gd)) * f32(u)).astype(np.float32))
     assert_bf16_close(got, exact, max_ulp=3, max_frac=0.6, atol_rel=1e-2, what="swiglu vs fp64")
+
+
+# ---- row-batched linear (prefill) ----
+
+def test_q4_gemm_constant_weights_closed_form():
+    """All codes 0: every weight is exactly bf16(bias), so row r of the output
+    is bf16(bias * sum(x[r])) per group; with one group and a power-of-two
+    bias the products and sums are exact."""
+    r = rng(501)
+    n, k, m = 8, 64, 5
+    codes = np.zeros((n, k // 8), dtype=np.uint32)
+    scales = bf16(np.full((n, 1), 0.5))
+    biases = bf16(np.full((n, 1), 0.25))
+    x = bf16(np.round(r.normal(0, 4, (m, k))))  # small integers: exact sums
+    y = O.q4_gemm(codes, scales, biases, x)
+    want = bf16(0.25 * f32(x).astype(np.float64).sum(axis=1))
+    assert np.array_equal(y, np.repeat(want[:, None], n, axis=1))
+
+
+def test_q4_gemm_dequant_rounding_and_rows():
+    """Within bf16 weight rounding of the unrounded fp64 dequantisation, row
+    by row identical to a one-row call, residual added after the bf16 round."""
+    r = rng(502)
+    n, k, m = 96, 1024, 7
+    codes, scales, biases = random_q4(r, n, k)
+    x = bf16(r.normal(0, 1, (m, k)))
+    y = O.q4_gemm(codes, scales, biases, x)
+    exact = f32(x).astype(np.float64) @ dequant_f64(codes, scales, biases).T
+    wq = O.q4_dequant_bf16(codes, scales, biases).astype(np.float64)
+    unrounded = dequant_f64(codes, scales, biases)
+    assert np.all(np.abs(wq - unrounded) <= np.abs(unrounded) * 2.0 ** -8 + 1e-30)
+    err_bound = (np.abs(f32(x)).astype(np.float64) @ np.abs(unrounded).T) * 2.0 ** -8 + np.abs(exact) * 2.0 ** -7
+    assert np.all(np.abs(f32(y) - exact) <= err_bound)
+    for i in range(m):
+        assert np.array_equal(O.q4_gemm(codes, scales, biases, x[i:i + 1])[0], y[i])
+    res = bf16(r.normal(0, 1, (m, n)))
+    ya = O.q4_gemm(codes, scales, biases, x, residual=res)
+    assert np.array_equal(ya, bf16(f32(res) + f32(y)))
