@@ -147,6 +147,75 @@ int es_q4_gemm(const es_q4* w, const uint16_t* x, int rows, const uint16_t* resi
   return hip_status(es::launch_q4_gemm(m, x, rows, residual, y, S(stream)), "es_q4_gemm");
 }
 
+// ---- prefill row operators ----
+int es_embed_rows(const es_q4* embed, const uint32_t* tokens, int rows, uint16_t* h, void* stream) {
+  es::Q4 e;
+  if (!to_q4(embed, &e) || !tokens || !h) return fail(ES_ERR_INVALID, "es_embed_rows: null argument");
+  if (rows < 1 || e.k != 1024) return fail(ES_ERR_INVALID, "es_embed_rows: rows >= 1 and a [vocab, 1024] table required");
+  return hip_status(es::launch_embed_rows(e, tokens, rows, h, S(stream)), "es_embed_rows");
+}
+
+int es_rmsnorm_rows(const uint16_t* x, const uint16_t* gain, int rows, uint16_t* out, void* stream) {
+  if (!x || !gain || !out || rows < 1) return fail(ES_ERR_INVALID, "es_rmsnorm_rows: null argument or rows < 1");
+  return hip_status(es::launch_rmsnorm_rows(x, gain, rows, out, S(stream)), "es_rmsnorm_rows");
+}
+
+int es_swiglu_rows(const uint16_t* gate, const uint16_t* up, int count, uint16_t* act, void* stream) {
+  if (!gate || !up || !act || count < 1) return fail(ES_ERR_INVALID, "es_swiglu_rows: null argument or count < 1");
+  return hip_status(es::launch_swiglu_rows(gate, up, count, act, S(stream)), "es_swiglu_rows");
+}
+
+int es_gdn_prepare_rows(const uint16_t* raw, uint16_t* ring, const uint16_t* conv_w, const uint16_t* a_proj,
+                        const uint16_t* b_proj, const float* a_log, const uint16_t* dt_bias, int position,
+                        int rows, uint16_t* q, uint16_t* k, uint16_t* v, float* g, float* beta,
+                        void* stream) {
+  es::GdnPrepRowsArgs a{raw, ring, conv_w, a_proj, b_proj, a_log, dt_bias, position, rows, q, k, v, g, beta};
+  if (!raw || !ring || !conv_w || !a_proj || !b_proj || !a_log || !dt_bias || !q || !k || !v || !g || !beta)
+    return fail(ES_ERR_INVALID, "es_gdn_prepare_rows: null argument");
+  if (rows < 1 || position < 0) return fail(ES_ERR_INVALID, "es_gdn_prepare_rows: rows >= 1 and position >= 0 required");
+  return hip_status(es::launch_gdn_prep_rows(a, S(stream)), "es_gdn_prepare_rows");
+}
+
+int es_gdn_recur_rows(const uint16_t* q, const uint16_t* k, const uint16_t* v, const float* g, const float* beta,
+                      int rows, float* state, uint16_t* y, void* stream) {
+  if (!q || !k || !v || !g || !beta || !state || !y || rows < 1)
+    return fail(ES_ERR_INVALID, "es_gdn_recur_rows: null argument or rows < 1");
+  return hip_status(es::launch_gdn_recur_rows(q, k, v, g, beta, rows, state, y, S(stream)), "es_gdn_recur_rows");
+}
+
+int es_gdn_norm_gate_rows(const uint16_t* y, const uint16_t* z, const uint16_t* norm_w, int rows, uint16_t* out,
+                          void* stream) {
+  if (!y || !z || !norm_w || !out || rows < 1) return fail(ES_ERR_INVALID, "es_gdn_norm_gate_rows: null argument or rows < 1");
+  return hip_status(es::launch_gdn_norm_gate_rows(y, z, norm_w, rows, out, S(stream)), "es_gdn_norm_gate_rows");
+}
+
+int es_attn_prepare_rows(const uint16_t* q_proj, const uint16_t* k_proj, const uint16_t* v_proj,
+                         const uint16_t* q_gain, const uint16_t* k_gain, const float* inv_freq, int position,
+                         int rows, uint16_t* query, uint16_t* kcache, uint16_t* vcache, int capacity,
+                         void* stream) {
+  es::AttnPrepRowsArgs a{q_proj, k_proj, v_proj, q_gain, k_gain, inv_freq, position, rows, query, kcache, vcache,
+                         capacity};
+  if (!q_proj || !k_proj || !v_proj || !q_gain || !k_gain || !inv_freq || !query || !kcache || !vcache)
+    return fail(ES_ERR_INVALID, "es_attn_prepare_rows: null argument");
+  if (rows < 1 || position < 0 || (int64_t)position + rows > capacity)
+    return fail(ES_ERR_INVALID, "es_attn_prepare_rows: rows >= 1 and 0 <= position, position + rows <= capacity required");
+  return hip_status(es::launch_attn_prep_rows(a, S(stream)), "es_attn_prepare_rows");
+}
+
+int es_attn_prefill(const uint16_t* query, const uint16_t* kcache, const uint16_t* vcache, int position, int rows,
+                    int capacity, uint16_t* out, void* stream) {
+  if (!query || !kcache || !vcache || !out) return fail(ES_ERR_INVALID, "es_attn_prefill: null argument");
+  if (rows < 1 || position < 0 || (int64_t)position + rows > capacity)
+    return fail(ES_ERR_INVALID, "es_attn_prefill: rows >= 1 and 0 <= position, position + rows <= capacity required");
+  return hip_status(es::launch_attn_prefill(query, kcache, vcache, position, rows, capacity, out, S(stream)),
+                    "es_attn_prefill");
+}
+
+int es_attn_gate_rows(const uint16_t* o, const uint16_t* q_proj, int rows, uint16_t* gated, void* stream) {
+  if (!o || !q_proj || !gated || rows < 1) return fail(ES_ERR_INVALID, "es_attn_gate_rows: null argument or rows < 1");
+  return hip_status(es::launch_attn_gate_rows(o, q_proj, rows, gated, S(stream)), "es_attn_gate_rows");
+}
+
 int es_q4_rmsnorm_matvec_multi(const es_q4* w, int count, const uint16_t* x, const uint16_t* gain,
                                uint16_t* norm_out, uint16_t* const* y, void* stream) {
   if (count < 1 || count > 4 || !w || !y || !x) return fail(ES_ERR_INVALID, "es_q4_rmsnorm_matvec_multi: bad count/pointers");

@@ -351,4 +351,75 @@ __device__ __forceinline__ int load_pos(const StepState* st, int pos_val) {
 }
 
 
+
+__device__ __forceinline__ void store_bf16x32(uint16_t* p, const float* v) {
+  u32x4* q = reinterpret_cast<u32x4*>(p);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    u32x4 o;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) o[j] = pack_bf2(v[8 * i + 2 * j], v[8 * i + 2 * j + 1]);
+    q[i] = o;
+  }
+}
+
+// ---- shared by the decode and the row-batched (prefill) kernels ----
+
+// Causal conv1d of one channel over taps (oldest first) + SiLU with the MLX
+// bf16 steps (gdn_input.metal:163-170): x = bf16(fma chain), bf16(x*sigmoid_bf(x)).
+__device__ __forceinline__ float conv4_silu(const uint32_t* x, uint2 w) {
+  float acc = 0.0f;
+  acc = fmaf(bf2f(x[0]), bf_lo(w.x), acc);
+  acc = fmaf(bf2f(x[1]), bf_hi(w.x), acc);
+  acc = fmaf(bf2f(x[2]), bf_lo(w.y), acc);
+  acc = fmaf(bf2f(x[3]), bf_hi(w.y), acc);
+  const float xv = rbf(acc);
+  return rbf(xv * sigmoid_bf(xv));
+}
+
+// RMSNorm of a 1024-wide row held as 32-element slices by the 32 lanes of a
+// half-wave (rms_norm_bf16 rounding points, linear.metal:311-329): sum of
+// squares by slice (fma chain) then tree32, out = bf16(bf16(x*inv)*gain).
+__device__ __forceinline__ void norm_slice_1024(const float* xv, const Raw64& gain, float* xn) {
+  const float ss = tree32(sumsq32(xv));
+  const float inv = 1.0f / sqrtf(ss / 1024.0f + 1e-6f);
+  float gv[32];
+  unpack_bf16x32(gain, gv);
+#pragma unroll
+  for (int j = 0; j < 32; ++j) xn[j] = rbf(rbf(xv[j] * inv) * gv[j]);
+}
+
+// Normalise 4 consecutive dims of a 256-wide head held by a full wave.
+// xv, gv: the lane's 4 bf16 values of the head and of the gain.
+__device__ __forceinline__ void head_norm4(const uint2 xv, const uint2 gv, float* out) {
+  const float xf[4] = {bf_lo(xv.x), bf_hi(xv.x), bf_lo(xv.y), bf_hi(xv.y)};
+  const float gf[4] = {bf_lo(gv.x), bf_hi(gv.x), bf_lo(gv.y), bf_hi(gv.y)};
+  float ss = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) ss = fmaf(xf[i], xf[i], ss);
+  ss = tree64(ss);
+  const float inv = 1.0f / sqrtf(ss / 256.0f + 1e-6f);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) out[i] = rbf(rbf(xf[i] * inv) * gf[i]);
+}
+
+// Rotary component d of a normalised head (attention.metal:55-70):
+// d < 32: fma(lo, c, -(hi*s)); 32 <= d < 64: fma(lo, s, hi*c), where lo and
+// hi are dims d & 31 and (d & 31) + 32. own is dim d, partner dim d ^ 32;
+// inv is inv_freq[d & 31] (only used for d < 64).
+__device__ __forceinline__ float rope_at(float own, float partner, int d, int pos, float inv) {
+  if (d >= 64) return own;
+  const float angle = (float)pos * inv;
+  float s, c;
+  es_sincos(angle, &s, &c);
+  const float lo = d < 32 ? own : partner, hi = d < 32 ? partner : own;
+  return rbf(d < 32 ? fmaf(lo, c, -(hi * s)) : fmaf(lo, s, hi * c));
+}
+
+// Value of lane l ^ 8 inside each 16-lane row (DPP row rotate by 8). With 4
+// dims per lane, dim d ^ 32 of a head (d < 64) sits in lane ^ 8.
+__device__ __forceinline__ float dpp_row_ror8(float v) {
+  return __builtin_amdgcn_update_dpp(0.0f, v, 0x128, 0xf, 0xf, false);
+}
+
 }  // namespace es

@@ -128,6 +128,52 @@ hipError_t launch_attn_merge_out(const AttnArgs& a, const Q4& o, float* part, hi
 // K a multiple of 64. Y may alias R.
 hipError_t launch_q4_gemm(const Q4& w, const uint16_t* x, int m, const uint16_t* residual, uint16_t* y,
                           hipStream_t s);
+// Row forms of the decode operators (m rows = consecutive positions
+// pos0 .. pos0+m-1), each with the decode kernels' arithmetic per row.
+hipError_t launch_embed_rows(const Q4& e, const uint32_t* tokens, int m, uint16_t* h, hipStream_t s);
+hipError_t launch_rmsnorm_rows(const uint16_t* x, const uint16_t* gain, int m, uint16_t* out, hipStream_t s);
+hipError_t launch_swiglu_rows(const uint16_t* gate, const uint16_t* up, int count, uint16_t* act,
+                              hipStream_t s);
+struct GdnPrepRowsArgs {
+  const uint16_t* raw;      // [m, 6144] projected q|k|v before the convolution
+  uint16_t* ring;           // [4, 6144] raw rows of the last positions, slot = position & 3
+  const uint16_t* conv_w;   // [6144, 4]
+  const uint16_t* a_proj;   // [m, 16]
+  const uint16_t* b_proj;   // [m, 16]
+  const float* a_log;       // [16]
+  const uint16_t* dt_bias;  // [16]
+  int pos0, m;
+  uint16_t *q, *k, *v;      // [m, 16, 128] normalised q, k and activated v
+  float *g, *beta;          // [m, 16]
+};
+// Convolution, activation, q/k normalisation and gates of every row, then
+// the ring takes the chunk's last raw rows.
+hipError_t launch_gdn_prep_rows(const GdnPrepRowsArgs& a, hipStream_t s);
+// Delta-rule recurrence over the m rows in order; y [m, 2048] bf16.
+hipError_t launch_gdn_recur_rows(const uint16_t* q, const uint16_t* k, const uint16_t* v, const float* g,
+                                 const float* beta, int m, float* state, uint16_t* y, hipStream_t s);
+hipError_t launch_gdn_norm_gate_rows(const uint16_t* y, const uint16_t* z, const uint16_t* norm_w, int m,
+                                     uint16_t* out, hipStream_t s);
+struct AttnPrepRowsArgs {
+  const uint16_t* qg;       // [m, 4096] q|gate per head
+  const uint16_t* k;        // [m, 512]
+  const uint16_t* v;        // [m, 512]
+  const uint16_t* q_gain;   // [256]
+  const uint16_t* k_gain;   // [256]
+  const float* inv_freq;    // [32]
+  int pos0, m;
+  uint16_t* qr;             // [m, 8, 256] normalised, roped queries
+  uint16_t* kcache;         // [2, capacity, 256]
+  uint16_t* vcache;
+  int capacity;
+};
+hipError_t launch_attn_prep_rows(const AttnPrepRowsArgs& a, hipStream_t s);
+// Causal GQA attention of the m queries at positions pos0.. over cache rows
+// 0 .. pos0+m-1: o [m, 8, 256] bf16 (attn_prefill).
+hipError_t launch_attn_prefill(const uint16_t* qr, const uint16_t* kcache, const uint16_t* vcache, int pos0,
+                               int m, int capacity, uint16_t* o, hipStream_t s);
+hipError_t launch_attn_gate_rows(const uint16_t* o, const uint16_t* qg, int m, uint16_t* gated,
+                                 hipStream_t s);
 
 // ---- vocab head, k_head.hip ----
 struct HeadArgs {

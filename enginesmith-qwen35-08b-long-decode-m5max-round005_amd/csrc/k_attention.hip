@@ -35,39 +35,6 @@ namespace {
 
 constexpr float kFiniteMin = -3.40282346638528859812e38f;
 
-// Normalise 4 consecutive dims of a 256-wide head held by a full wave.
-// xv, gv: the lane's 4 bf16 values of the head and of the gain.
-__device__ __forceinline__ void head_norm4(const uint2 xv, const uint2 gv, float* out) {
-  const float xf[4] = {bf_lo(xv.x), bf_hi(xv.x), bf_lo(xv.y), bf_hi(xv.y)};
-  const float gf[4] = {bf_lo(gv.x), bf_hi(gv.x), bf_lo(gv.y), bf_hi(gv.y)};
-  float ss = 0.0f;
-#pragma unroll
-  for (int i = 0; i < 4; ++i) ss = fmaf(xf[i], xf[i], ss);
-  ss = tree64(ss);
-  const float inv = 1.0f / sqrtf(ss / 256.0f + 1e-6f);
-#pragma unroll
-  for (int i = 0; i < 4; ++i) out[i] = rbf(rbf(xf[i] * inv) * gf[i]);
-}
-
-// Rotary component d of a normalised head (attention.metal:55-70):
-// d < 32: fma(lo, c, -(hi*s)); 32 <= d < 64: fma(lo, s, hi*c), where lo and
-// hi are dims d & 31 and (d & 31) + 32. own is dim d, partner dim d ^ 32;
-// inv is inv_freq[d & 31] (only used for d < 64).
-__device__ __forceinline__ float rope_at(float own, float partner, int d, int pos, float inv) {
-  if (d >= 64) return own;
-  const float angle = (float)pos * inv;
-  float s, c;
-  es_sincos(angle, &s, &c);
-  const float lo = d < 32 ? own : partner, hi = d < 32 ? partner : own;
-  return rbf(d < 32 ? fmaf(lo, c, -(hi * s)) : fmaf(lo, s, hi * c));
-}
-
-// Value of lane l ^ 8 inside each 16-lane row (DPP row rotate by 8). With 4
-// dims per lane, dim d ^ 32 of a head (d < 64) sits in lane ^ 8.
-__device__ __forceinline__ float dpp_row_ror8(float v) {
-  return __builtin_amdgcn_update_dpp(0.0f, v, 0x128, 0xf, 0xf, false);
-}
-
 __device__ __forceinline__ float tree8(float v) {
   v = tree4(v);
   return v + dpp_half_mirror(v);

@@ -47,13 +47,7 @@ __device__ __forceinline__ float conv_silu(const RingTaps& r, int pos) {
     const int slot = (sh + t) & 3;
     x[t] = slot == 0 ? r.v[0] : slot == 1 ? r.v[1] : slot == 2 ? r.v[2] : r.v[3];
   }
-  float acc = 0.0f;
-  acc = fmaf(bf2f(x[0]), bf_lo(r.w.x), acc);
-  acc = fmaf(bf2f(x[1]), bf_hi(r.w.x), acc);
-  acc = fmaf(bf2f(x[2]), bf_lo(r.w.y), acc);
-  acc = fmaf(bf2f(x[3]), bf_hi(r.w.y), acc);
-  const float xv = rbf(acc);
-  return rbf(xv * sigmoid_bf(xv));
+  return conv4_silu(x, r.w);
 }
 
 __global__ __launch_bounds__(256) void k_gdn_recur(GdnRecurArgs a) {

@@ -20,29 +20,6 @@
 namespace es {
 namespace {
 
-__device__ __forceinline__ void store_bf16x32(uint16_t* p, const float* v) {
-  u32x4* q = reinterpret_cast<u32x4*>(p);
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    u32x4 o;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) o[j] = pack_bf2(v[8 * i + 2 * j], v[8 * i + 2 * j + 1]);
-    q[i] = o;
-  }
-}
-
-// RMSNorm of a K=1024 vector whose 32-element slice `sl` this lane holds; the
-// 32 lanes of a half-wave cover the vector once (rms_norm_bf16 arithmetic,
-// linear.metal:311-329: fp32 sum of squares, bf16(bf16(x*inv)*gain)).
-__device__ __forceinline__ void norm_slice_1024(const float* xv, const Raw64& gain, float* xn) {
-  const float ss = tree32(sumsq32(xv));
-  const float inv = 1.0f / sqrtf(ss / 1024.0f + 1e-6f);
-  float gv[32];
-  unpack_bf16x32(gain, gv);
-#pragma unroll
-  for (int j = 0; j < 32; ++j) xn[j] = rbf(rbf(xv[j] * inv) * gv[j]);
-}
-
 // Dequantised embedding slice (embedding_q4, linear.metal:20-23). The table
 // is taken by value: a reference into the kernel-argument struct made the
 // compiler copy the whole struct (272 B) to per-thread scratch memory.

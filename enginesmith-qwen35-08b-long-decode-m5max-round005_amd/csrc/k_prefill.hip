@@ -134,6 +134,415 @@ __global__ __launch_bounds__(256) void k_q4_gemm(Q4 w, const uint16_t* __restric
     }
 }
 
+// ---- row kernels: the decode operators' arithmetic, one row per token ----
+
+// Embedding rows (embedding_q4, linear.metal:11-24): h = bf16(scale*q + bias).
+// Half-wave per row, 32 elements per lane.
+__global__ __launch_bounds__(256) void k_embed_rows(Q4 e, const uint32_t* tokens, int m, uint16_t* h) {
+  const int row = blockIdx.x * 8 + (threadIdx.x >> 5), sl = threadIdx.x & 31;
+  if (row >= m) return;
+  uint32_t tok = tokens[row];
+  if (tok >= (uint32_t)e.n) tok = 0;
+  const u32x4 c = *reinterpret_cast<const u32x4*>(e.w + (size_t)tok * 128 + sl * 4);
+  const float sc = bf2f(e.s[(size_t)tok * 16 + sl / 2]), bi = bf2f(e.b[(size_t)tok * 16 + sl / 2]);
+  float xv[32];
+#pragma unroll
+  for (int w = 0; w < 4; ++w)
+#pragma unroll
+    for (int j = 0; j < 8; ++j) xv[8 * w + j] = rbf(fmaf(sc, (float)((c[w] >> (4 * j)) & 15u), bi));
+  store_bf16x32(h + (size_t)row * 1024 + sl * 32, xv);
+}
+
+// RMSNorm rows (rms_norm_bf16 rounding points, the decode kernels' order).
+__global__ __launch_bounds__(256) void k_rmsnorm_rows(const uint16_t* x, const uint16_t* gain, int m,
+                                                      uint16_t* out) {
+  const int row = blockIdx.x * 8 + (threadIdx.x >> 5), sl = threadIdx.x & 31;
+  if (row >= m) return;
+  const Raw64 xr = load_raw64(x + (size_t)row * 1024 + sl * 32);
+  const Raw64 gr = load_raw64(gain + sl * 32);
+  float xv[32], xn[32];
+  unpack_bf16x32(xr, xv);
+  norm_slice_1024(xv, gr, xn);
+  store_bf16x32(out + (size_t)row * 1024 + sl * 32, xn);
+}
+
+// SwiGLU (swiglu_bf16, linear.metal:382-398): silu = bf16(g*sigmoid_bf(g)),
+// act = bf16(silu*up), over bf16 gate and up.
+__global__ __launch_bounds__(256) void k_swiglu_rows(const uint16_t* gate, const uint16_t* up, int count,
+                                                     uint16_t* act) {
+  const int i = blockIdx.x * 256 + threadIdx.x;
+  if (i >= count) return;
+  const float gb = bf2f(gate[i]), ub = bf2f(up[i]);
+  const float silu = rbf(gb * sigmoid_bf(gb));
+  act[i] = (uint16_t)f2bf(silu * ub);
+}
+
+// GDN prepare rows (gdn_conv + gdn_prepare, gdn.metal:33-120, with the decode
+// kernels' arithmetic): one wave per (row, head). Lane i takes channels i and
+// 64+i of the head's q, k and v: causal conv over taps (pos-3 .. pos) whose
+// inputs are the chunk's raw rows, or the ring for positions before the
+// chunk; SiLU; q and k L2-normalised (sum of squares tree64 over channels
+// 0..63 plus tree64 over 64..127) and scaled (q by 1/128, k by bf16(128^-1/2));
+// lane 0 forms the gates g = exp(-exp(A_log)*softplus(bf16(a+dt))), beta =
+// sigmoid_bf(b). Outputs bf16 q, k, v [m,16,128] and fp32 g, beta [m,16].
+__global__ __launch_bounds__(256) void k_gdn_prep_rows(const uint16_t* raw, const uint16_t* ring,
+                                                       const uint16_t* conv_w, const uint16_t* a_proj,
+                                                       const uint16_t* b_proj, const float* a_log,
+                                                       const uint16_t* dt_bias, int pos0, int m,
+                                                       uint16_t* q, uint16_t* k, uint16_t* v, float* g,
+                                                       float* beta) {
+  const int lane = threadIdx.x & 63, h = blockIdx.y * 4 + (threadIdx.x >> 6), t = blockIdx.x;
+  if (t >= m) return;
+  const int pos = pos0 + t;
+  float out[3][2];
+#pragma unroll
+  for (int part = 0; part < 3; ++part)
+#pragma unroll
+    for (int half = 0; half < 2; ++half) {
+      const int c = part * 2048 + h * 128 + half * 64 + lane;
+      uint32_t x[4];
+#pragma unroll
+      for (int tap = 0; tap < 4; ++tap) {
+        const int tt = t - 3 + tap;
+        x[tap] = tt >= 0 ? raw[(size_t)tt * kConv + c] : ring[(size_t)((pos - 3 + tap) & 3) * kConv + c];
+      }
+      const uint2 w = *reinterpret_cast<const uint2*>(conv_w + (size_t)c * 4);
+      out[part][half] = conv4_silu(x, w);
+    }
+  const size_t o = ((size_t)t * 16 + h) * 128;
+#pragma unroll
+  for (int part = 0; part < 2; ++part) {
+    const float tot = tree64(out[part][0] * out[part][0]) + tree64(out[part][1] * out[part][1]);
+    const float inv = 1.0f / sqrtf(tot / 128.0f + 1.0e-6f / 128.0f);
+    const float scale = part == 0 ? 0.0078125f : rbf(0.08838834764831845f);
+    uint16_t* dst = part == 0 ? q : k;
+    dst[o + lane] = (uint16_t)f2bf(rbf(out[part][0] * inv) * scale);
+    dst[o + 64 + lane] = (uint16_t)f2bf(rbf(out[part][1] * inv) * scale);
+  }
+  v[o + lane] = (uint16_t)f2bf(out[2][0]);
+  v[o + 64 + lane] = (uint16_t)f2bf(out[2][1]);
+  if (lane == 0) {
+    const float ax = rbf(bf2f(a_proj[(size_t)t * 16 + h]) + bf2f(dt_bias[h]));
+    g[(size_t)t * 16 + h] = es_exp(-es_exp(a_log[h]) * softplus_bf(ax));
+    beta[(size_t)t * 16 + h] = sigmoid_bf(bf2f(b_proj[(size_t)t * 16 + h]));
+  }
+}
+
+// History after a chunk (gdn_history, gdn.metal:56-73, as the decode ring):
+// the raw rows of the chunk's last min(m, 4) positions go to slot pos & 3.
+__global__ __launch_bounds__(256) void k_ring_update(const uint16_t* raw, int pos0, int m, uint16_t* ring) {
+  const int i = blockIdx.x * 256 + threadIdx.x;
+  const int r = i / kConv, c = i % kConv;
+  const int t = m - 4 + r;
+  if (r >= 4 || t < 0) return;
+  ring[(size_t)((pos0 + t) & 3) * kConv + c] = raw[(size_t)t * kConv + c];
+}
+
+// GDN recurrence over the rows of a chunk (gdn_recur with rows > 1,
+// gdn.metal:176-228), the decode kernel's arithmetic and order per token:
+// block = (16 value rows, head), thread = (row, 8 keys), state in registers
+// for the whole chunk. Tokens go through LDS in tiles of 32.
+constexpr int kRecurTile = 32;
+__global__ __launch_bounds__(256) void k_gdn_recur_rows(const uint16_t* q, const uint16_t* k,
+                                                        const uint16_t* v, const float* g,
+                                                        const float* beta, int m, float* state,
+                                                        uint16_t* y) {
+  __shared__ float qs[kRecurTile][128], ks[kRecurTile][128], vs[kRecurTile][16], gs[kRecurTile][2];
+  const int t = threadIdx.x, h = blockIdx.y, r0 = blockIdx.x * 16;
+  const int row = r0 + (t >> 4), j = t & 15;
+  float* sp = state + ((size_t)(h * 128 + row)) * 128 + 8 * j;
+  const float4 s_lo = reinterpret_cast<const float4*>(sp)[0];
+  const float4 s_hi = reinterpret_cast<const float4*>(sp)[1];
+  float S[8] = {s_lo.x, s_lo.y, s_lo.z, s_lo.w, s_hi.x, s_hi.y, s_hi.z, s_hi.w};
+  for (int t0 = 0; t0 < m; t0 += kRecurTile) {
+    const int nt = min(kRecurTile, m - t0);
+    __syncthreads();
+    for (int i = t; i < nt * 128; i += 256) {
+      const int tt = i >> 7, c = i & 127;
+      const size_t o = ((size_t)(t0 + tt) * 16 + h) * 128 + c;
+      qs[tt][c] = bf2f(q[o]);
+      ks[tt][c] = bf2f(k[o]);
+    }
+    for (int i = t; i < nt * 16; i += 256) {
+      const int tt = i >> 4, rr = i & 15;
+      vs[tt][rr] = bf2f(v[((size_t)(t0 + tt) * 16 + h) * 128 + r0 + rr]);
+    }
+    if (t < nt) {
+      gs[t][0] = g[(size_t)(t0 + t) * 16 + h];
+      gs[t][1] = beta[(size_t)(t0 + t) * 16 + h];
+    }
+    __syncthreads();
+    for (int tt = 0; tt < nt; ++tt) {
+      const float gg = gs[tt][0], bb = gs[tt][1];
+      float kk[8], qq[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        kk[i] = ks[tt][8 * j + i];
+        qq[i] = qs[tt][8 * j + i];
+      }
+      float mem = 0.0f;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        S[i] = S[i] * gg;
+        mem = fmaf(S[i], kk[i], mem);
+      }
+      mem = tree16(mem);
+      const float delta = (vs[tt][t >> 4] - mem) * bb;
+      float out = 0.0f;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        S[i] = fmaf(kk[i], delta, S[i]);
+        out = fmaf(S[i], qq[i], out);
+      }
+      out = tree16(out);
+      if (j == 0) y[(size_t)(t0 + tt) * 2048 + h * 128 + row] = (uint16_t)f2bf(out);
+    }
+  }
+  reinterpret_cast<float4*>(sp)[0] = make_float4(S[0], S[1], S[2], S[3]);
+  reinterpret_cast<float4*>(sp)[1] = make_float4(S[4], S[5], S[6], S[7]);
+}
+
+// GDN gated norm rows (gdn_norm_gate, gdn.metal:230-255, the decode kernels'
+// arithmetic): 16 lanes per (row, head), 8 channels per lane: sum of squares
+// as an fma chain per lane then tree16; out = bf16(SiLU_fp32(z) *
+// bf16(bf16(y*inv)*w)). One block per row (16 heads).
+__global__ __launch_bounds__(256) void k_gdn_norm_gate_rows(const uint16_t* y, const uint16_t* z,
+                                                            const uint16_t* norm_w, int m, uint16_t* out) {
+  const int t = blockIdx.x, h = threadIdx.x >> 4, li = threadIdx.x & 15;
+  if (t >= m) return;
+  const size_t o = (size_t)t * 2048 + h * 128 + li * 8;
+  const uint4 yr = *reinterpret_cast<const uint4*>(y + o);
+  const uint4 zr = *reinterpret_cast<const uint4*>(z + o);
+  const uint4 wr = *reinterpret_cast<const uint4*>(norm_w + li * 8);
+  const uint32_t yw[4] = {yr.x, yr.y, yr.z, yr.w}, zw[4] = {zr.x, zr.y, zr.z, zr.w}, ww[4] = {wr.x, wr.y, wr.z, wr.w};
+  float yv[8], zv[8], wv[8];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    yv[2 * i] = bf_lo(yw[i]); yv[2 * i + 1] = bf_hi(yw[i]);
+    zv[2 * i] = bf_lo(zw[i]); zv[2 * i + 1] = bf_hi(zw[i]);
+    wv[2 * i] = bf_lo(ww[i]); wv[2 * i + 1] = bf_hi(ww[i]);
+  }
+  float ss = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) ss = fmaf(yv[i], yv[i], ss);
+  ss = tree16(ss);
+  const float ginv = 1.0f / sqrtf(ss / 128.0f + 1e-6f);
+  uint32_t res[4];
+#pragma unroll
+  for (int i = 0; i < 8; i += 2) {
+    float r2[2];
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const float norm = rbf(rbf(yv[i + u] * ginv) * wv[i + u]);
+      const float gz = zv[i + u];
+      const float sy = 1.0f / (1.0f + es_exp(fabsf(gz)));
+      const float sig = gz < 0.0f ? sy : 1.0f - sy;
+      r2[u] = rbf((gz * sig) * norm);
+    }
+    res[i / 2] = pack_bf2(r2[0], r2[1]);
+  }
+  *reinterpret_cast<uint4*>(out + o) = make_uint4(res[0], res[1], res[2], res[3]);
+}
+
+// Attention prepare rows (attn_prepare_q / attn_prepare_kv,
+// attention.metal:72-131, with the decode kernel's arithmetic): one wave per
+// (row, q head) for q, per (row, kv head) for k (RMSNorm, RoPE at position
+// pos0 + row) and v; k and v rows go to the cache. Block = one row, 12 waves.
+__global__ __launch_bounds__(768) void k_attn_prep_rows(const uint16_t* qg, const uint16_t* kp,
+                                                        const uint16_t* vp, const uint16_t* q_gain,
+                                                        const uint16_t* k_gain, const float* inv_freq,
+                                                        int pos0, int m, uint16_t* qr, uint16_t* kcache,
+                                                        uint16_t* vcache, int capacity) {
+  const int t = blockIdx.x, lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  if (t >= m) return;
+  const int pos = pos0 + t;
+  if (wave >= 10) {  // v rows of the two kv heads
+    const int kvh = wave - 10;
+    const uint2 xv = *reinterpret_cast<const uint2*>(vp + (size_t)t * 512 + kvh * 256 + lane * 4);
+    *reinterpret_cast<uint2*>(vcache + ((size_t)kvh * capacity + pos) * 256 + lane * 4) = xv;
+    return;
+  }
+  uint2 xv, gv;
+  if (wave < 8) {
+    xv = *reinterpret_cast<const uint2*>(qg + (size_t)t * 4096 + wave * 512 + lane * 4);
+    gv = *reinterpret_cast<const uint2*>(q_gain + lane * 4);
+  } else {
+    xv = *reinterpret_cast<const uint2*>(kp + (size_t)t * 512 + (wave - 8) * 256 + lane * 4);
+    gv = *reinterpret_cast<const uint2*>(k_gain + lane * 4);
+  }
+  float inv[4];
+#pragma unroll
+  for (int x = 0; x < 4; ++x) inv[x] = inv_freq[((lane * 4) & 31) + x];
+  float o4[4], p4[4], r[4];
+  head_norm4(xv, gv, o4);
+#pragma unroll
+  for (int x = 0; x < 4; ++x) p4[x] = dpp_row_ror8(o4[x]);
+#pragma unroll
+  for (int x = 0; x < 4; ++x) r[x] = rope_at(o4[x], p4[x], lane * 4 + x, pos, inv[x]);
+  const uint2 packed = make_uint2(pack_bf2(r[0], r[1]), pack_bf2(r[2], r[3]));
+  if (wave < 8)
+    *reinterpret_cast<uint2*>(qr + ((size_t)t * 8 + wave) * 256 + lane * 4) = packed;
+  else
+    *reinterpret_cast<uint2*>(kcache + ((size_t)(wave - 8) * capacity + pos) * 256 + lane * 4) = packed;
+}
+
+// Output gate rows (attn_gate, attention.metal:133-151): gated =
+// bf16(o * sigmoid_bf(gate)) with o the bf16 attention output and gate the
+// second half of each head's q_proj row.
+__global__ __launch_bounds__(256) void k_attn_gate_rows(const uint16_t* o, const uint16_t* qg, int m,
+                                                        uint16_t* gated) {
+  const int i = blockIdx.x * 256 + threadIdx.x;
+  if (i >= m * 2048) return;
+  const int t = i >> 11, hd = i & 2047, h = hd >> 8, d = hd & 255;
+  const float gate = sigmoid_bf(bf2f(qg[(size_t)t * 4096 + h * 512 + 256 + d]));
+  gated[i] = (uint16_t)f2bf(bf2f(o[i]) * gate);
+}
+
+// Causal GQA attention of m consecutive queries (positions pos0 .. pos0+m-1)
+// over the cache (attn_prefill, attention_prefill.metal:2256; model.rs:337-343):
+// o = bf16(softmax(q.K^T / 16) . V), fp32 softmax, MFMA products.
+// Block = (32 queries, KV head), wave w = query head 4*kvh + w. Per block of
+// 32 keys: S^T = K . Q^T (32x32x16 MFMA, K from LDS, the wave's Q fragments
+// held in registers), so lane l holds 16 scores of query l%32 (keys
+// 8(r/4) + 4(l/32) + r%4): the online-softmax max, sum and rescale are
+// per-lane values with one exchange between lanes l and l^32. The exp'ed
+// scores, rounded to bf16, are then directly the B operand of
+// O^T += V^T . P^T, with the MFMA's k index j of lane half h standing for key
+// (j < 4 ? 4h + j : 8 + 4h + j - 4) (+16 for the second step); V is staged
+// transposed in LDS and read in that key order. Exponentials are base 2 on
+// scores scaled by log2(e)/16.
+constexpr int kFaQ = 32, kFaKs = 264, kFaVs = 40;
+__global__ __launch_bounds__(256, 1) void k_attn_prefill(const uint16_t* qr, const uint16_t* kcache,
+                                                         const uint16_t* vcache, int pos0, int m,
+                                                         int capacity, uint16_t* o) {
+  __shared__ __attribute__((aligned(16))) uint16_t ks[2][32][kFaKs];
+  __shared__ __attribute__((aligned(16))) uint16_t vt[2][256][kFaVs];
+  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+  const int t0 = blockIdx.x * kFaQ, kvh = blockIdx.y, hq = 4 * kvh + wave;
+  const int ql = lane & 31, hh = lane >> 5;
+  const int qrow = t0 + ql;
+  const bool qvalid = qrow < m;
+  const int qpos = pos0 + (qvalid ? qrow : m - 1);
+  // Q fragments: B operand of step s holds Q[q][16s + 8hh .. +7]
+  bf16x8 qf[16];
+  {
+    const uint16_t* qp = qr + ((size_t)(qvalid ? qrow : 0) * 8 + hq) * 256 + 8 * hh;
+#pragma unroll
+    for (int s2 = 0; s2 < 16; ++s2) {
+      u32x4 v = *reinterpret_cast<const u32x4*>(qp + 16 * s2);
+      if (!qvalid) v = u32x4{0u, 0u, 0u, 0u};
+      qf[s2] = __builtin_bit_cast(bf16x8, v);
+    }
+  }
+  f32x16 ot[8];
+#pragma unroll
+  for (int dt = 0; dt < 8; ++dt)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) ot[dt][r] = 0.0f;
+  float mrun = -INFINITY, lrun = 0.0f;
+  const float c = 0.0625f * 1.4426950408889634f;  // 1/16 * log2(e)
+
+  // staging roles: key t/8, 32 dims (t%8)
+  const int sk = t >> 3, sd = (t & 7) * 32;
+  const int last_key = pos0 + min(t0 + kFaQ, m) - 1;
+  const int nkb = last_key / 32 + 1;
+  u32x4 kreg[4], vreg[4];
+  auto gload = [&](int kb) {
+    const int key = kb * 32 + sk;
+    const bool ok = key < capacity;
+    const size_t off = ((size_t)kvh * capacity + (ok ? key : 0)) * 256 + sd;
+    const u32x4* kp = reinterpret_cast<const u32x4*>(kcache + off);
+    const u32x4* vp = reinterpret_cast<const u32x4*>(vcache + off);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      kreg[i] = ok ? kp[i] : u32x4{0u, 0u, 0u, 0u};
+      vreg[i] = ok ? vp[i] : u32x4{0u, 0u, 0u, 0u};
+    }
+  };
+  auto lstore = [&](int buf) {
+    u32x4* kd = reinterpret_cast<u32x4*>(&ks[buf][sk][sd]);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) kd[i] = kreg[i];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int w2 = 0; w2 < 4; ++w2) {
+        const uint32_t u = vreg[i][w2];
+        vt[buf][sd + 8 * i + 2 * w2][sk] = (uint16_t)(u & 0xffffu);
+        vt[buf][sd + 8 * i + 2 * w2 + 1][sk] = (uint16_t)(u >> 16);
+      }
+  };
+  gload(0);
+  lstore(0);
+  __syncthreads();
+  for (int kb = 0; kb < nkb; ++kb) {
+    const int buf = kb & 1;
+    if (kb + 1 < nkb) gload(kb + 1);
+    // scores S^T[key][q] for the 32 keys of this block
+    f32x16 st;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) st[r] = 0.0f;
+#pragma unroll
+    for (int s2 = 0; s2 < 16; ++s2) {
+      const bf16x8 kf = *reinterpret_cast<const bf16x8*>(&ks[buf][ql][16 * s2 + 8 * hh]);
+      st = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf[s2], st, 0, 0, 0);
+    }
+    // scale, causal mask, online softmax for query ql
+    float x[16];
+    float mloc = -INFINITY;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int key = kb * 32 + 8 * (r >> 2) + 4 * hh + (r & 3);
+      x[r] = key <= qpos ? st[r] * c : -INFINITY;
+      mloc = fmaxf(mloc, x[r]);
+    }
+    const float2 mp = rows_xor32(mloc);
+    const float mnew = fmaxf(mrun, fmaxf(mp.x, mp.y));
+    const float factor = exp2f(mrun - mnew);
+    float psum = 0.0f;
+    float pv[16];
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      pv[r] = exp2f(x[r] - mnew);
+      psum += pv[r];
+    }
+    const float2 sp = rows_xor32(psum);
+    lrun = lrun * factor + (sp.x + sp.y);
+    mrun = mnew;
+#pragma unroll
+    for (int dt = 0; dt < 8; ++dt)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) ot[dt][r] *= factor;
+    // O^T += V^T . P^T, two 16-key steps
+#pragma unroll
+    for (int ks2 = 0; ks2 < 2; ++ks2) {
+      const u32x4 pb = u32x4{pack2(pv[8 * ks2 + 0], pv[8 * ks2 + 1]), pack2(pv[8 * ks2 + 2], pv[8 * ks2 + 3]),
+                             pack2(pv[8 * ks2 + 4], pv[8 * ks2 + 5]), pack2(pv[8 * ks2 + 6], pv[8 * ks2 + 7])};
+      const bf16x8 pf = __builtin_bit_cast(bf16x8, pb);
+#pragma unroll
+      for (int dt = 0; dt < 8; ++dt) {
+        const uint16_t* vrow = &vt[buf][32 * dt + ql][16 * ks2 + 4 * hh];
+        const uint2 lo = *reinterpret_cast<const uint2*>(vrow);
+        const uint2 hi = *reinterpret_cast<const uint2*>(vrow + 8);
+        const bf16x8 vf = __builtin_bit_cast(bf16x8, u32x4{lo.x, lo.y, hi.x, hi.y});
+        ot[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf, pf, ot[dt], 0, 0, 0);
+      }
+    }
+    if (kb + 1 < nkb) {
+      __syncthreads();  // every wave is done with buffer buf ^ 1 (previous block)
+      lstore(buf ^ 1);
+    }
+    __syncthreads();
+  }
+  if (!qvalid) return;
+  const float inv = 1.0f / lrun;
+  uint16_t* op = o + ((size_t)qrow * 8 + hq) * 256;
+#pragma unroll
+  for (int dt = 0; dt < 8; ++dt)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) op[32 * dt + 8 * (r >> 2) + 4 * hh + (r & 3)] = (uint16_t)f2bf(ot[dt][r] * inv);
+}
+
 }  // namespace
 
 hipError_t launch_q4_gemm(const Q4& w, const uint16_t* x, int m, const uint16_t* residual, uint16_t* y,
@@ -142,6 +551,79 @@ hipError_t launch_q4_gemm(const Q4& w, const uint16_t* x, int m, const uint16_t*
     return hipErrorInvalidValue;
   const dim3 grid((w.n + kGemmBN - 1) / kGemmBN, (m + kGemmBM - 1) / kGemmBM);
   hipLaunchKernelGGL(k_q4_gemm, grid, dim3(256), 0, s, w, x, m, residual, y);
+  return hipGetLastError();
+}
+
+}  // namespace es
+
+namespace es {
+
+hipError_t launch_embed_rows(const Q4& e, const uint32_t* tokens, int m, uint16_t* h, hipStream_t s) {
+  if (!e.w || m < 1 || !tokens || !h || e.k != 1024) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(k_embed_rows, dim3((m + 7) / 8), dim3(256), 0, s, e, tokens, m, h);
+  return hipGetLastError();
+}
+
+hipError_t launch_rmsnorm_rows(const uint16_t* x, const uint16_t* gain, int m, uint16_t* out, hipStream_t s) {
+  if (!x || !gain || !out || m < 1) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(k_rmsnorm_rows, dim3((m + 7) / 8), dim3(256), 0, s, x, gain, m, out);
+  return hipGetLastError();
+}
+
+hipError_t launch_swiglu_rows(const uint16_t* gate, const uint16_t* up, int count, uint16_t* act,
+                              hipStream_t s) {
+  if (!gate || !up || !act || count < 1) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(k_swiglu_rows, dim3((count + 255) / 256), dim3(256), 0, s, gate, up, count, act);
+  return hipGetLastError();
+}
+
+hipError_t launch_gdn_prep_rows(const GdnPrepRowsArgs& a, hipStream_t s) {
+  if (!a.raw || !a.ring || !a.conv_w || !a.a_proj || !a.b_proj || !a.a_log || !a.dt_bias || a.m < 1 ||
+      a.pos0 < 0 || !a.q || !a.k || !a.v || !a.g || !a.beta)
+    return hipErrorInvalidValue;
+  hipLaunchKernelGGL(k_gdn_prep_rows, dim3(a.m, 4), dim3(256), 0, s, a.raw, a.ring, a.conv_w, a.a_proj,
+                     a.b_proj, a.a_log, a.dt_bias, a.pos0, a.m, a.q, a.k, a.v, a.g, a.beta);
+  if (hipGetLastError() != hipSuccess) return hipErrorLaunchFailure;
+  hipLaunchKernelGGL(k_ring_update, dim3((4 * kConv + 255) / 256), dim3(256), 0, s, a.raw, a.pos0, a.m,
+                     a.ring);
+  return hipGetLastError();
+}
+
+hipError_t launch_gdn_recur_rows(const uint16_t* q, const uint16_t* k, const uint16_t* v, const float* g,
+                                 const float* beta, int m, float* state, uint16_t* y, hipStream_t s) {
+  if (!q || !k || !v || !g || !beta || !state || !y || m < 1) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(k_gdn_recur_rows, dim3(8, kGdnHeads), dim3(256), 0, s, q, k, v, g, beta, m, state, y);
+  return hipGetLastError();
+}
+
+hipError_t launch_gdn_norm_gate_rows(const uint16_t* y, const uint16_t* z, const uint16_t* norm_w, int m,
+                                     uint16_t* out, hipStream_t s) {
+  if (!y || !z || !norm_w || !out || m < 1) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(k_gdn_norm_gate_rows, dim3(m), dim3(256), 0, s, y, z, norm_w, m, out);
+  return hipGetLastError();
+}
+
+hipError_t launch_attn_prep_rows(const AttnPrepRowsArgs& a, hipStream_t s) {
+  if (!a.qg || !a.k || !a.v || !a.q_gain || !a.k_gain || !a.inv_freq || a.m < 1 || a.pos0 < 0 ||
+      a.pos0 + a.m > a.capacity || !a.qr || !a.kcache || !a.vcache)
+    return hipErrorInvalidValue;
+  hipLaunchKernelGGL(k_attn_prep_rows, dim3(a.m), dim3(768), 0, s, a.qg, a.k, a.v, a.q_gain, a.k_gain,
+                     a.inv_freq, a.pos0, a.m, a.qr, a.kcache, a.vcache, a.capacity);
+  return hipGetLastError();
+}
+
+hipError_t launch_attn_prefill(const uint16_t* qr, const uint16_t* kcache, const uint16_t* vcache, int pos0,
+                               int m, int capacity, uint16_t* o, hipStream_t s) {
+  if (!qr || !kcache || !vcache || !o || m < 1 || pos0 < 0 || pos0 + m > capacity) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(k_attn_prefill, dim3((m + kFaQ - 1) / kFaQ, kKvHeads), dim3(256), 0, s, qr, kcache, vcache,
+                     pos0, m, capacity, o);
+  return hipGetLastError();
+}
+
+hipError_t launch_attn_gate_rows(const uint16_t* o, const uint16_t* qg, int m, uint16_t* gated,
+                                 hipStream_t s) {
+  if (!o || !qg || !gated || m < 1) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(k_attn_gate_rows, dim3((m * 2048 + 255) / 256), dim3(256), 0, s, o, qg, m, gated);
   return hipGetLastError();
 }
 

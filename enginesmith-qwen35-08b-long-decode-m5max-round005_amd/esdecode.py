@@ -74,6 +74,15 @@ _SIGNATURES = {
                                        POINTER(c_int)]),
     "es_weights_random": (c_int, [c_int, c_int, c_uint64, c_void_p, c_size_t, c_int]),
     "es_q4_gemm": (c_int, [POINTER(Q4), c_void_p, c_int, c_void_p, c_void_p, c_void_p]),
+    "es_embed_rows": (c_int, [POINTER(Q4), c_void_p, c_int, c_void_p, c_void_p]),
+    "es_rmsnorm_rows": (c_int, [c_void_p, c_void_p, c_int, c_void_p, c_void_p]),
+    "es_swiglu_rows": (c_int, [c_void_p, c_void_p, c_int, c_void_p, c_void_p]),
+    "es_gdn_prepare_rows": (c_int, [c_void_p] * 7 + [c_int, c_int] + [c_void_p] * 6),
+    "es_gdn_recur_rows": (c_int, [c_void_p] * 5 + [c_int, c_void_p, c_void_p, c_void_p]),
+    "es_gdn_norm_gate_rows": (c_int, [c_void_p, c_void_p, c_void_p, c_int, c_void_p, c_void_p]),
+    "es_attn_prepare_rows": (c_int, [c_void_p] * 6 + [c_int, c_int, c_void_p, c_void_p, c_void_p, c_int, c_void_p]),
+    "es_attn_prefill": (c_int, [c_void_p, c_void_p, c_void_p, c_int, c_int, c_int, c_void_p, c_void_p]),
+    "es_attn_gate_rows": (c_int, [c_void_p, c_void_p, c_int, c_void_p, c_void_p]),
     "es_weights_tensor_shape": (c_int, [c_int, c_int, c_int, POINTER(ctypes.c_int64), c_int]),
     "es_checkpoint_config": (c_int, [c_char_p, POINTER(c_int), POINTER(c_int)]),
     "es_checkpoint_load": (c_int, [c_char_p, c_int, c_int, c_void_p, c_size_t]),

@@ -96,6 +96,64 @@ int es_q4_matvec_add(const es_q4* w, const uint16_t* x, const uint16_t* residual
 int es_q4_gemm(const es_q4* w, const uint16_t* x, int rows, const uint16_t* residual, uint16_t* y,
                void* stream);
 
+/* ------------------------------------------------------------------ */
+/* Prefill row operators (encode_forward with rows > 1, model.rs:228-343) */
+/* ------------------------------------------------------------------ */
+/* Each reproduces its decode counterpart's arithmetic row by row; rows are
+ * consecutive tokens at positions position .. position+rows-1. */
+
+/* embedding_q4 (linear.metal:11-24): h [rows, 1024] = bf16(scale*q + bias) of
+ * each token's table row. Tokens outside the table read row 0. */
+int es_embed_rows(const es_q4* embed, const uint32_t* tokens, int rows, uint16_t* h, void* stream);
+
+/* rms_norm_bf16 (linear.metal:300-333, eps 1e-6): out [rows, 1024]. */
+int es_rmsnorm_rows(const uint16_t* x, const uint16_t* gain, int rows, uint16_t* out, void* stream);
+
+/* swiglu_bf16 (linear.metal:382-398) over `count` elements:
+ * act = bf16(bf16(gate*sigmoid(gate)) * up). */
+int es_swiglu_rows(const uint16_t* gate, const uint16_t* up, int count, uint16_t* act, void* stream);
+
+/* gdn_conv + gdn_history + gdn_prepare (gdn.metal:33-120): raw [rows, 6144]
+ * projected q|k|v; ring [4, 6144] holds the raw rows of earlier positions in
+ * slot (position & 3) and receives the chunk's last min(rows, 4) rows;
+ * a_proj, b_proj [rows, 16]. Outputs q, k [rows, 16, 128] (L2-normalised and
+ * scaled), v [rows, 16, 128] (SiLU of the convolution), g, beta [rows, 16]
+ * fp32. */
+int es_gdn_prepare_rows(const uint16_t* raw, uint16_t* ring, const uint16_t* conv_w, const uint16_t* a_proj,
+                        const uint16_t* b_proj, const float* a_log, const uint16_t* dt_bias, int position,
+                        int rows, uint16_t* q, uint16_t* k, uint16_t* v, float* g, float* beta,
+                        void* stream);
+
+/* gdn_recur with rows > 1 (gdn.metal:176-228): the delta-rule update of state
+ * [16, 128v, 128k] fp32 (in place) for each row in order; y [rows, 2048]. */
+int es_gdn_recur_rows(const uint16_t* q, const uint16_t* k, const uint16_t* v, const float* g, const float* beta,
+                      int rows, float* state, uint16_t* y, void* stream);
+
+/* gdn_norm_gate (gdn.metal:230-255): out [rows, 2048] =
+ * bf16(SiLU(z) * bf16(bf16(y * rsqrt(mean(y^2) + 1e-6)) * norm_w)) per head. */
+int es_gdn_norm_gate_rows(const uint16_t* y, const uint16_t* z, const uint16_t* norm_w, int rows, uint16_t* out,
+                          void* stream);
+
+/* attn_prepare_q + attn_prepare_kv (attention.metal:72-131): per row, query
+ * [rows, 8, 256] = RoPE(RMSNorm(q head) * q_gain) at its position; K row =
+ * RoPE(RMSNorm(k head) * k_gain) and V row written to kcache/vcache
+ * [2, capacity, 256] at that position. q_proj [rows, 8, 512] (query|gate). */
+int es_attn_prepare_rows(const uint16_t* q_proj, const uint16_t* k_proj, const uint16_t* v_proj,
+                         const uint16_t* q_gain, const uint16_t* k_gain, const float* inv_freq, int position,
+                         int rows, uint16_t* query, uint16_t* kcache, uint16_t* vcache, int capacity,
+                         void* stream);
+
+/* attn_prefill (attention_prefill.metal:2256; model.rs:337-343): causal GQA
+ * attention, row r attends to cache positions 0 .. position+r; out
+ * [rows, 8, 256] = bf16(softmax(q.K^T / 16) V), fp32 softmax, products on
+ * bf16 operands (the probabilities rounded to bf16) with fp32 accumulation. */
+int es_attn_prefill(const uint16_t* query, const uint16_t* kcache, const uint16_t* vcache, int position, int rows,
+                    int capacity, uint16_t* out, void* stream);
+
+/* attn_gate (attention.metal:133-151): gated [rows, 2048] =
+ * bf16(o * sigmoid(gate)), gate the second half of each q_proj head. */
+int es_attn_gate_rows(const uint16_t* o, const uint16_t* q_proj, int rows, uint16_t* gated, void* stream);
+
 /* qmv_multi_g8_norm (linear_input_norm.metal:13-119) with the rms_norm_bf16
  * arithmetic (linear.metal:300-331): u = bf16(bf16(x*rsqrt(mean(x^2)+1e-6))*gain)
  * over 1024 columns, then y[i] = bf16(W_i u) for count (1..4) matrices of
