@@ -439,6 +439,12 @@ int es_engine_generate(es_engine* e, const uint32_t* prompt, int len, int max_to
   return engine_rc(e->impl->generate(prompt, len, max_tokens, reset != 0, out, &err), err);
 }
 
+int es_engine_set_prefill(es_engine* e, int chunk_rows) {
+  if (!e) return fail(ES_ERR_INVALID, "null engine");
+  std::string err;
+  return engine_rc(e->impl->set_prefill(chunk_rows, &err), err);
+}
+
 void es_engine_cancel(es_engine* e) {
   if (e) e->impl->cancel();
 }

@@ -406,16 +406,14 @@ int Engine::generate(const uint32_t* prompt, int len, int count, bool reset, uin
     reset_state();
     ES_HIP(hipMemcpyAsync(prompt_, prompt, (size_t)len * 4, hipMemcpyHostToDevice, stream_),
            "prompt upload");
-    if (int rc = upload_state(0, 0, prompt[0], err)) return rc;
-    if (len > 1) {
-      if (int rc = run_steps(kKindPrompt, 0, len - 1, nullptr, nullptr, err)) {
-        reset_state();
-        return rc;
-      }
+    if (int rc = consume_prompt(prompt, len - 1, err)) {
+      reset_state();
+      return rc;
     }
     position_ = len - 1;
     first = position_;
-    // token for the first decode step is prompt[len-1], already in the state
+    // the first decode step consumes prompt[len-1]
+    if (int rc = upload_state(position_, 0, prompt[len - 1], err)) return rc;
   } else {
     if (len != 0) {
       if (err) *err = "continuation prompt must be empty";
@@ -440,6 +438,126 @@ int Engine::generate(const uint32_t* prompt, int len, int count, bool reset, uin
   position_ = first + count;
   pending_ = out[count - 1];
   has_pending_ = true;
+  return 0;
+}
+
+int Engine::set_prefill(int chunk_rows, std::string* err) {
+  if (chunk_rows < 0 || chunk_rows == 1 || chunk_rows > (1 << 20)) {
+    if (err) *err = "prefill chunk rows must be 0 or 2 .. 2^20";
+    return 1;
+  }
+  prefill_rows_ = chunk_rows;
+  return 0;
+}
+
+int Engine::ensure_prefill_buffers(std::string* err) {
+  const int rows = std::min(prefill_rows_, capacity_);
+  if (prefill_alloc_rows_ >= rows) return 0;
+  // buffers are kept until the engine is destroyed; a larger chunk size adds a
+  // second, larger set
+  const size_t r = (size_t)rows;
+  auto alloc = [&](size_t n) -> void* {
+    void* p = nullptr;
+    if (hipMalloc(&p, std::max<size_t>(n, 256)) != hipSuccess) return nullptr;
+    allocations_.push_back(p);
+    return p;
+  };
+  PrefillBuffers b{};
+  uint16_t** bf[] = {&b.h, &b.u, &b.raw, &b.z, &b.a, &b.b, &b.q, &b.k, &b.v, &b.y, &b.gated, &b.qp, &b.kp,
+                     &b.vp, &b.query, &b.o, &b.gate, &b.up, &b.act};
+  const size_t width[] = {1024, 1024, 6144, 2048, 16, 16, 2048, 2048, 2048, 2048, 2048, 4096, 512,
+                          512, 2048, 2048, 3584, 3584, 3584};
+  for (size_t i = 0; i < sizeof(width) / sizeof(width[0]); ++i) {
+    *bf[i] = static_cast<uint16_t*>(alloc(r * width[i] * 2));
+    if (!*bf[i]) {
+      if (err) *err = "device allocation of prefill buffers failed";
+      return 2;
+    }
+  }
+  b.g = static_cast<float*>(alloc(r * 16 * 4));
+  b.beta = static_cast<float*>(alloc(r * 16 * 4));
+  if (!b.g || !b.beta) {
+    if (err) *err = "device allocation of prefill buffers failed";
+    return 2;
+  }
+  pf_ = b;
+  prefill_alloc_rows_ = rows;
+  return 0;
+}
+
+// encode_forward with rows > 1 and no output (model.rs:228-343): embedding
+// rows; per layer input RMSNorm rows, the layer's row-batched Q4 linears,
+// the mixer (GDN: conv/prepare + ring, recurrence over the rows in order,
+// gated norm; attention: q/k norm + RoPE with the K/V rows written to the
+// cache, causal flash attention, output gate), the output linear with the
+// residual add, post RMSNorm rows, gate/up linears, SwiGLU, down linear with
+// the residual add.
+int Engine::prefill_rows(int pos0, int m, std::string* err) {
+  const PrefillBuffers& b = pf_;
+  hipStream_t s = stream_;
+  ES_HIP(launch_embed_rows(embed_, prompt_ + pos0, m, b.h, s), "prefill embedding");
+  for (int l = 0; l < shape_.n_layers; ++l) {
+    const LayerDev& L = layers_[l];
+    ES_HIP(launch_rmsnorm_rows(b.h, L.input_norm, m, b.u, s), "prefill input norm");
+    if (!L.attention) {
+      ES_HIP(launch_q4_gemm(L.qkv, b.u, m, nullptr, b.raw, s), "prefill qkv");
+      ES_HIP(launch_q4_gemm(L.z, b.u, m, nullptr, b.z, s), "prefill z");
+      ES_HIP(launch_q4_gemm(L.a, b.u, m, nullptr, b.a, s), "prefill a");
+      ES_HIP(launch_q4_gemm(L.b, b.u, m, nullptr, b.b, s), "prefill b");
+      GdnPrepRowsArgs g{b.raw, L.ring, L.conv_w, b.a, b.b, L.a_log, L.dt_bias, pos0, m,
+                        b.q, b.k, b.v, b.g, b.beta};
+      ES_HIP(launch_gdn_prep_rows(g, s), "prefill gdn prepare");
+      ES_HIP(launch_gdn_recur_rows(b.q, b.k, b.v, b.g, b.beta, m, L.state, b.y, s), "prefill gdn recurrence");
+      ES_HIP(launch_gdn_norm_gate_rows(b.y, b.z, L.gdn_norm, m, b.gated, s), "prefill gdn norm gate");
+      ES_HIP(launch_q4_gemm(L.out, b.gated, m, b.h, b.h, s), "prefill out_proj");
+    } else {
+      ES_HIP(launch_q4_gemm(L.q, b.u, m, nullptr, b.qp, s), "prefill q");
+      ES_HIP(launch_q4_gemm(L.k, b.u, m, nullptr, b.kp, s), "prefill k");
+      ES_HIP(launch_q4_gemm(L.v, b.u, m, nullptr, b.vp, s), "prefill v");
+      AttnPrepRowsArgs a{b.qp, b.kp, b.vp, L.q_norm, L.k_norm, inv_freq_, pos0, m,
+                         b.query, L.kcache, L.vcache, capacity_};
+      ES_HIP(launch_attn_prep_rows(a, s), "prefill attention prepare");
+      ES_HIP(launch_attn_prefill(b.query, L.kcache, L.vcache, pos0, m, capacity_, b.o, s), "prefill attention");
+      ES_HIP(launch_attn_gate_rows(b.o, b.qp, m, b.gated, s), "prefill attention gate");
+      ES_HIP(launch_q4_gemm(L.o, b.gated, m, b.h, b.h, s), "prefill o_proj");
+    }
+    ES_HIP(launch_rmsnorm_rows(b.h, L.post_norm, m, b.u, s), "prefill post norm");
+    ES_HIP(launch_q4_gemm(L.gate, b.u, m, nullptr, b.gate, s), "prefill gate");
+    ES_HIP(launch_q4_gemm(L.up, b.u, m, nullptr, b.up, s), "prefill up");
+    ES_HIP(launch_swiglu_rows(b.gate, b.up, m * 3584, b.act, s), "prefill swiglu");
+    ES_HIP(launch_q4_gemm(L.down, b.act, m, b.h, b.h, s), "prefill down");
+  }
+  return 0;
+}
+
+// The prompt loop of Model::generate (model.rs:106-109): chunks of at most
+// prefill_rows_ rows until n tokens are consumed, a cancellation check before
+// each chunk (forward, model.rs:182).
+int Engine::consume_prompt(const uint32_t* prompt, int n, std::string* err) {
+  if (n <= 0) return 0;
+  if (prefill_rows_ == 0) {
+    // each prompt step advances the step state to the next prompt token
+    if (int rc = upload_state(0, 0, prompt[0], err)) return rc;
+    return run_steps(kKindPrompt, 0, n, nullptr, nullptr, err);
+  }
+  if (int rc = ensure_prefill_buffers(err)) return rc;
+  int pos = 0;
+  while (pos < n) {
+    if (cancelled_.load()) {
+      (void)hipStreamSynchronize(stream_);
+      if (err) *err = "input disconnected";
+      return 3;
+    }
+    const int m = std::min(prefill_alloc_rows_, n - pos);
+    if (m == 1) {
+      if (int rc = upload_state(pos, 0, prompt[pos], err)) return rc;
+      if (int rc = run_steps(kKindPrompt, pos, 1, nullptr, nullptr, err)) return rc;
+    } else if (int rc = prefill_rows(pos, m, err)) {
+      return rc;
+    }
+    pos += m;
+  }
+  ES_HIP(hipStreamSynchronize(stream_), "prefill sync");
   return 0;
 }
 

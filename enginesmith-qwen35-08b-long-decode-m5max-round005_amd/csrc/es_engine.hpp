@@ -52,6 +52,12 @@ class Engine {
   // greedy pick after it. logits_out (optional, host) receives [n, vocab] bf16.
   int forced_decode(const uint32_t* tokens, int n, uint32_t* argmax_out, uint16_t* logits_out,
                     std::string* err);
+  // Prompt consumption (model.rs:106-109): chunk_rows >= 2 consumes the
+  // prompt in batched chunks of at most chunk_rows rows (a chunk of one row
+  // runs the decode kernels, as forward(rows = 1) does); 0 replays one decode
+  // step per prompt token. Results do not depend on the chunk size.
+  int set_prefill(int chunk_rows, std::string* err);
+  int prefill_chunk_rows() const { return prefill_rows_; }
   void cancel() { cancelled_.store(true); }
   void clear_cancel() { cancelled_.store(false); }
   int position() const { return position_; }
@@ -94,6 +100,13 @@ class Engine {
   int run_steps(int kind, int first_pos, int count, const uint32_t* forced_dev,
                 uint16_t* logits_out, std::string* err);
   int upload_state(int pos, int step, uint32_t token, std::string* err);
+  // Batched forward over prompt_[pos0 .. pos0+m) without output (encode_forward
+  // with rows > 1, model.rs:228-343); m <= prefill_rows_.
+  int prefill_rows(int pos0, int m, std::string* err);
+  int ensure_prefill_buffers(std::string* err);
+  // Consume the first n prompt tokens (host copy `prompt`, device copy
+  // prompt_) in chunks or steps; the state then stands at position n.
+  int consume_prompt(const uint32_t* prompt, int n, std::string* err);
   AttnArgs attn_args(const LayerDev& L, int splits);
   hipError_t launch_attention_part(const AttnArgs& a, int which);
 
@@ -125,6 +138,15 @@ class Engine {
   uint32_t* prompt_ = nullptr;  // [capacity]
   uint32_t* out_ = nullptr;     // [capacity]
   uint32_t* forced_ = nullptr;  // [capacity]
+
+  // batched prefill buffers, rows = prefill_rows_ (allocated on first use)
+  static constexpr int kDefaultPrefillRows = 8192;
+  int prefill_rows_ = kDefaultPrefillRows;
+  int prefill_alloc_rows_ = 0;
+  struct PrefillBuffers {
+    uint16_t *h, *u, *raw, *z, *a, *b, *q, *k, *v, *y, *gated, *qp, *kp, *vp, *query, *o, *gate, *up, *act;
+    float *g, *beta;
+  } pf_{};
 
   struct GraphEntry {
     int kind;

@@ -89,6 +89,7 @@ _SIGNATURES = {
     "es_engine_create": (c_void_p, [c_void_p, c_size_t, c_int, c_int, c_int]),
     "es_engine_destroy": (None, [c_void_p]),
     "es_engine_generate": (c_int, [c_void_p, c_void_p, c_int, c_int, c_int, c_void_p]),
+    "es_engine_set_prefill": (c_int, [c_void_p, c_int]),
     "es_engine_cancel": (None, [c_void_p]),
     "es_engine_clear_cancel": (None, [c_void_p]),
     "es_engine_position": (c_int, [c_void_p]),
@@ -309,6 +310,11 @@ class Engine:
         check(lib().es_engine_generate(self.h, _ptr(p) if p.size else None, int(p.size), int(max_tokens),
                                        1 if reset else 0, _ptr(out)))
         return out[:max_tokens].tolist()
+
+    def set_prefill(self, chunk_rows: int) -> None:
+        """Prompt consumption: batched chunks of at most chunk_rows rows (>= 2),
+        or 0 for one decode step per prompt token."""
+        check(lib().es_engine_set_prefill(self.h, int(chunk_rows)))
 
     def cancel(self):
         lib().es_engine_cancel(self.h)

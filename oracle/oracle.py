@@ -171,6 +171,31 @@ def q4_gemm(codes, scales, biases, x, residual=None):
     return y
 
 
+def attn_prefill(query, kcache, vcache, position, rows):
+    """Causal GQA attention of a chunk (attn_prefill, attention_prefill.metal:
+    2256; model.rs:337-343): row r (position position+r) attends to cache rows
+    0..position+r of KV head h//4 with scale 1/16; the softmax is taken in
+    fp64 and its probabilities rounded to bf16 before the product with V (the
+    kernel's second product takes bf16 operands), normalised by the sum of the
+    unrounded probabilities; output rounded to bf16. query [rows, 2048] bf16
+    bits, caches [2, capacity, 256]; returns [rows, 2048] bf16 bits. The
+    kernel keeps a running maximum per block of keys, so its probabilities
+    carry different rounding: results agree to a stated tolerance."""
+    qf = bf16_to_f32(np.asarray(query, dtype=np.uint16)).astype(np.float64).reshape(rows, 8, 256)
+    out = np.empty((rows, 8, 256), dtype=np.float64)
+    for kvh in range(2):
+        n_all = position + rows
+        K = bf16_to_f32(kcache[kvh, :n_all]).astype(np.float64)
+        V = bf16_to_f32(vcache[kvh, :n_all]).astype(np.float64)
+        s = np.einsum("rhd,nd->rhn", qf[:, 4 * kvh:4 * kvh + 4], K) / 16.0
+        mask = np.arange(n_all)[None, :] > (position + np.arange(rows))[:, None]
+        s[np.broadcast_to(mask[:, None, :], s.shape)] = -np.inf
+        p = np.exp(s - s.max(axis=-1, keepdims=True))
+        pb = bf16_to_f32(f32_to_bf16(p.astype(np.float32))).astype(np.float64)
+        out[:, 4 * kvh:4 * kvh + 4] = (pb @ V) / p.sum(axis=-1, keepdims=True)
+    return f32_to_bf16(out.astype(np.float32).reshape(rows, 2048))
+
+
 def q4_matvec_add(codes, scales, biases, x, residual):
     n, k8 = codes.shape
     y = np.empty(n, dtype=np.uint16)
@@ -361,6 +386,61 @@ class OracleModel:
             tok = self.step(tok)
             out.append(tok)
         return out
+
+    def _q4(self, name, n, k):
+        v = self.views
+        return (v[name + ".weight"].reshape(n, k // 8), v[name + ".scales"].reshape(n, k // 64),
+                v[name + ".biases"].reshape(n, k // 64))
+
+    def prefill(self, tokens):
+        """Reference forward over a chunk of rows > 1 prompt tokens from the
+        current position, no output (model.rs:181-188 and encode_forward
+        rows != 1, model.rs:228-343): embedding rows; per layer RMSNorm rows,
+        the row-batched linears (q4_gemm), GDN conv/prepare/recurrence/gated
+        norm token by token or attention prepare/attn_prefill/gate, the
+        residual add bf16(h + bf16(out)) fused into the output linear as
+        add_bf16 follows it, post-norm, gate/up linears, SwiGLU, down linear
+        with its residual. Updates histories, states, caches and position."""
+        v = self.views
+        m = len(tokens)
+        pos0 = self.position
+        emb = self._q4("embed_tokens", self.vocab, 1024)
+        h = np.stack([embedding(*emb, int(t)) for t in tokens])
+        for l in range(self.n_layers):
+            p = f"layers.{l}"
+            gain = v[p + ".input_layernorm.weight"]
+            u = np.stack([rms_norm(h[i], gain) for i in range(m)])
+            if l % 4 != 3:
+                g = p + ".linear_attn"
+                raw = q4_gemm(*self._q4(g + ".in_proj_qkv", 6144, 1024), u)
+                z = q4_gemm(*self._q4(g + ".in_proj_z", 2048, 1024), u)
+                a = q4_gemm(*self._q4(g + ".in_proj_a", 16, 1024), u)
+                b = q4_gemm(*self._q4(g + ".in_proj_b", 16, 1024), u)
+                gated = np.empty((m, 2048), dtype=np.uint16)
+                for t in range(m):
+                    conv, gg, beta = gdn_conv_prepare(raw[t], self.history[l], v[g + ".conv1d.weight"], a[t], b[t],
+                                                      v[g + ".A_log"], v[g + ".dt_bias"])
+                    y = gdn_recur(conv, gg, beta, self.state[l])
+                    gated[t] = gdn_norm_gate(y, z[t], v[g + ".norm.weight"])
+                h = q4_gemm(*self._q4(g + ".out_proj", 1024, 2048), gated, residual=h)
+            else:
+                a = p + ".self_attn"
+                qp = q4_gemm(*self._q4(a + ".q_proj", 4096, 1024), u)
+                kp = q4_gemm(*self._q4(a + ".k_proj", 512, 1024), u)
+                vp = q4_gemm(*self._q4(a + ".v_proj", 512, 1024), u)
+                query = np.stack([attn_prepare(qp[t], kp[t], vp[t], v[a + ".q_norm.weight"], v[a + ".k_norm.weight"],
+                                               self.kcache[l], self.vcache[l], pos0 + t, self.capacity)
+                                  for t in range(m)])
+                o = attn_prefill(query, self.kcache[l], self.vcache[l], pos0, m)
+                gated = np.stack([attn_gate(o[t], qp[t]) for t in range(m)])
+                h = q4_gemm(*self._q4(a + ".o_proj", 1024, 2048), gated, residual=h)
+            gain = v[p + ".post_attention_layernorm.weight"]
+            u = np.stack([rms_norm(h[i], gain) for i in range(m)])
+            act = swiglu(q4_gemm(*self._q4(p + ".mlp.gate_proj", 3584, 1024), u),
+                         q4_gemm(*self._q4(p + ".mlp.up_proj", 3584, 1024), u)).reshape(m, 3584)
+            h = q4_gemm(*self._q4(p + ".mlp.down_proj", 1024, 3584), act, residual=h)
+        self.position += m
+        return h
 
     def load_ring(self, layer: int, ring: np.ndarray, position: int):
         """Engine ring [4,6144] -> reference history [3,6144] at `position`."""

@@ -65,8 +65,7 @@ def test_forced_decode_logits_close(small):
     forced = [first[0]] + r.integers(0, SMALL["vocab"], 7).tolist()
     am, lg = eng.forced_decode(forced, want_logits=True)
     orc.reset()
-    for t in prompt[:-1]:
-        orc.step(t, want_head=False)
+    orc.prefill(prompt[:-1])  # the engine's default batched prompt forward
     orc.step(prompt[-1])
     from helpers import f32
     for i, t in enumerate(forced):
@@ -97,11 +96,19 @@ def test_graph_batches_equal_one_step_launches(small):
     eng, _, _ = small
     r = rng(46)
     prompt = r.integers(0, SMALL["vocab"], 40).tolist()  # 39 prompt steps: 2 batches of 16 + 7
-    gen = eng.generate(prompt, 37, reset=True)           # 2 batches of 16 + 5
+    eng.set_prefill(0)
+    try:
+        gen = eng.generate(prompt, 37, reset=True)       # 2 batches of 16 + 5
+    finally:
+        eng.set_prefill(8192)
     end = eng.position
     ring_a, state_a = eng.read_gdn(0)
     kv_a = eng.read_kv(3, 0, end - 40, 40)
-    first = eng.generate(prompt, 1, reset=True)
+    eng.set_prefill(0)
+    try:
+        first = eng.generate(prompt, 1, reset=True)
+    finally:
+        eng.set_prefill(8192)
     assert first[0] == gen[0]
     am = eng.forced_decode(gen[:-1])
     assert am.tolist() == gen[1:]
@@ -227,30 +234,43 @@ def test_protocol_server_serves_a_checkpoint_directory(tmp_path):
 CONTROL_LENGTHS = [1, 2, 15, 16, 17, 31, 32, 33, 63, 64, 65, 1023, 1024, 1025]
 
 
-def test_control_prompts_pass_the_harness_gates():
+@pytest.mark.parametrize("chunk_rows", [0, 8192])
+def test_control_prompts_pass_the_harness_gates(chunk_rows):
     """Short control prompts at the lengths where tiled and chunked kernels
     usually break (docs/protocol.md:64-65), here around the 16-step graphs,
     the 32-position tiles, the 64 chains and the 1024-position route switch:
     prefixes of one random prompt, each generated from a reset and judged
-    teacher-forced against the oracle with the harness's gates. The oracle
-    walks the prompt once and branches at each length (snapshot / restore)."""
+    teacher-forced against the oracle with the harness's gates. With the
+    prompt replayed step by step (chunk_rows 0) the oracle walks the prompt
+    once and branches at each length (snapshot / restore); with the batched
+    prompt forward the oracle runs its own batched forward over each prefix
+    (a one-token prefix is a decode step in both)."""
     from judge import gates, judge_from
     blob = E.random_weights(SMALL["n_layers"], SMALL["vocab"], seed=31)
     eng = E.Engine(blob, SMALL["n_layers"], SMALL["vocab"], capacity=1100)
+    eng.set_prefill(chunk_rows)
     orc = O.OracleModel(E.tensor_views(blob, **SMALL), SMALL["n_layers"], SMALL["vocab"], capacity=1100)
     prompt = rng(47).integers(0, SMALL["vocab"], max(CONTROL_LENGTHS)).tolist()
     cases = []
     try:
         orc.reset()
-        consumed = 0  # prompt tokens the oracle has consumed
+        consumed = 0  # prompt tokens the oracle has consumed (step replay)
         for n in CONTROL_LENGTHS:
             toks = eng.generate(prompt[:n], 8, reset=True)
-            while consumed < n - 1:
-                orc.step(prompt[consumed], want_head=False)
-                consumed += 1
-            snap = orc.snapshot()
-            m = judge_from(orc, prompt[n - 1], toks)
-            orc.restore(snap)
+            if chunk_rows == 0:
+                while consumed < n - 1:
+                    orc.step(prompt[consumed], want_head=False)
+                    consumed += 1
+                snap = orc.snapshot()
+                m = judge_from(orc, prompt[n - 1], toks)
+                orc.restore(snap)
+            else:
+                orc.reset()
+                if n - 1 == 1:
+                    orc.step(prompt[0], want_head=False)
+                elif n - 1 > 1:
+                    orc.prefill(prompt[:n - 1])
+                m = judge_from(orc, prompt[n - 1], toks)
             print(f"prompt {n}: {len(m)} mismatches {m}", flush=True)
             cases.append((len(toks), m))
     finally:

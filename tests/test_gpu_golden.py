@@ -77,6 +77,7 @@ def test_model_tokens_fixture():
     blob = E.random_weights(m["n_layers"], m["vocab"], m["seed"], threads=4)
     eng = E.Engine(blob, m["n_layers"], m["vocab"], capacity=64)
     try:
+        eng.set_prefill(0)  # the fixture is the token-by-token replay of the prompt
         got = eng.generate(m["prompt"], m["tokens"], reset=True)
     finally:
         eng.close()
