@@ -241,44 +241,99 @@ __global__ __launch_bounds__(256) void k_ring_update(const uint16_t* raw, int po
 // GDN recurrence over the rows of a chunk (gdn_recur with rows > 1,
 // gdn.metal:176-228), the decode kernel's arithmetic and order per token:
 // block = (16 value rows, head), thread = (row, 8 keys), state in registers
-// for the whole chunk. Tokens go through LDS in tiles of 32.
-constexpr int kRecurTile = 32;
-__global__ __launch_bounds__(256) void k_gdn_recur_rows(const uint16_t* q, const uint16_t* k,
-                                                        const uint16_t* v, const float* g,
-                                                        const float* beta, int m, float* state,
-                                                        uint16_t* y) {
-  __shared__ float qs[kRecurTile][128], ks[kRecurTile][128], vs[kRecurTile][16], gs[kRecurTile][2];
+// for the whole chunk. Tokens go through LDS in tiles of 64, double
+// buffered: the next tile's global loads are issued before the current tile
+// is walked and land in the other buffer after it, one barrier per tile.
+// Within a tile the next token's operands are read from LDS while the
+// current token's chain runs. Lane j of a row keeps the readout of tokens
+// with index j mod 16 and stores them 16 tokens at a time.
+constexpr int kRecurTile = 64;
+struct RecurTileRegs {
+  u32x4 q[4], k[4];
+  uint2 v;
+  float gb;
+};
+__device__ __forceinline__ void recur_tile_load(const uint16_t* q, const uint16_t* k, const uint16_t* v,
+                                                const float* g, const float* beta, int h, int r0, int t0,
+                                                int nt, RecurTileRegs& R) {
+  const int t = threadIdx.x;
+  const int tt = t >> 2, c = (t & 3) * 32;
+  if (tt < nt) {
+    const size_t o = ((size_t)(t0 + tt) * 16 + h) * 128 + c;
+    const u32x4* qp = reinterpret_cast<const u32x4*>(q + o);
+    const u32x4* kp = reinterpret_cast<const u32x4*>(k + o);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      R.q[i] = qp[i];
+      R.k[i] = kp[i];
+    }
+    R.v = *reinterpret_cast<const uint2*>(v + ((size_t)(t0 + tt) * 16 + h) * 128 + r0 + (t & 3) * 4);
+  }
+  if (t < 2 * kRecurTile && (t & 63) < nt) R.gb = (t < 64 ? g : beta)[(size_t)(t0 + (t & 63)) * 16 + h];
+}
+__device__ __forceinline__ void recur_tile_store(const RecurTileRegs& R, int nt, float (*qs)[128],
+                                                 float (*ks)[128], float (*vs)[16], float (*gs)[2]) {
+  const int t = threadIdx.x;
+  const int tt = t >> 2, c = (t & 3) * 32;
+  if (tt < nt) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int w = 0; w < 4; ++w) {
+        qs[tt][c + 8 * i + 2 * w] = bf_lo(R.q[i][w]);
+        qs[tt][c + 8 * i + 2 * w + 1] = bf_hi(R.q[i][w]);
+        ks[tt][c + 8 * i + 2 * w] = bf_lo(R.k[i][w]);
+        ks[tt][c + 8 * i + 2 * w + 1] = bf_hi(R.k[i][w]);
+      }
+    const int rr = (t & 3) * 4;
+    vs[tt][rr] = bf_lo(R.v.x);
+    vs[tt][rr + 1] = bf_hi(R.v.x);
+    vs[tt][rr + 2] = bf_lo(R.v.y);
+    vs[tt][rr + 3] = bf_hi(R.v.y);
+  }
+  if (t < 2 * kRecurTile && (t & 63) < nt) gs[t & 63][t >> 6] = R.gb;
+}
+__global__ __launch_bounds__(256, 1) void k_gdn_recur_rows(const uint16_t* q, const uint16_t* k,
+                                                           const uint16_t* v, const float* g,
+                                                           const float* beta, int m, float* state,
+                                                           uint16_t* y) {
+  __shared__ __attribute__((aligned(16))) float qs[2][kRecurTile][128];
+  __shared__ __attribute__((aligned(16))) float ks[2][kRecurTile][128];
+  __shared__ float vs[2][kRecurTile][16];
+  __shared__ float gs[2][kRecurTile][2];
   const int t = threadIdx.x, h = blockIdx.y, r0 = blockIdx.x * 16;
-  const int row = r0 + (t >> 4), j = t & 15;
+  const int rl = t >> 4, row = r0 + rl, j = t & 15;
   float* sp = state + ((size_t)(h * 128 + row)) * 128 + 8 * j;
   const float4 s_lo = reinterpret_cast<const float4*>(sp)[0];
   const float4 s_hi = reinterpret_cast<const float4*>(sp)[1];
   float S[8] = {s_lo.x, s_lo.y, s_lo.z, s_lo.w, s_hi.x, s_hi.y, s_hi.z, s_hi.w};
-  for (int t0 = 0; t0 < m; t0 += kRecurTile) {
+  RecurTileRegs R;
+  recur_tile_load(q, k, v, g, beta, h, r0, 0, min(kRecurTile, m), R);
+  recur_tile_store(R, min(kRecurTile, m), qs[0], ks[0], vs[0], gs[0]);
+  __syncthreads();
+  uint16_t* yrow = y + h * 128 + row;
+  for (int t0 = 0, buf = 0; t0 < m; t0 += kRecurTile, buf ^= 1) {
     const int nt = min(kRecurTile, m - t0);
-    __syncthreads();
-    for (int i = t; i < nt * 128; i += 256) {
-      const int tt = i >> 7, c = i & 127;
-      const size_t o = ((size_t)(t0 + tt) * 16 + h) * 128 + c;
-      qs[tt][c] = bf2f(q[o]);
-      ks[tt][c] = bf2f(k[o]);
-    }
-    for (int i = t; i < nt * 16; i += 256) {
-      const int tt = i >> 4, rr = i & 15;
-      vs[tt][rr] = bf2f(v[((size_t)(t0 + tt) * 16 + h) * 128 + r0 + rr]);
-    }
-    if (t < nt) {
-      gs[t][0] = g[(size_t)(t0 + t) * 16 + h];
-      gs[t][1] = beta[(size_t)(t0 + t) * 16 + h];
-    }
-    __syncthreads();
+    const int nt_next = min(kRecurTile, m - t0 - kRecurTile);
+    if (nt_next > 0) recur_tile_load(q, k, v, g, beta, h, r0, t0 + kRecurTile, nt_next, R);
+    float4 k0 = *reinterpret_cast<const float4*>(&ks[buf][0][8 * j]);
+    float4 k1 = *reinterpret_cast<const float4*>(&ks[buf][0][8 * j + 4]);
+    float4 q0 = *reinterpret_cast<const float4*>(&qs[buf][0][8 * j]);
+    float4 q1 = *reinterpret_cast<const float4*>(&qs[buf][0][8 * j + 4]);
+    float2 gb = *reinterpret_cast<const float2*>(&gs[buf][0][0]);
+    float vv = vs[buf][0][rl];
+    float keep = 0.0f;
     for (int tt = 0; tt < nt; ++tt) {
-      const float gg = gs[tt][0], bb = gs[tt][1];
-      float kk[8], qq[8];
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        kk[i] = ks[tt][8 * j + i];
-        qq[i] = qs[tt][8 * j + i];
+      const float kk[8] = {k0.x, k0.y, k0.z, k0.w, k1.x, k1.y, k1.z, k1.w};
+      const float qq[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
+      const float gg = gb.x, bb = gb.y, vc = vv;
+      if (tt + 1 < nt) {
+        k0 = *reinterpret_cast<const float4*>(&ks[buf][tt + 1][8 * j]);
+        k1 = *reinterpret_cast<const float4*>(&ks[buf][tt + 1][8 * j + 4]);
+        q0 = *reinterpret_cast<const float4*>(&qs[buf][tt + 1][8 * j]);
+        q1 = *reinterpret_cast<const float4*>(&qs[buf][tt + 1][8 * j + 4]);
+        gb = *reinterpret_cast<const float2*>(&gs[buf][tt + 1][0]);
+        vv = vs[buf][tt + 1][rl];
       }
       float mem = 0.0f;
 #pragma unroll
@@ -287,7 +342,7 @@ __global__ __launch_bounds__(256) void k_gdn_recur_rows(const uint16_t* q, const
         mem = fmaf(S[i], kk[i], mem);
       }
       mem = tree16(mem);
-      const float delta = (vs[tt][t >> 4] - mem) * bb;
+      const float delta = (vc - mem) * bb;
       float out = 0.0f;
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
@@ -295,8 +350,14 @@ __global__ __launch_bounds__(256) void k_gdn_recur_rows(const uint16_t* q, const
         out = fmaf(S[i], qq[i], out);
       }
       out = tree16(out);
-      if (j == 0) y[(size_t)(t0 + tt) * 2048 + h * 128 + row] = (uint16_t)f2bf(out);
+      keep = (tt & 15) == j ? out : keep;
+      if ((tt & 15) == 15 || tt == nt - 1) {
+        const int base = tt & ~15;
+        if (base + j <= tt) yrow[(size_t)(t0 + base + j) * 2048] = (uint16_t)f2bf(keep);
+      }
     }
+    if (nt_next > 0) recur_tile_store(R, nt_next, qs[buf ^ 1], ks[buf ^ 1], vs[buf ^ 1], gs[buf ^ 1]);
+    __syncthreads();
   }
   reinterpret_cast<float4*>(sp)[0] = make_float4(S[0], S[1], S[2], S[3]);
   reinterpret_cast<float4*>(sp)[1] = make_float4(S[4], S[5], S[6], S[7]);
@@ -508,11 +569,16 @@ __global__ __launch_bounds__(256, 1) void k_attn_prefill(const uint16_t* qr, con
     }
     const float2 sp = rows_xor32(psum);
     lrun = lrun * factor + (sp.x + sp.y);
+    const float mrun_old = mrun;
     mrun = mnew;
+    // factor is exactly 1 where the maximum did not grow: the rescale is
+    // skipped unless some lane's maximum grew
+    if (__any(mnew > mrun_old)) {
 #pragma unroll
-    for (int dt = 0; dt < 8; ++dt)
+      for (int dt = 0; dt < 8; ++dt)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) ot[dt][r] *= factor;
+        for (int r = 0; r < 16; ++r) ot[dt][r] *= factor;
+    }
     // O^T += V^T . P^T, two 16-key steps
 #pragma unroll
     for (int ks2 = 0; ks2 < 2; ++ks2) {

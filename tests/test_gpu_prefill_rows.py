@@ -109,7 +109,7 @@ def test_gdn_prepare_rows(pos0, m):
     assert_bits_equal(ring, want, what="ring after the chunk")
 
 
-@pytest.mark.parametrize("m", [1, 33, 100])
+@pytest.mark.parametrize("m", [1, 33, 100, 257])
 def test_gdn_recur_rows(m):
     print(f"case gdn_recur_rows m={m}", flush=True)
     r = rng(70 + m)
