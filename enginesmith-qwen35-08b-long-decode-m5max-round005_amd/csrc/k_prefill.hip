@@ -469,21 +469,56 @@ __global__ __launch_bounds__(256) void k_attn_gate_rows(const uint16_t* o, const
 // per-lane values with one exchange between lanes l and l^32. The exp'ed
 // scores, rounded to bf16, are then directly the B operand of
 // O^T += V^T . P^T, with the MFMA's k index j of lane half h standing for key
-// (j < 4 ? 4h + j : 8 + 4h + j - 4) (+16 for the second step); V is staged
-// transposed in LDS and read in that key order. Exponentials are base 2 on
-// scores scaled by log2(e)/16.
-constexpr int kFaQ = 32, kFaKs = 264, kFaVs = 40;
+// (j < 4 ? 4h + j : 8 + 4h + j - 4) (+16 for the second step). Exponentials
+// are base 2 on scores scaled by log2(e)/16.
+//
+// K and V blocks reach LDS by DMA (global_load_lds, 16 bytes a lane, no
+// registers), kFaStages blocks deep: block kb + kFaStages - 1 is issued while
+// block kb is computed. One DMA instruction moves one 512-byte row (32
+// lanes); K rows sit 528 bytes apart and V rows 576 bytes apart, strides at
+// which the K reads (32 rows, one 16-byte column) and the transposing V reads
+// (ds_read_b64_tr_b16: 8 rows x 64 bytes) spread over the banks. The
+// transposing read gives lane i of each 16-lane group element i of the 4 rows
+// x 16 columns its lanes address: lane l gets V[4 keys][d = l%32] for its
+// A-operand k indices. It is issued as inline assembly with its own
+// lgkmcnt wait, which keeps the compiler from waiting for every DMA in
+// flight before it.
+constexpr int kFaQ = 32, kFaStages = 4, kFaKs = 264, kFaVs = 288;
+constexpr int kFaStageHalves = 32 * kFaKs + 32 * kFaVs;
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+// four transposing reads at a + 64*i bytes (i = 0..3: four 32-dim tiles),
+// then their wait
+__device__ __forceinline__ void lds_read_tr16_x4(uint32_t a, uint2& r0, uint2& r1, uint2& r2, uint2& r3) {
+  uint64_t x0, x1, x2, x3;
+  asm volatile(
+      "ds_read_b64_tr_b16 %0, %4\n\t"
+      "ds_read_b64_tr_b16 %1, %4 offset:64\n\t"
+      "ds_read_b64_tr_b16 %2, %4 offset:128\n\t"
+      "ds_read_b64_tr_b16 %3, %4 offset:192\n\t"
+      "s_waitcnt lgkmcnt(0)"
+      : "=&v"(x0), "=&v"(x1), "=&v"(x2), "=&v"(x3)
+      : "v"(a)
+      : "memory");
+  r0 = __builtin_bit_cast(uint2, x0);
+  r1 = __builtin_bit_cast(uint2, x1);
+  r2 = __builtin_bit_cast(uint2, x2);
+  r3 = __builtin_bit_cast(uint2, x3);
+}
 __global__ __launch_bounds__(256, 1) void k_attn_prefill(const uint16_t* qr, const uint16_t* kcache,
                                                          const uint16_t* vcache, int pos0, int m,
                                                          int capacity, uint16_t* o) {
-  __shared__ __attribute__((aligned(16))) uint16_t ks[2][32][kFaKs];
-  __shared__ __attribute__((aligned(16))) uint16_t vt[2][256][kFaVs];
+  __shared__ __attribute__((aligned(16))) uint16_t kv[kFaStages][kFaStageHalves];
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
   const int t0 = blockIdx.x * kFaQ, kvh = blockIdx.y, hq = 4 * kvh + wave;
   const int ql = lane & 31, hh = lane >> 5;
   const int qrow = t0 + ql;
   const bool qvalid = qrow < m;
   const int qpos = pos0 + (qvalid ? qrow : m - 1);
+  const int last_key = pos0 + min(t0 + kFaQ, m) - 1;
+  const int nkb = last_key / 32 + 1;
   // Q fragments: B operand of step s holds Q[q][16s + 8hh .. +7]
   bf16x8 qf[16];
   {
@@ -495,6 +530,25 @@ __global__ __launch_bounds__(256, 1) void k_attn_prefill(const uint16_t* qr, con
       qf[s2] = __builtin_bit_cast(bf16x8, v);
     }
   }
+  // DMA of one block of 32 keys: wave w moves rows 8w .. 8w+7 of K and V,
+  // one row per instruction, lane L < 32 the row's 16-byte chunk L
+  auto issue = [&](int kb) {
+    uint16_t* stage = kv[kb % kFaStages];
+    if (lane < 32) {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const int r = 8 * wave + i;
+        const int key = min(kb * 32 + r, capacity - 1);
+        const size_t off = ((size_t)kvh * capacity + key) * 256 + lane * 8;
+        __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)(kcache + off),
+                                         (__attribute__((address_space(3))) void*)(stage + r * kFaKs), 16, 0, 0);
+        __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)(vcache + off),
+                                         (__attribute__((address_space(3))) void*)(stage + 32 * kFaKs + r * kFaVs),
+                                         16, 0, 0);
+      }
+    }
+  };
+  for (int kb = 0; kb < min(kFaStages - 1, nkb); ++kb) issue(kb);
   f32x16 ot[8];
 #pragma unroll
   for (int dt = 0; dt < 8; ++dt)
@@ -502,50 +556,34 @@ __global__ __launch_bounds__(256, 1) void k_attn_prefill(const uint16_t* qr, con
     for (int r = 0; r < 16; ++r) ot[dt][r] = 0.0f;
   float mrun = -INFINITY, lrun = 0.0f;
   const float c = 0.0625f * 1.4426950408889634f;  // 1/16 * log2(e)
-
-  // staging roles: key t/8, 32 dims (t%8)
-  const int sk = t >> 3, sd = (t & 7) * 32;
-  const int last_key = pos0 + min(t0 + kFaQ, m) - 1;
-  const int nkb = last_key / 32 + 1;
-  u32x4 kreg[4], vreg[4];
-  auto gload = [&](int kb) {
-    const int key = kb * 32 + sk;
-    const bool ok = key < capacity;
-    const size_t off = ((size_t)kvh * capacity + (ok ? key : 0)) * 256 + sd;
-    const u32x4* kp = reinterpret_cast<const u32x4*>(kcache + off);
-    const u32x4* vp = reinterpret_cast<const u32x4*>(vcache + off);
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      kreg[i] = ok ? kp[i] : u32x4{0u, 0u, 0u, 0u};
-      vreg[i] = ok ? vp[i] : u32x4{0u, 0u, 0u, 0u};
-    }
-  };
-  auto lstore = [&](int buf) {
-    u32x4* kd = reinterpret_cast<u32x4*>(&ks[buf][sk][sd]);
-#pragma unroll
-    for (int i = 0; i < 4; ++i) kd[i] = kreg[i];
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-#pragma unroll
-      for (int w2 = 0; w2 < 4; ++w2) {
-        const uint32_t u = vreg[i][w2];
-        vt[buf][sd + 8 * i + 2 * w2][sk] = (uint16_t)(u & 0xffffu);
-        vt[buf][sd + 8 * i + 2 * w2 + 1][sk] = (uint16_t)(u >> 16);
-      }
-  };
-  gload(0);
-  lstore(0);
-  __syncthreads();
+  // V read roles (see above): lane address row 4(g/2) + j/4, columns
+  // 16(g%2) + 4(j%4) of the 32-dim tile, g = lane/16, j = lane%16
+  const int g16 = lane >> 4, j16 = lane & 15;
+  const uint32_t kv_base =
+      (uint32_t)(uintptr_t)((const __attribute__((address_space(3))) uint16_t*)(&kv[0][0]));
+  const uint32_t v_lane = (uint32_t)(2 * (32 * kFaKs + (4 * (g16 >> 1) + (j16 >> 2)) * kFaVs +
+                                          16 * (g16 & 1) + 4 * (j16 & 3)));
   for (int kb = 0; kb < nkb; ++kb) {
-    const int buf = kb & 1;
-    if (kb + 1 < nkb) gload(kb + 1);
+    // blocks issued after kb and still in flight: min(kFaStages - 2, nkb-1-kb),
+    // 16 DMA instructions each per wave
+    const int ahead = min(kFaStages - 2, nkb - 1 - kb);
+    if (ahead >= 2)
+      wait_vmcnt<32>();
+    else if (ahead == 1)
+      wait_vmcnt<16>();
+    else
+      wait_vmcnt<0>();
+    __syncthreads();  // block kb visible; every wave is past block kb-1
+    if (kb + kFaStages - 1 < nkb) issue(kb + kFaStages - 1);
+    const uint16_t* ks = kv[kb % kFaStages];
+    const uint32_t vs_addr = kv_base + (uint32_t)(2 * kFaStageHalves * (kb % kFaStages)) + v_lane;
     // scores S^T[key][q] for the 32 keys of this block
     f32x16 st;
 #pragma unroll
     for (int r = 0; r < 16; ++r) st[r] = 0.0f;
 #pragma unroll
     for (int s2 = 0; s2 < 16; ++s2) {
-      const bf16x8 kf = *reinterpret_cast<const bf16x8*>(&ks[buf][ql][16 * s2 + 8 * hh]);
+      const bf16x8 kf = *reinterpret_cast<const bf16x8*>(ks + ql * kFaKs + 16 * s2 + 8 * hh);
       st = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf[s2], st, 0, 0, 0);
     }
     // scale, causal mask, online softmax for query ql
@@ -585,20 +623,21 @@ __global__ __launch_bounds__(256, 1) void k_attn_prefill(const uint16_t* qr, con
       const u32x4 pb = u32x4{pack2(pv[8 * ks2 + 0], pv[8 * ks2 + 1]), pack2(pv[8 * ks2 + 2], pv[8 * ks2 + 3]),
                              pack2(pv[8 * ks2 + 4], pv[8 * ks2 + 5]), pack2(pv[8 * ks2 + 6], pv[8 * ks2 + 7])};
       const bf16x8 pf = __builtin_bit_cast(bf16x8, pb);
+      // rows 16ks2 + (0..7) hold the keys of k indices 0..3, rows + 8 those of 4..7
+      const uint32_t a_lo = vs_addr + 2 * 16 * ks2 * kFaVs, a_hi = a_lo + 2 * 8 * kFaVs;
 #pragma unroll
-      for (int dt = 0; dt < 8; ++dt) {
-        const uint16_t* vrow = &vt[buf][32 * dt + ql][16 * ks2 + 4 * hh];
-        const uint2 lo = *reinterpret_cast<const uint2*>(vrow);
-        const uint2 hi = *reinterpret_cast<const uint2*>(vrow + 8);
-        const bf16x8 vf = __builtin_bit_cast(bf16x8, u32x4{lo.x, lo.y, hi.x, hi.y});
-        ot[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf, pf, ot[dt], 0, 0, 0);
+      for (int d4 = 0; d4 < 2; ++d4) {
+        uint2 lo[4], hi[4];
+        lds_read_tr16_x4(a_lo + 256 * d4, lo[0], lo[1], lo[2], lo[3]);
+        lds_read_tr16_x4(a_hi + 256 * d4, hi[0], hi[1], hi[2], hi[3]);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int dt = 4 * d4 + i;
+          const bf16x8 vf = __builtin_bit_cast(bf16x8, u32x4{lo[i].x, lo[i].y, hi[i].x, hi[i].y});
+          ot[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf, pf, ot[dt], 0, 0, 0);
+        }
       }
     }
-    if (kb + 1 < nkb) {
-      __syncthreads();  // every wave is done with buffer buf ^ 1 (previous block)
-      lstore(buf ^ 1);
-    }
-    __syncthreads();
   }
   if (!qvalid) return;
   const float inv = 1.0f / lrun;
