@@ -301,7 +301,10 @@ __global__ __launch_bounds__(256, 1) void k_gdn_recur_rows(const uint16_t* q, co
   __shared__ __attribute__((aligned(16))) float ks[2][kRecurTile][128];
   __shared__ float vs[2][kRecurTile][16];
   __shared__ float gs[2][kRecurTile][2];
-  const int t = threadIdx.x, h = blockIdx.y, r0 = blockIdx.x * 16;
+  // blockIdx.x = head, blockIdx.y = block of 16 value rows: the dispatcher
+  // deals consecutive blocks to the 8 XCDs in turn, so the 8 row blocks of a
+  // head land on one XCD and share its L2 copy of the head's q and k
+  const int t = threadIdx.x, h = blockIdx.x, r0 = blockIdx.y * 16;
   const int rl = t >> 4, row = r0 + rl, j = t & 15;
   float* sp = state + ((size_t)(h * 128 + row)) * 128 + 8 * j;
   const float4 s_lo = reinterpret_cast<const float4*>(sp)[0];
@@ -316,33 +319,25 @@ __global__ __launch_bounds__(256, 1) void k_gdn_recur_rows(const uint16_t* q, co
     const int nt = min(kRecurTile, m - t0);
     const int nt_next = min(kRecurTile, m - t0 - kRecurTile);
     if (nt_next > 0) recur_tile_load(q, k, v, g, beta, h, r0, t0 + kRecurTile, nt_next, R);
-    float4 k0 = *reinterpret_cast<const float4*>(&ks[buf][0][8 * j]);
-    float4 k1 = *reinterpret_cast<const float4*>(&ks[buf][0][8 * j + 4]);
-    float4 q0 = *reinterpret_cast<const float4*>(&qs[buf][0][8 * j]);
-    float4 q1 = *reinterpret_cast<const float4*>(&qs[buf][0][8 * j + 4]);
-    float2 gb = *reinterpret_cast<const float2*>(&gs[buf][0][0]);
-    float vv = vs[buf][0][rl];
-    float keep = 0.0f;
-    for (int tt = 0; tt < nt; ++tt) {
+    // one token: lane j of the row keeps the readout of token index j
+    // within its group of 16
+    auto token = [&](int tt, int u, float& keep) {
+      const float4 k0 = *reinterpret_cast<const float4*>(&ks[buf][tt][8 * j]);
+      const float4 k1 = *reinterpret_cast<const float4*>(&ks[buf][tt][8 * j + 4]);
+      const float4 q0 = *reinterpret_cast<const float4*>(&qs[buf][tt][8 * j]);
+      const float4 q1 = *reinterpret_cast<const float4*>(&qs[buf][tt][8 * j + 4]);
+      const float2 gb = *reinterpret_cast<const float2*>(&gs[buf][tt][0]);
+      const float vc = vs[buf][tt][rl];
       const float kk[8] = {k0.x, k0.y, k0.z, k0.w, k1.x, k1.y, k1.z, k1.w};
       const float qq[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
-      const float gg = gb.x, bb = gb.y, vc = vv;
-      if (tt + 1 < nt) {
-        k0 = *reinterpret_cast<const float4*>(&ks[buf][tt + 1][8 * j]);
-        k1 = *reinterpret_cast<const float4*>(&ks[buf][tt + 1][8 * j + 4]);
-        q0 = *reinterpret_cast<const float4*>(&qs[buf][tt + 1][8 * j]);
-        q1 = *reinterpret_cast<const float4*>(&qs[buf][tt + 1][8 * j + 4]);
-        gb = *reinterpret_cast<const float2*>(&gs[buf][tt + 1][0]);
-        vv = vs[buf][tt + 1][rl];
-      }
       float mem = 0.0f;
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
-        S[i] = S[i] * gg;
+        S[i] = S[i] * gb.x;
         mem = fmaf(S[i], kk[i], mem);
       }
       mem = tree16(mem);
-      const float delta = (vc - mem) * bb;
+      const float delta = (vc - mem) * gb.y;
       float out = 0.0f;
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
@@ -350,11 +345,18 @@ __global__ __launch_bounds__(256, 1) void k_gdn_recur_rows(const uint16_t* q, co
         out = fmaf(S[i], qq[i], out);
       }
       out = tree16(out);
-      keep = (tt & 15) == j ? out : keep;
-      if ((tt & 15) == 15 || tt == nt - 1) {
-        const int base = tt & ~15;
-        if (base + j <= tt) yrow[(size_t)(t0 + base + j) * 2048] = (uint16_t)f2bf(keep);
+      keep = u == j ? out : keep;
+    };
+    for (int g0 = 0; g0 < nt; g0 += 16) {
+      const int n16 = min(16, nt - g0);
+      float keep = 0.0f;
+      if (n16 == 16) {
+#pragma unroll
+        for (int u = 0; u < 16; ++u) token(g0 + u, u, keep);
+      } else {
+        for (int u = 0; u < n16; ++u) token(g0 + u, u, keep);
       }
+      if (j < n16) yrow[(size_t)(t0 + g0 + j) * 2048] = (uint16_t)f2bf(keep);
     }
     if (nt_next > 0) recur_tile_store(R, nt_next, qs[buf ^ 1], ks[buf ^ 1], vs[buf ^ 1], gs[buf ^ 1]);
     __syncthreads();
@@ -512,7 +514,13 @@ __global__ __launch_bounds__(256, 1) void k_attn_prefill(const uint16_t* qr, con
                                                          int capacity, uint16_t* o) {
   __shared__ __attribute__((aligned(16))) uint16_t kv[kFaStages][kFaStageHalves];
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
-  const int t0 = blockIdx.x * kFaQ, kvh = blockIdx.y, hq = 4 * kvh + wave;
+  // 1-D grid dealt to the 8 XCDs in turn (block b on XCD b % 8): XCDs
+  // 0, 2, 4, 6 take KV head 0 and 1, 3, 5, 7 head 1, so the query tiles that
+  // stream one head's K and V share an XCD's L2
+  const int b = blockIdx.x, xcd = b & 7;
+  const int tile = 4 * (b >> 3) + (xcd >> 1);
+  if (tile * kFaQ >= m) return;
+  const int t0 = tile * kFaQ, kvh = xcd & 1, hq = 4 * kvh + wave;
   const int ql = lane & 31, hh = lane >> 5;
   const int qrow = t0 + ql;
   const bool qvalid = qrow < m;
@@ -697,7 +705,7 @@ hipError_t launch_gdn_prep_rows(const GdnPrepRowsArgs& a, hipStream_t s) {
 hipError_t launch_gdn_recur_rows(const uint16_t* q, const uint16_t* k, const uint16_t* v, const float* g,
                                  const float* beta, int m, float* state, uint16_t* y, hipStream_t s) {
   if (!q || !k || !v || !g || !beta || !state || !y || m < 1) return hipErrorInvalidValue;
-  hipLaunchKernelGGL(k_gdn_recur_rows, dim3(8, kGdnHeads), dim3(256), 0, s, q, k, v, g, beta, m, state, y);
+  hipLaunchKernelGGL(k_gdn_recur_rows, dim3(kGdnHeads, 8), dim3(256), 0, s, q, k, v, g, beta, m, state, y);
   return hipGetLastError();
 }
 
@@ -720,8 +728,9 @@ hipError_t launch_attn_prep_rows(const AttnPrepRowsArgs& a, hipStream_t s) {
 hipError_t launch_attn_prefill(const uint16_t* qr, const uint16_t* kcache, const uint16_t* vcache, int pos0,
                                int m, int capacity, uint16_t* o, hipStream_t s) {
   if (!qr || !kcache || !vcache || !o || m < 1 || pos0 < 0 || pos0 + m > capacity) return hipErrorInvalidValue;
-  hipLaunchKernelGGL(k_attn_prefill, dim3((m + kFaQ - 1) / kFaQ, kKvHeads), dim3(256), 0, s, qr, kcache, vcache,
-                     pos0, m, capacity, o);
+  const int tiles = (m + kFaQ - 1) / kFaQ;
+  hipLaunchKernelGGL(k_attn_prefill, dim3(8 * ((tiles + 3) / 4)), dim3(256), 0, s, qr, kcache, vcache, pos0, m,
+                     capacity, o);
   return hipGetLastError();
 }
 
