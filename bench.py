@@ -156,6 +156,8 @@ def main():
     copy_bytes = 1 << 30
     copy_ms = E.time_copy(copy_bytes, reps=20 if args.copy_calibration else 5)
     copy_gbs = 2 * copy_bytes / (copy_ms / 1e3) / 1e9
+    read_ms = E.time_read(copy_bytes, reps=10)
+    read_gbs = copy_bytes / (read_ms / 1e3) / 1e9
 
     cpu = None
     if not args.no_cpu:
@@ -198,6 +200,8 @@ def main():
             "launch_us": round(chain_ms * 1e3, 2),
             "attention_layer_us": {k: round(v * 1e3, 2) for k, v in parts.items()},
             "measured_copy_GBs": round(copy_gbs, 1),
+            "measured_read_GBs": round(read_gbs, 1),
+            "frac_of_measured_read": round(chain_bytes / (chain_ms / 1e3) / 1e9 / read_gbs, 4),
         },
         "cpu_baseline": cpu,
     }

@@ -86,6 +86,24 @@ int es_copy_d2d(void* dst, const void* src, size_t bytes, void* stream) {
   if (bytes % 16 != 0) return fail(ES_ERR_INVALID, "es_copy_d2d: bytes must be a multiple of 16");
   return hip_status(es::launch_copy16(dst, src, bytes, S(stream)), "es_copy_d2d");
 }
+int es_time_read(const void* src, size_t bytes, void* out, size_t out_bytes, int reps, double* ms_avg) {
+  if (!ms_avg || !src || !out || reps <= 0 || bytes == 0 || bytes % 16 != 0 || out_bytes < es::read16_out_bytes())
+    return fail(ES_ERR_INVALID, "es_time_read: bad arguments");
+  hipEvent_t e0, e1;
+  if (int rc = hip_status(hipEventCreate(&e0), "hipEventCreate")) return rc;
+  if (int rc = hip_status(hipEventCreate(&e1), "hipEventCreate")) return rc;
+  int rc = hip_status(es::launch_read16(src, bytes, out, nullptr), "read warmup");
+  if (!rc) rc = hip_status(hipEventRecord(e0, nullptr), "hipEventRecord");
+  for (int i = 0; i < reps && !rc; ++i) rc = hip_status(es::launch_read16(src, bytes, out, nullptr), "read");
+  if (!rc) rc = hip_status(hipEventRecord(e1, nullptr), "hipEventRecord");
+  if (!rc) rc = hip_status(hipEventSynchronize(e1), "hipEventSynchronize");
+  float ms = 0.0f;
+  if (!rc) rc = hip_status(hipEventElapsedTime(&ms, e0, e1), "hipEventElapsedTime");
+  (void)hipEventDestroy(e0);
+  (void)hipEventDestroy(e1);
+  if (!rc) *ms_avg = ms / reps;
+  return rc;
+}
 int es_time_copy_d2d(void* dst, const void* src, size_t bytes, int reps, double* ms_avg) {
   if (!ms_avg || reps <= 0 || bytes % 16 != 0) return fail(ES_ERR_INVALID, "es_time_copy_d2d: bad arguments");
   hipEvent_t e0, e1;

@@ -225,7 +225,33 @@ __global__ __launch_bounds__(256) void k_copy16(u32x4* __restrict__ dst,
     dst[i] = __builtin_nontemporal_load(src + i);
 }
 
+// Plain streaming read: non-temporal 16-byte loads, four in flight per
+// thread, xor-folded; one 4-byte store per thread (out holds gridDim x 256
+// words). The measured read-only ceiling beside the nameplate HBM figure.
+__global__ __launch_bounds__(256) void k_read16(const u32x4* __restrict__ src, size_t n16, uint32_t* out) {
+  const size_t stride = (size_t)gridDim.x * blockDim.x;
+  size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  u32x4 acc = {0u, 0u, 0u, 0u};
+  for (; i + 3 * stride < n16; i += 4 * stride) {
+    const u32x4 a = __builtin_nontemporal_load(src + i), b = __builtin_nontemporal_load(src + i + stride);
+    const u32x4 c = __builtin_nontemporal_load(src + i + 2 * stride);
+    const u32x4 d = __builtin_nontemporal_load(src + i + 3 * stride);
+    acc ^= a ^ b ^ c ^ d;
+  }
+  for (; i < n16; i += stride) acc ^= __builtin_nontemporal_load(src + i);
+  out[(size_t)blockIdx.x * blockDim.x + threadIdx.x] = acc[0] ^ acc[1] ^ acc[2] ^ acc[3];
+}
+
 }  // namespace
+
+size_t read16_out_bytes() { return (size_t)8192 * 256 * 4; }
+
+hipError_t launch_read16(const void* src, size_t bytes, void* out, hipStream_t s) {
+  if (!src || !out || bytes % 16 != 0 || bytes == 0) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(k_read16, dim3(8192), dim3(256), 0, s, static_cast<const u32x4*>(src), bytes / 16,
+                     static_cast<uint32_t*>(out));
+  return hipGetLastError();
+}
 
 hipError_t launch_copy16(void* dst, const void* src, size_t bytes, hipStream_t s) {
   if (!dst || !src || bytes % 16 != 0) return hipErrorInvalidValue;

@@ -47,6 +47,7 @@ _SIGNATURES = {
     "es_memset": (c_int, [c_void_p, c_int, c_size_t]),
     "es_copy_d2d": (c_int, [c_void_p, c_void_p, c_size_t, c_void_p]),
     "es_time_copy_d2d": (c_int, [c_void_p, c_void_p, c_size_t, c_int, POINTER(c_double)]),
+    "es_time_read": (c_int, [c_void_p, c_size_t, c_void_p, c_size_t, c_int, POINTER(c_double)]),
     "es_synchronize": (c_int, []),
     "es_stream_create": (c_int, [POINTER(c_void_p)]),
     "es_stream_destroy": (c_int, [c_void_p]),
@@ -377,6 +378,19 @@ class Engine:
 
 def splits_for(length: int) -> int:
     return int(lib().es_engine_splits_for(length))
+
+
+def time_read(nbytes: int, reps: int = 10) -> float:
+    """Average ms of the plain streaming-read kernel over nbytes."""
+    src, out = DeviceBuffer(nbytes), DeviceBuffer(8 << 20)
+    ms = c_double()
+    try:
+        check(lib().es_memset(src.ptr, 1, nbytes))
+        check(lib().es_time_read(src.ptr, nbytes, out.ptr, out.nbytes, reps, ctypes.byref(ms)))
+    finally:
+        src.close()
+        out.close()
+    return ms.value
 
 
 def time_copy(nbytes: int, reps: int = 10) -> float:

@@ -67,6 +67,11 @@ int es_copy_d2d(void* dst, const void* src, size_t bytes, void* stream);
 /* Average ms of `reps` es_copy_d2d launches on the null stream (HIP events):
  * the measured streaming-copy peak beside the nameplate HBM figure. */
 int es_time_copy_d2d(void* dst, const void* src, size_t bytes, int reps, double* ms_avg);
+/* Average ms of `reps` launches of a plain streaming-read kernel over `bytes`
+ * (a multiple of 16) at src; out is device scratch of at least 8 MiB. No
+ * reference counterpart: the measured read-only ceiling beside the nameplate
+ * HBM figure, for kernels that only read. */
+int es_time_read(const void* src, size_t bytes, void* out, size_t out_bytes, int reps, double* ms_avg);
 int es_synchronize(void);
 int es_stream_create(void** stream);
 int es_stream_destroy(void* stream);
