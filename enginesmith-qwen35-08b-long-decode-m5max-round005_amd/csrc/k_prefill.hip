@@ -513,7 +513,8 @@ __global__ __launch_bounds__(256, 1) void k_attn_prefill(const uint16_t* qr, con
                                                          const uint16_t* vcache, int pos0, int m,
                                                          int capacity, uint16_t* o) {
   __shared__ __attribute__((aligned(16))) uint16_t kv[kFaStages][kFaStageHalves];
-  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+  const int t = threadIdx.x, lane = t & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(t >> 6);  // uniform: scalar DMA addressing
   // 1-D grid dealt to the 8 XCDs in turn (block b on XCD b % 8): XCDs
   // 0, 2, 4, 6 take KV head 0 and 1, 3, 5, 7 head 1, so the query tiles that
   // stream one head's K and V share an XCD's L2
@@ -547,10 +548,10 @@ __global__ __launch_bounds__(256, 1) void k_attn_prefill(const uint16_t* qr, con
       for (int i = 0; i < 8; ++i) {
         const int r = 8 * wave + i;
         const int key = min(kb * 32 + r, capacity - 1);
-        const size_t off = ((size_t)kvh * capacity + key) * 256 + lane * 8;
-        __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)(kcache + off),
+        const size_t row = ((size_t)kvh * capacity + key) * 256;  // uniform
+        __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)(kcache + row + lane * 8),
                                          (__attribute__((address_space(3))) void*)(stage + r * kFaKs), 16, 0, 0);
-        __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)(vcache + off),
+        __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)(vcache + row + lane * 8),
                                          (__attribute__((address_space(3))) void*)(stage + 32 * kFaKs + r * kFaVs),
                                          16, 0, 0);
       }
@@ -594,23 +595,27 @@ __global__ __launch_bounds__(256, 1) void k_attn_prefill(const uint16_t* qr, con
       const bf16x8 kf = *reinterpret_cast<const bf16x8*>(ks + ql * kFaKs + 16 * s2 + 8 * hh);
       st = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf[s2], st, 0, 0, 0);
     }
-    // scale, causal mask, online softmax for query ql
-    float x[16];
-    float mloc = -INFINITY;
+    // causal mask (only blocks that reach past the tile's first query),
+    // online softmax for query ql; the maximum is taken on the raw scores
+    // (scaling by c > 0 keeps the order) and the exponent is fma(s, c, -max)
+    if (kb * 32 + 31 > pos0 + t0) {
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const int key = kb * 32 + 8 * (r >> 2) + 4 * hh + (r & 3);
-      x[r] = key <= qpos ? st[r] * c : -INFINITY;
-      mloc = fmaxf(mloc, x[r]);
+      for (int r = 0; r < 16; ++r) {
+        const int key = kb * 32 + 8 * (r >> 2) + 4 * hh + (r & 3);
+        st[r] = key <= qpos ? st[r] : -INFINITY;
+      }
     }
+    float mloc = st[0];
+#pragma unroll
+    for (int r = 1; r < 16; ++r) mloc = fmaxf(mloc, st[r]);
     const float2 mp = rows_xor32(mloc);
-    const float mnew = fmaxf(mrun, fmaxf(mp.x, mp.y));
-    const float factor = exp2f(mrun - mnew);
+    const float mnew = fmaxf(mrun, fmaxf(mp.x, mp.y) * c);
+    const float factor = __builtin_amdgcn_exp2f(mrun - mnew);
     float psum = 0.0f;
     float pv[16];
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
-      pv[r] = exp2f(x[r] - mnew);
+      pv[r] = __builtin_amdgcn_exp2f(fmaf(st[r], c, -mnew));
       psum += pv[r];
     }
     const float2 sp = rows_xor32(psum);
