@@ -609,7 +609,13 @@ __global__ __launch_bounds__(256, 1) void k_attn_prefill(const uint16_t* qr, con
 #pragma unroll
     for (int r = 1; r < 16; ++r) mloc = fmaxf(mloc, st[r]);
     const float2 mp = rows_xor32(mloc);
-    const float mnew = fmaxf(mrun, fmaxf(mp.x, mp.y) * c);
+    // The exponent's reference value moves only when the block's maximum
+    // exceeds it by more than 8 (probabilities stay below 2^8; the output is
+    // normalised by a sum taken against the same reference, so the softmax is
+    // unchanged). The choice is per row, so a row's result depends on its own
+    // scores only.
+    const float mblk = fmaxf(mp.x, mp.y) * c;
+    const float mnew = mblk > mrun + 8.0f ? mblk : mrun;
     const float factor = __builtin_amdgcn_exp2f(mrun - mnew);
     float psum = 0.0f;
     float pv[16];
@@ -622,8 +628,8 @@ __global__ __launch_bounds__(256, 1) void k_attn_prefill(const uint16_t* qr, con
     lrun = lrun * factor + (sp.x + sp.y);
     const float mrun_old = mrun;
     mrun = mnew;
-    // factor is exactly 1 where the maximum did not grow: the rescale is
-    // skipped unless some lane's maximum grew
+    // factor is exactly 1 where the reference did not move: the rescale is
+    // skipped unless some lane's reference moved
     if (__any(mnew > mrun_old)) {
 #pragma unroll
       for (int dt = 0; dt < 8; ++dt)
