@@ -271,20 +271,28 @@ __device__ __forceinline__ void recur_tile_load(const uint16_t* q, const uint16_
   }
   if (t < 2 * kRecurTile && (t & 63) < nt) R.gb = (t < 64 ? g : beta)[(size_t)(t0 + (t & 63)) * 16 + h];
 }
-__device__ __forceinline__ void recur_tile_store(const RecurTileRegs& R, int nt, float (*qs)[128],
-                                                 float (*ks)[128], float (*vs)[16], float (*gs)[2]) {
+// LDS tile rows: 132 floats apart (the 16 rows a store instruction covers
+// fall in different banks); within a row, channel c of 8-channel group j sits
+// at 4j + (c & 3), plus 64 for the group's upper four, so the two 16-byte
+// reads of a row's 16 lanes each cover 256 contiguous bytes.
+constexpr int kRecurRow = 132;
+__device__ __forceinline__ void recur_tile_store(const RecurTileRegs& R, int nt, float (*qs)[kRecurRow],
+                                                 float (*ks)[kRecurRow], float (*vs)[16], float (*gs)[2]) {
   const int t = threadIdx.x;
-  const int tt = t >> 2, c = (t & 3) * 32;
+  const int tt = t >> 2, j0 = (t & 3) * 4;
   if (tt < nt) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
-#pragma unroll
-      for (int w = 0; w < 4; ++w) {
-        qs[tt][c + 8 * i + 2 * w] = bf_lo(R.q[i][w]);
-        qs[tt][c + 8 * i + 2 * w + 1] = bf_hi(R.q[i][w]);
-        ks[tt][c + 8 * i + 2 * w] = bf_lo(R.k[i][w]);
-        ks[tt][c + 8 * i + 2 * w + 1] = bf_hi(R.k[i][w]);
-      }
+    for (int i = 0; i < 4; ++i) {
+      const int jj = j0 + i;
+      *reinterpret_cast<float4*>(&qs[tt][4 * jj]) =
+          make_float4(bf_lo(R.q[i][0]), bf_hi(R.q[i][0]), bf_lo(R.q[i][1]), bf_hi(R.q[i][1]));
+      *reinterpret_cast<float4*>(&qs[tt][64 + 4 * jj]) =
+          make_float4(bf_lo(R.q[i][2]), bf_hi(R.q[i][2]), bf_lo(R.q[i][3]), bf_hi(R.q[i][3]));
+      *reinterpret_cast<float4*>(&ks[tt][4 * jj]) =
+          make_float4(bf_lo(R.k[i][0]), bf_hi(R.k[i][0]), bf_lo(R.k[i][1]), bf_hi(R.k[i][1]));
+      *reinterpret_cast<float4*>(&ks[tt][64 + 4 * jj]) =
+          make_float4(bf_lo(R.k[i][2]), bf_hi(R.k[i][2]), bf_lo(R.k[i][3]), bf_hi(R.k[i][3]));
+    }
     const int rr = (t & 3) * 4;
     vs[tt][rr] = bf_lo(R.v.x);
     vs[tt][rr + 1] = bf_hi(R.v.x);
@@ -297,8 +305,8 @@ __global__ __launch_bounds__(256, 1) void k_gdn_recur_rows(const uint16_t* q, co
                                                            const uint16_t* v, const float* g,
                                                            const float* beta, int m, float* state,
                                                            uint16_t* y) {
-  __shared__ __attribute__((aligned(16))) float qs[2][kRecurTile][128];
-  __shared__ __attribute__((aligned(16))) float ks[2][kRecurTile][128];
+  __shared__ __attribute__((aligned(16))) float qs[2][kRecurTile][kRecurRow];
+  __shared__ __attribute__((aligned(16))) float ks[2][kRecurTile][kRecurRow];
   __shared__ float vs[2][kRecurTile][16];
   __shared__ float gs[2][kRecurTile][2];
   // blockIdx.x = head, blockIdx.y = block of 16 value rows: the dispatcher
@@ -320,24 +328,33 @@ __global__ __launch_bounds__(256, 1) void k_gdn_recur_rows(const uint16_t* q, co
     const int nt_next = min(kRecurTile, m - t0 - kRecurTile);
     if (nt_next > 0) recur_tile_load(q, k, v, g, beta, h, r0, t0 + kRecurTile, nt_next, R);
     // one token: lane j of the row keeps the readout of token index j
-    // within its group of 16
-    auto token = [&](int tt, int u, float& keep) {
-      const float4 k0 = *reinterpret_cast<const float4*>(&ks[buf][tt][8 * j]);
-      const float4 k1 = *reinterpret_cast<const float4*>(&ks[buf][tt][8 * j + 4]);
-      const float4 q0 = *reinterpret_cast<const float4*>(&qs[buf][tt][8 * j]);
-      const float4 q1 = *reinterpret_cast<const float4*>(&qs[buf][tt][8 * j + 4]);
-      const float2 gb = *reinterpret_cast<const float2*>(&gs[buf][tt][0]);
-      const float vc = vs[buf][tt][rl];
-      const float kk[8] = {k0.x, k0.y, k0.z, k0.w, k1.x, k1.y, k1.z, k1.w};
-      const float qq[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
+    // within its group of 16; its operands are read one token ahead
+    struct TokOps {
+      float4 k0, k1, q0, q1;
+      float2 gb;
+      float v;
+    };
+    auto operands = [&](int tt) {
+      TokOps o;
+      o.k0 = *reinterpret_cast<const float4*>(&ks[buf][tt][4 * j]);
+      o.k1 = *reinterpret_cast<const float4*>(&ks[buf][tt][64 + 4 * j]);
+      o.q0 = *reinterpret_cast<const float4*>(&qs[buf][tt][4 * j]);
+      o.q1 = *reinterpret_cast<const float4*>(&qs[buf][tt][64 + 4 * j]);
+      o.gb = *reinterpret_cast<const float2*>(&gs[buf][tt][0]);
+      o.v = vs[buf][tt][rl];
+      return o;
+    };
+    auto token = [&](const TokOps& o, int u, float& keep) {
+      const float kk[8] = {o.k0.x, o.k0.y, o.k0.z, o.k0.w, o.k1.x, o.k1.y, o.k1.z, o.k1.w};
+      const float qq[8] = {o.q0.x, o.q0.y, o.q0.z, o.q0.w, o.q1.x, o.q1.y, o.q1.z, o.q1.w};
       float mem = 0.0f;
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
-        S[i] = S[i] * gb.x;
+        S[i] = S[i] * o.gb.x;
         mem = fmaf(S[i], kk[i], mem);
       }
       mem = tree16(mem);
-      const float delta = (vc - mem) * gb.y;
+      const float delta = (o.v - mem) * o.gb.y;
       float out = 0.0f;
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
@@ -351,10 +368,16 @@ __global__ __launch_bounds__(256, 1) void k_gdn_recur_rows(const uint16_t* q, co
       const int n16 = min(16, nt - g0);
       float keep = 0.0f;
       if (n16 == 16) {
+        TokOps cur = operands(g0);
 #pragma unroll
-        for (int u = 0; u < 16; ++u) token(g0 + u, u, keep);
+        for (int u = 0; u < 16; ++u) {
+          TokOps nxt;
+          if (u + 1 < 16) nxt = operands(g0 + u + 1);
+          token(cur, u, keep);
+          cur = nxt;
+        }
       } else {
-        for (int u = 0; u < n16; ++u) token(g0 + u, u, keep);
+        for (int u = 0; u < n16; ++u) token(operands(g0 + u), u, keep);
       }
       if (j < n16) yrow[(size_t)(t0 + g0 + j) * 2048] = (uint16_t)f2bf(keep);
     }
