@@ -514,23 +514,31 @@ template <int N>
 __device__ __forceinline__ void wait_vmcnt() {
   __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
 }
-// four transposing reads at a + 64*i bytes (i = 0..3: four 32-dim tiles),
-// then their wait
-__device__ __forceinline__ void lds_read_tr16_x4(uint32_t a, uint2& r0, uint2& r1, uint2& r2, uint2& r3) {
-  uint64_t x0, x1, x2, x3;
+// eight transposing reads: at a + 64*i and b + 64*i bytes (i = 0..3: four
+// 32-dim tiles of the two key groups), then one wait for all of them
+__device__ __forceinline__ void lds_read_tr16_x8(uint32_t a, uint32_t b, uint2 (&ra)[4], uint2 (&rb)[4]) {
+  uint64_t x0, x1, x2, x3, y0, y1, y2, y3;
   asm volatile(
-      "ds_read_b64_tr_b16 %0, %4\n\t"
-      "ds_read_b64_tr_b16 %1, %4 offset:64\n\t"
-      "ds_read_b64_tr_b16 %2, %4 offset:128\n\t"
-      "ds_read_b64_tr_b16 %3, %4 offset:192\n\t"
+      "ds_read_b64_tr_b16 %0, %8\n\t"
+      "ds_read_b64_tr_b16 %1, %8 offset:64\n\t"
+      "ds_read_b64_tr_b16 %2, %8 offset:128\n\t"
+      "ds_read_b64_tr_b16 %3, %8 offset:192\n\t"
+      "ds_read_b64_tr_b16 %4, %9\n\t"
+      "ds_read_b64_tr_b16 %5, %9 offset:64\n\t"
+      "ds_read_b64_tr_b16 %6, %9 offset:128\n\t"
+      "ds_read_b64_tr_b16 %7, %9 offset:192\n\t"
       "s_waitcnt lgkmcnt(0)"
-      : "=&v"(x0), "=&v"(x1), "=&v"(x2), "=&v"(x3)
-      : "v"(a)
+      : "=&v"(x0), "=&v"(x1), "=&v"(x2), "=&v"(x3), "=&v"(y0), "=&v"(y1), "=&v"(y2), "=&v"(y3)
+      : "v"(a), "v"(b)
       : "memory");
-  r0 = __builtin_bit_cast(uint2, x0);
-  r1 = __builtin_bit_cast(uint2, x1);
-  r2 = __builtin_bit_cast(uint2, x2);
-  r3 = __builtin_bit_cast(uint2, x3);
+  ra[0] = __builtin_bit_cast(uint2, x0);
+  ra[1] = __builtin_bit_cast(uint2, x1);
+  ra[2] = __builtin_bit_cast(uint2, x2);
+  ra[3] = __builtin_bit_cast(uint2, x3);
+  rb[0] = __builtin_bit_cast(uint2, y0);
+  rb[1] = __builtin_bit_cast(uint2, y1);
+  rb[2] = __builtin_bit_cast(uint2, y2);
+  rb[3] = __builtin_bit_cast(uint2, y3);
 }
 __global__ __launch_bounds__(256, 1) void k_attn_prefill(const uint16_t* qr, const uint16_t* kcache,
                                                          const uint16_t* vcache, int pos0, int m,
@@ -670,8 +678,7 @@ __global__ __launch_bounds__(256, 1) void k_attn_prefill(const uint16_t* qr, con
 #pragma unroll
       for (int d4 = 0; d4 < 2; ++d4) {
         uint2 lo[4], hi[4];
-        lds_read_tr16_x4(a_lo + 256 * d4, lo[0], lo[1], lo[2], lo[3]);
-        lds_read_tr16_x4(a_hi + 256 * d4, hi[0], hi[1], hi[2], hi[3]);
+        lds_read_tr16_x8(a_lo + 256 * d4, a_hi + 256 * d4, lo, hi);
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           const int dt = 4 * d4 + i;
