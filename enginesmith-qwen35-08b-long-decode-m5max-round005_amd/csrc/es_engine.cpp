@@ -49,6 +49,16 @@ Engine* Engine::create(const void* blob, uint64_t bytes, int n_layers, int vocab
 
 Engine::~Engine() {
   if (stream_) (void)hipStreamSynchronize(stream_);
+  for (hipStream_t ps : pstream_)
+    if (ps) {
+      (void)hipStreamSynchronize(ps);
+      (void)hipStreamDestroy(ps);
+    }
+  for (auto& row : state_done_)
+    for (hipEvent_t e : row)
+      if (e) (void)hipEventDestroy(e);
+  for (hipEvent_t e : join_ev_)
+    if (e) (void)hipEventDestroy(e);
   for (auto& g : graphs_) {
     (void)hipGraphExecDestroy(g.exec);
     (void)hipGraphDestroy(g.g);
@@ -462,25 +472,34 @@ int Engine::ensure_prefill_buffers(std::string* err) {
     allocations_.push_back(p);
     return p;
   };
-  PrefillBuffers b{};
-  uint16_t** bf[] = {&b.h, &b.u, &b.raw, &b.z, &b.a, &b.b, &b.q, &b.k, &b.v, &b.y, &b.gated, &b.qp, &b.kp,
-                     &b.vp, &b.query, &b.o, &b.gate, &b.up, &b.act};
-  const size_t width[] = {1024, 1024, 6144, 2048, 16, 16, 2048, 2048, 2048, 2048, 2048, 4096, 512,
-                          512, 2048, 2048, 3584, 3584, 3584};
-  for (size_t i = 0; i < sizeof(width) / sizeof(width[0]); ++i) {
-    *bf[i] = static_cast<uint16_t*>(alloc(r * width[i] * 2));
-    if (!*bf[i]) {
+  if (!pstream_[0]) {
+    for (auto& ps : pstream_) ES_HIP(hipStreamCreateWithFlags(&ps, hipStreamNonBlocking), "prefill stream");
+    for (int slot = 0; slot < 2; ++slot)
+      for (int l = 0; l < shape_.n_layers; ++l)
+        ES_HIP(hipEventCreateWithFlags(&state_done_[slot][l], hipEventDisableTiming), "prefill event");
+    for (auto& e : join_ev_) ES_HIP(hipEventCreateWithFlags(&e, hipEventDisableTiming), "prefill event");
+  }
+  for (int slot = 0; slot < 2; ++slot) {
+    PrefillBuffers b{};
+    uint16_t** bf[] = {&b.h, &b.u, &b.raw, &b.z, &b.a, &b.b, &b.q, &b.k, &b.v, &b.y, &b.gated, &b.qp, &b.kp,
+                       &b.vp, &b.query, &b.o, &b.gate, &b.up, &b.act};
+    const size_t width[] = {1024, 1024, 6144, 2048, 16, 16, 2048, 2048, 2048, 2048, 2048, 4096, 512,
+                            512, 2048, 2048, 3584, 3584, 3584};
+    for (size_t i = 0; i < sizeof(width) / sizeof(width[0]); ++i) {
+      *bf[i] = static_cast<uint16_t*>(alloc(r * width[i] * 2));
+      if (!*bf[i]) {
+        if (err) *err = "device allocation of prefill buffers failed";
+        return 2;
+      }
+    }
+    b.g = static_cast<float*>(alloc(r * 16 * 4));
+    b.beta = static_cast<float*>(alloc(r * 16 * 4));
+    if (!b.g || !b.beta) {
       if (err) *err = "device allocation of prefill buffers failed";
       return 2;
     }
+    pf_[slot] = b;
   }
-  b.g = static_cast<float*>(alloc(r * 16 * 4));
-  b.beta = static_cast<float*>(alloc(r * 16 * 4));
-  if (!b.g || !b.beta) {
-    if (err) *err = "device allocation of prefill buffers failed";
-    return 2;
-  }
-  pf_ = b;
   prefill_alloc_rows_ = rows;
   return 0;
 }
@@ -492,13 +511,16 @@ int Engine::ensure_prefill_buffers(std::string* err) {
 // cache, causal flash attention, output gate), the output linear with the
 // residual add, post RMSNorm rows, gate/up linears, SwiGLU, down linear with
 // the residual add.
-int Engine::prefill_rows(int pos0, int m, std::string* err) {
-  const PrefillBuffers& b = pf_;
-  hipStream_t s = stream_;
+int Engine::prefill_rows(int pos0, int m, int slot, bool wait_prev, std::string* err) {
+  const PrefillBuffers& b = pf_[slot];
+  hipStream_t s = pstream_[slot];
   ES_HIP(launch_embed_rows(embed_, prompt_ + pos0, m, b.h, s), "prefill embedding");
   for (int l = 0; l < shape_.n_layers; ++l) {
     const LayerDev& L = layers_[l];
     ES_HIP(launch_rmsnorm_rows(b.h, L.input_norm, m, b.u, s), "prefill input norm");
+    // the previous chunk must have finished this layer's conv ring, state or
+    // K/V rows before this chunk's mixer reads them
+    if (wait_prev) ES_HIP(hipStreamWaitEvent(s, state_done_[slot ^ 1][l], 0), "prefill wait");
     if (!L.attention) {
       ES_HIP(launch_q4_gemm(L.qkv, b.u, m, nullptr, b.raw, s), "prefill qkv");
       ES_HIP(launch_q4_gemm(L.z, b.u, m, nullptr, b.z, s), "prefill z");
@@ -508,6 +530,7 @@ int Engine::prefill_rows(int pos0, int m, std::string* err) {
                         b.q, b.k, b.v, b.g, b.beta};
       ES_HIP(launch_gdn_prep_rows(g, s), "prefill gdn prepare");
       ES_HIP(launch_gdn_recur_rows(b.q, b.k, b.v, b.g, b.beta, m, L.state, b.y, s), "prefill gdn recurrence");
+      ES_HIP(hipEventRecord(state_done_[slot][l], s), "prefill record");
       ES_HIP(launch_gdn_norm_gate_rows(b.y, b.z, L.gdn_norm, m, b.gated, s), "prefill gdn norm gate");
       ES_HIP(launch_q4_gemm(L.out, b.gated, m, b.h, b.h, s), "prefill out_proj");
     } else {
@@ -518,6 +541,9 @@ int Engine::prefill_rows(int pos0, int m, std::string* err) {
                          b.query, L.kcache, L.vcache, capacity_};
       ES_HIP(launch_attn_prep_rows(a, s), "prefill attention prepare");
       ES_HIP(launch_attn_prefill(b.query, L.kcache, L.vcache, pos0, m, capacity_, b.o, s), "prefill attention");
+      // after the attention, which reads key blocks that may reach into the
+      // next chunk's rows (masked, but read)
+      ES_HIP(hipEventRecord(state_done_[slot][l], s), "prefill record");
       ES_HIP(launch_attn_gate_rows(b.o, b.qp, m, b.gated, s), "prefill attention gate");
       ES_HIP(launch_q4_gemm(L.o, b.gated, m, b.h, b.h, s), "prefill o_proj");
     }
@@ -541,22 +567,38 @@ int Engine::consume_prompt(const uint32_t* prompt, int n, std::string* err) {
     return run_steps(kKindPrompt, 0, n, nullptr, nullptr, err);
   }
   if (int rc = ensure_prefill_buffers(err)) return rc;
-  int pos = 0;
+  // the prefill streams start after the reset and the prompt upload on stream_
+  ES_HIP(hipEventRecord(join_ev_[0], stream_), "prefill join");
+  for (hipStream_t ps : pstream_) ES_HIP(hipStreamWaitEvent(ps, join_ev_[0], 0), "prefill join");
+  auto join_back = [&]() -> int {
+    for (int i = 0; i < 2; ++i) {
+      ES_HIP(hipEventRecord(join_ev_[1 + i], pstream_[i]), "prefill join");
+      ES_HIP(hipStreamWaitEvent(stream_, join_ev_[1 + i], 0), "prefill join");
+    }
+    return 0;
+  };
+  int pos = 0, chunk = 0;
   while (pos < n) {
     if (cancelled_.load()) {
+      for (hipStream_t ps : pstream_) (void)hipStreamSynchronize(ps);
       (void)hipStreamSynchronize(stream_);
       if (err) *err = "input disconnected";
       return 3;
     }
     const int m = std::min(prefill_alloc_rows_, n - pos);
     if (m == 1) {
+      // a one-row chunk runs the decode kernels on stream_, after the chunks
+      if (int rc = join_back()) return rc;
       if (int rc = upload_state(pos, 0, prompt[pos], err)) return rc;
       if (int rc = run_steps(kKindPrompt, pos, 1, nullptr, nullptr, err)) return rc;
-    } else if (int rc = prefill_rows(pos, m, err)) {
+    } else if (int rc = prefill_rows(pos, m, chunk & 1, chunk > 0, err)) {
+      for (hipStream_t ps : pstream_) (void)hipStreamSynchronize(ps);
       return rc;
     }
     pos += m;
+    ++chunk;
   }
+  if (int rc = join_back()) return rc;
   ES_HIP(hipStreamSynchronize(stream_), "prefill sync");
   return 0;
 }
