@@ -143,7 +143,7 @@ class Engine {
   uint32_t* forced_ = nullptr;  // [capacity]
 
   // batched prefill buffers, rows = prefill_rows_ (allocated on first use)
-  static constexpr int kDefaultPrefillRows = 8192;
+  static constexpr int kDefaultPrefillRows = 4096;
   int prefill_rows_ = kDefaultPrefillRows;
   int prefill_alloc_rows_ = 0;
   struct PrefillBuffers {

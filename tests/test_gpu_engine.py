@@ -100,7 +100,7 @@ def test_graph_batches_equal_one_step_launches(small):
     try:
         gen = eng.generate(prompt, 37, reset=True)       # 2 batches of 16 + 5
     finally:
-        eng.set_prefill(8192)
+        eng.set_prefill(4096)
     end = eng.position
     ring_a, state_a = eng.read_gdn(0)
     kv_a = eng.read_kv(3, 0, end - 40, 40)
@@ -108,7 +108,7 @@ def test_graph_batches_equal_one_step_launches(small):
     try:
         first = eng.generate(prompt, 1, reset=True)
     finally:
-        eng.set_prefill(8192)
+        eng.set_prefill(4096)
     assert first[0] == gen[0]
     am = eng.forced_decode(gen[:-1])
     assert am.tolist() == gen[1:]

@@ -84,7 +84,7 @@ def test_chunk_size_does_not_change_results(small):
             toks = eng.generate(prompt, 6, reset=True)
             runs.append((toks, engine_state(eng, 706)))
     finally:
-        eng.set_prefill(8192)
+        eng.set_prefill(4096)
     toks0, (gdn0, kv0) = runs[0]
     for toks, (gdn, kv) in runs[1:]:
         assert toks == toks0
@@ -104,7 +104,7 @@ def test_prompt_steps_mode_is_the_decode_replay(small):
     try:
         first = eng.generate(prompt, 1, reset=True)[0]
     finally:
-        eng.set_prefill(8192)
+        eng.set_prefill(4096)
     orc = O.OracleModel(E.tensor_views(blob, **SMALL), **SMALL, capacity=64)
     assert first == orc.generate(prompt, 1)[0]
     ring, state = eng.read_gdn(0)
@@ -134,7 +134,7 @@ def test_tokens_after_batched_prefill_pass_the_harness_gates(small):
                     orc.prefill(part)
             cases.append((16, judge_from(orc, prompt[-1], toks)))
     finally:
-        eng.set_prefill(8192)
+        eng.set_prefill(4096)
     print(cases)
     assert not gates(cases), gates(cases)
 
@@ -152,7 +152,7 @@ def test_cancel_before_a_chunk_fails_and_resets(small):
             eng.generate([], 1, reset=False)
     finally:
         eng.clear_cancel()
-        eng.set_prefill(8192)
+        eng.set_prefill(4096)
 
 
 def test_set_prefill_rejects_one_row_chunks(small):
