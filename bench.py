@@ -105,8 +105,9 @@ def main():
                     help="also run the 1 GiB plain-copy kernel that calibrates the HBM byte counters")
     args = ap.parse_args()
     if args.gpus != 1:
-        print(json.dumps({"error": "this engine runs on one GPU; multi-GPU decode is not built "
-                                   "(see DESIGN.md for how the path would shard)"}))
+        print(json.dumps({"error": "this engine runs on one GPU; multi-GPU decode is not built (it would "
+                                   "shard the KV cache by position chain, one all-gather of chain states "
+                                   "per attention layer)"}))
         sys.exit(2)
     if E.device_count() < 1:
         print(json.dumps({"error": "no GPU visible"}))
