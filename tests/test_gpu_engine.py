@@ -167,6 +167,8 @@ def test_protocol_server(small, tmp_path):
     eng, _, _ = small
     prompt = [11, 22, 33, 44, 55]
     expect = eng.generate(prompt, 6, reset=True)
+    long_prompt = rng(48).integers(0, SMALL["vocab"], 3000).tolist()  # one batched chunk of 2999 rows
+    expect_long = eng.generate(long_prompt, 5, reset=True)
     p = subprocess.Popen([E.SERVER_PATH, "--model", str(d)], stdin=subprocess.PIPE, stdout=subprocess.PIPE,
                          stderr=subprocess.PIPE, text=True)
     try:
@@ -187,6 +189,8 @@ def test_protocol_server(small, tmp_path):
             {"id": 6, "ok": False, "error": "invalid token"}
         assert json.loads(ask({"op": "generate", "prompt": [1], "max_tokens": 1})) == \
             {"id": None, "ok": False, "error": "missing reset"}
+        assert json.loads(ask({"id": 8, "op": "generate", "prompt": long_prompt, "max_tokens": 5, "reset": True})) == \
+            {"id": 8, "ok": True, "tokens": expect_long}
         p.stdin.close()
         assert p.wait(timeout=60) == 0
     finally:
