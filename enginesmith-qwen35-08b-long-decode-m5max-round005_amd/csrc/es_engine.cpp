@@ -474,12 +474,12 @@ int Engine::ensure_prefill_buffers(std::string* err) {
   };
   if (!pstream_[0]) {
     for (auto& ps : pstream_) ES_HIP(hipStreamCreateWithFlags(&ps, hipStreamNonBlocking), "prefill stream");
-    for (int slot = 0; slot < 2; ++slot)
+    for (int slot = 0; slot < kPrefillStreams; ++slot)
       for (int l = 0; l < shape_.n_layers; ++l)
         ES_HIP(hipEventCreateWithFlags(&state_done_[slot][l], hipEventDisableTiming), "prefill event");
     for (auto& e : join_ev_) ES_HIP(hipEventCreateWithFlags(&e, hipEventDisableTiming), "prefill event");
   }
-  for (int slot = 0; slot < 2; ++slot) {
+  for (int slot = 0; slot < kPrefillStreams; ++slot) {
     PrefillBuffers b{};
     uint16_t** bf[] = {&b.h, &b.u, &b.raw, &b.z, &b.a, &b.b, &b.q, &b.k, &b.v, &b.y, &b.gated, &b.qp, &b.kp,
                        &b.vp, &b.query, &b.o, &b.gate, &b.up, &b.act};
@@ -520,7 +520,9 @@ int Engine::prefill_rows(int pos0, int m, int slot, bool wait_prev, std::string*
     ES_HIP(launch_rmsnorm_rows(b.h, L.input_norm, m, b.u, s), "prefill input norm");
     // the previous chunk must have finished this layer's conv ring, state or
     // K/V rows before this chunk's mixer reads them
-    if (wait_prev) ES_HIP(hipStreamWaitEvent(s, state_done_[slot ^ 1][l], 0), "prefill wait");
+    if (wait_prev)
+      ES_HIP(hipStreamWaitEvent(s, state_done_[(slot + kPrefillStreams - 1) % kPrefillStreams][l], 0),
+             "prefill wait");
     if (!L.attention) {
       ES_HIP(launch_q4_gemm(L.qkv, b.u, m, nullptr, b.raw, s), "prefill qkv");
       ES_HIP(launch_q4_gemm(L.z, b.u, m, nullptr, b.z, s), "prefill z");
@@ -571,7 +573,7 @@ int Engine::consume_prompt(const uint32_t* prompt, int n, std::string* err) {
   ES_HIP(hipEventRecord(join_ev_[0], stream_), "prefill join");
   for (hipStream_t ps : pstream_) ES_HIP(hipStreamWaitEvent(ps, join_ev_[0], 0), "prefill join");
   auto join_back = [&]() -> int {
-    for (int i = 0; i < 2; ++i) {
+    for (int i = 0; i < kPrefillStreams; ++i) {
       ES_HIP(hipEventRecord(join_ev_[1 + i], pstream_[i]), "prefill join");
       ES_HIP(hipStreamWaitEvent(stream_, join_ev_[1 + i], 0), "prefill join");
     }
@@ -591,7 +593,7 @@ int Engine::consume_prompt(const uint32_t* prompt, int n, std::string* err) {
       if (int rc = join_back()) return rc;
       if (int rc = upload_state(pos, 0, prompt[pos], err)) return rc;
       if (int rc = run_steps(kKindPrompt, pos, 1, nullptr, nullptr, err)) return rc;
-    } else if (int rc = prefill_rows(pos, m, chunk & 1, chunk > 0, err)) {
+    } else if (int rc = prefill_rows(pos, m, chunk % kPrefillStreams, chunk > 0, err)) {
       for (hipStream_t ps : pstream_) (void)hipStreamSynchronize(ps);
       return rc;
     }

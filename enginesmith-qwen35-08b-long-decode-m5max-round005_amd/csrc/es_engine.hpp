@@ -102,9 +102,10 @@ class Engine {
   int upload_state(int pos, int step, uint32_t token, std::string* err);
   // Batched forward over prompt_[pos0 .. pos0+m) without output (encode_forward
   // with rows > 1, model.rs:228-343); m <= prefill_rows_.
-  // Chunks alternate between two prefill streams (slot = chunk index & 1);
-  // with wait_prev, each layer's state update waits for the previous chunk's
-  // update of the same layer, so consecutive chunks overlap one layer apart.
+  // Chunks rotate over kPrefillStreams prefill streams (slot = chunk index
+  // mod kPrefillStreams); with wait_prev, each layer's state update waits for
+  // the previous chunk's update of the same layer, so consecutive chunks
+  // overlap one layer apart.
   int prefill_rows(int pos0, int m, int slot, bool wait_prev, std::string* err);
   int ensure_prefill_buffers(std::string* err);
   // Consume the first n prompt tokens (host copy `prompt`, device copy
@@ -149,10 +150,12 @@ class Engine {
   struct PrefillBuffers {
     uint16_t *h, *u, *raw, *z, *a, *b, *q, *k, *v, *y, *gated, *qp, *kp, *vp, *query, *o, *gate, *up, *act;
     float *g, *beta;
-  } pf_[2]{};
-  hipStream_t pstream_[2] = {nullptr, nullptr};
-  hipEvent_t state_done_[2][64] = {};  // [slot][layer]: the chunk's update of that layer's state
-  hipEvent_t join_ev_[3] = {nullptr, nullptr, nullptr};
+  };
+  static constexpr int kPrefillStreams = 2;
+  PrefillBuffers pf_[kPrefillStreams]{};
+  hipStream_t pstream_[kPrefillStreams] = {};
+  hipEvent_t state_done_[kPrefillStreams][64] = {};  // [slot][layer]: the chunk's update of that layer's state
+  hipEvent_t join_ev_[1 + kPrefillStreams] = {};
 
   struct GraphEntry {
     int kind;
