@@ -452,8 +452,9 @@ int Engine::generate(const uint32_t* prompt, int len, int count, bool reset, uin
 }
 
 int Engine::set_prefill(int chunk_rows, std::string* err) {
-  if (chunk_rows < 0 || chunk_rows == 1 || chunk_rows > (1 << 20)) {
-    if (err) *err = "prefill chunk rows must be 0 or 2 .. 2^20";
+  // rows x 6144 element counts of the chunk buffers stay below 2^31
+  if (chunk_rows < 0 || chunk_rows == 1 || chunk_rows > 65536) {
+    if (err) *err = "prefill chunk rows must be 0 or 2 .. 65536";
     return 1;
   }
   prefill_rows_ = chunk_rows;

@@ -777,7 +777,7 @@ hipError_t launch_attn_prefill(const uint16_t* qr, const uint16_t* kcache, const
 
 hipError_t launch_attn_gate_rows(const uint16_t* o, const uint16_t* qg, int m, uint16_t* gated,
                                  hipStream_t s) {
-  if (!o || !qg || !gated || m < 1) return hipErrorInvalidValue;
+  if (!o || !qg || !gated || m < 1 || m > (1 << 20) - 1) return hipErrorInvalidValue;  // m * 2048 < 2^31
   hipLaunchKernelGGL(k_attn_gate_rows, dim3((m * 2048 + 255) / 256), dim3(256), 0, s, o, qg, m, gated);
   return hipGetLastError();
 }

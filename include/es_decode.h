@@ -304,7 +304,7 @@ int es_engine_generate(es_engine* e, const uint32_t* prompt, int len, int max_to
  * model.rs:7): chunk_rows >= 2 consumes prompt[0 .. len-1) in batched
  * forwards of at most chunk_rows rows (the row operators above; a chunk of
  * one row runs the decode kernels, as forward with rows == 1 does), default
- * 4096; 0 replays one decode step per prompt token. Results do not depend on
+ * 4096, at most 65536; 0 replays one decode step per prompt token. Results do not depend on
  * the chunk size (except that a one-row chunk runs the decode kernels).
  * Consecutive chunks run on two streams, one layer apart. Batched prefill
  * allocates two sets of chunk buffers (about 81 KB per row each) on first

@@ -161,3 +161,5 @@ def test_set_prefill_rejects_one_row_chunks(small):
         eng.set_prefill(1)
     with pytest.raises(E.EsError):
         eng.set_prefill(-2)
+    with pytest.raises(E.EsError, match="65536"):
+        eng.set_prefill(65537)
