@@ -69,3 +69,31 @@ def test_full_model_teacher_forced_agreement(full):
     for (_, _, _, gap, _) in bad:
         assert gap <= 0.1, "a mismatch must be a near tie"
     assert rate >= 0.95
+
+
+@pytest.mark.parametrize("ctx,steps", [(32768, 24), (131072, 12)])
+def test_long_context_agreement_after_batched_prefill(ctx, steps):
+    """Full model: a prompt of `ctx` uniform-random ids consumed by the
+    batched prefill, then greedy tokens; the post-prefill state is handed to
+    the oracle and the stream judged teacher-forced (the harness's gates;
+    every mismatch a near tie)."""
+    from judge import gates
+    print(f"case long context {ctx}", flush=True)
+    blob = E.random_weights(N_LAYERS, VOCAB, seed=20260101, threads=16)
+    eng = E.Engine(blob, N_LAYERS, VOCAB, capacity=ctx + steps + 8)
+    try:
+        prompt = rng(ctx).integers(0, VOCAB, ctx).tolist()
+        first = eng.generate(prompt, 1, reset=True)[0]
+        pos = eng.position
+        orc = O.OracleModel(E.tensor_views(blob, N_LAYERS, VOCAB), N_LAYERS, VOCAB, capacity=pos + steps + 4)
+        handoff(eng, orc, pos)
+        stream = eng.generate([], steps, reset=False)
+    finally:
+        eng.close()
+    O.set_threads(16)
+    bad = judge(orc, first, stream)
+    print(f"ctx {ctx}: {steps - len(bad)}/{steps} steps agree: {bad}")
+    cases = [(steps, [(i, gap, tok, 1) for i, tok, _, gap, _ in bad])]
+    assert gates(cases) == []
+    for (_, _, _, gap, _) in bad:
+        assert gap <= 0.1, "a mismatch must be a near tie"
