@@ -173,12 +173,15 @@ int Engine::init(const void* blob, uint64_t bytes, std::string* err) {
   float inv_freq[32];
   for (int i = 0; i < 32; ++i) inv_freq[i] = rope_inv_freq_host(i);
   ES_HIP(hipMemcpy(inv_freq_, inv_freq, sizeof(inv_freq), hipMemcpyHostToDevice), "inv_freq");
-  ES_HIP(hipMemset(h_, 0, 1024 * 2), "memset");
+  // Clears go on the engine stream: a null-stream memset is asynchronous and
+  // not ordered with this non-blocking stream, so a late one could zero K/V
+  // rows the first steps have already written.
+  ES_HIP(hipMemsetAsync(h_, 0, 1024 * 2, stream_), "memset");
   for (auto& L : layers_)
     if (L.attention) {
       const size_t cache = (size_t)2 * capacity_ * 256 * sizeof(uint16_t);
-      ES_HIP(hipMemset(L.kcache, 0, cache), "memset kv");
-      ES_HIP(hipMemset(L.vcache, 0, cache), "memset kv");
+      ES_HIP(hipMemsetAsync(L.kcache, 0, cache, stream_), "memset kv");
+      ES_HIP(hipMemsetAsync(L.vcache, 0, cache, stream_), "memset kv");
     }
   reset_state();
   ES_HIP(hipStreamSynchronize(stream_), "init sync");
