@@ -163,3 +163,28 @@ def test_set_prefill_rejects_one_row_chunks(small):
         eng.set_prefill(-2)
     with pytest.raises(E.EsError, match="65536"):
         eng.set_prefill(65537)
+
+
+def test_prompt_filling_the_whole_capacity(small):
+    """A 4096-token prompt on a 4096-row engine (the last decode step writes
+    the last cache row; attention key blocks end at the capacity): one
+    4096-row chunk and chunks of 1000 give the same token and state."""
+    eng, _ = small
+    prompt = rng(4096).integers(0, SMALL["vocab"], 4096).tolist()
+    runs = []
+    try:
+        for rows in (4096, 1000):
+            eng.set_prefill(rows)
+            tok = eng.generate(prompt, 1, reset=True)
+            assert eng.position == 4096
+            runs.append((tok, engine_state(eng, 4096)))
+    finally:
+        eng.set_prefill(4096)
+    (t0, (g0, k0)), (t1, (g1, k1)) = runs
+    assert t0 == t1
+    for l in g0:
+        assert np.array_equal(g0[l][1].view(np.uint32), g1[l][1].view(np.uint32))
+    for l in k0:
+        assert np.array_equal(k0[l][0], k1[l][0]) and np.array_equal(k0[l][1], k1[l][1])
+    with pytest.raises(E.EsError, match="capacity"):
+        eng.generate(prompt + [1], 1, reset=True)
