@@ -165,6 +165,16 @@ int es_q4_gemm(const es_q4* w, const uint16_t* x, int rows, const uint16_t* resi
   return hip_status(es::launch_q4_gemm(m, x, rows, residual, y, S(stream)), "es_q4_gemm");
 }
 
+int es_q4_gemm_swiglu(const es_q4* gate, const es_q4* up, const uint16_t* x, int rows, uint16_t* act,
+                      void* stream) {
+  es::Q4 g, u;
+  if (!to_q4(gate, &g) || !to_q4(up, &u) || !x || !act) return fail(ES_ERR_INVALID, "es_q4_gemm_swiglu: null argument");
+  if (rows < 1 || g.k % 64 != 0 || g.n != u.n || g.k != u.k)
+    return fail(ES_ERR_INVALID, "es_q4_gemm_swiglu: rows >= 1, k % 64 == 0 and equal gate/up shapes required");
+  if (x == act) return fail(ES_ERR_INVALID, "es_q4_gemm_swiglu: x must not alias act");
+  return hip_status(es::launch_q4_gemm_swiglu(g, u, x, rows, act, S(stream)), "es_q4_gemm_swiglu");
+}
+
 // ---- prefill row operators ----
 int es_embed_rows(const es_q4* embed, const uint32_t* tokens, int rows, uint16_t* h, void* stream) {
   es::Q4 e;

@@ -486,9 +486,9 @@ int Engine::ensure_prefill_buffers(std::string* err) {
   for (int slot = 0; slot < kPrefillStreams; ++slot) {
     PrefillBuffers b{};
     uint16_t** bf[] = {&b.h, &b.u, &b.raw, &b.z, &b.a, &b.b, &b.q, &b.k, &b.v, &b.y, &b.gated, &b.qp, &b.kp,
-                       &b.vp, &b.query, &b.o, &b.gate, &b.up, &b.act};
+                       &b.vp, &b.query, &b.o, &b.act};
     const size_t width[] = {1024, 1024, 6144, 2048, 16, 16, 2048, 2048, 2048, 2048, 2048, 4096, 512,
-                            512, 2048, 2048, 3584, 3584, 3584};
+                            512, 2048, 2048, 3584};
     for (size_t i = 0; i < sizeof(width) / sizeof(width[0]); ++i) {
       *bf[i] = static_cast<uint16_t*>(alloc(r * width[i] * 2));
       if (!*bf[i]) {
@@ -554,9 +554,7 @@ int Engine::prefill_rows(int pos0, int m, int slot, bool wait_prev, std::string*
       ES_HIP(launch_q4_gemm(L.o, b.gated, m, b.h, b.h, s), "prefill o_proj");
     }
     ES_HIP(launch_rmsnorm_rows(b.h, L.post_norm, m, b.u, s), "prefill post norm");
-    ES_HIP(launch_q4_gemm(L.gate, b.u, m, nullptr, b.gate, s), "prefill gate");
-    ES_HIP(launch_q4_gemm(L.up, b.u, m, nullptr, b.up, s), "prefill up");
-    ES_HIP(launch_swiglu_rows(b.gate, b.up, m * 3584, b.act, s), "prefill swiglu");
+    ES_HIP(launch_q4_gemm_swiglu(L.gate, L.up, b.u, m, b.act, s), "prefill gate/up/swiglu");
     ES_HIP(launch_q4_gemm(L.down, b.act, m, b.h, b.h, s), "prefill down");
   }
   return 0;

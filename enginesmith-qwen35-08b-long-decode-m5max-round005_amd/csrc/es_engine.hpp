@@ -148,7 +148,7 @@ class Engine {
   int prefill_rows_ = kDefaultPrefillRows;
   int prefill_alloc_rows_ = 0;
   struct PrefillBuffers {
-    uint16_t *h, *u, *raw, *z, *a, *b, *q, *k, *v, *y, *gated, *qp, *kp, *vp, *query, *o, *gate, *up, *act;
+    uint16_t *h, *u, *raw, *z, *a, *b, *q, *k, *v, *y, *gated, *qp, *kp, *vp, *query, *o, *act;
     float *g, *beta;
   };
   static constexpr int kPrefillStreams = 2;

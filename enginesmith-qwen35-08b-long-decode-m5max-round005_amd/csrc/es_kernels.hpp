@@ -128,6 +128,10 @@ hipError_t launch_attn_merge_out(const AttnArgs& a, const Q4& o, float* part, hi
 // K a multiple of 64. Y may alias R.
 hipError_t launch_q4_gemm(const Q4& w, const uint16_t* x, int m, const uint16_t* residual, uint16_t* y,
                           hipStream_t s);
+// MLP gate/up linears with SwiGLU in one GEMM (the same results as the two
+// row-batched linears followed by swiglu_bf16): act [m, gate.n].
+hipError_t launch_q4_gemm_swiglu(const Q4& gate, const Q4& up, const uint16_t* x, int m, uint16_t* act,
+                                 hipStream_t s);
 // Row forms of the decode operators (m rows = consecutive positions
 // pos0 .. pos0+m-1), each with the decode kernels' arithmetic per row.
 hipError_t launch_embed_rows(const Q4& e, const uint32_t* tokens, int m, uint16_t* h, hipStream_t s);

@@ -34,21 +34,30 @@ __device__ __forceinline__ uint32_t pack2(float lo, float hi) {
   return (uint32_t)f2bf(lo) | ((uint32_t)f2bf(hi) << 16);
 }
 
-__global__ __launch_bounds__(256) void k_q4_gemm(Q4 w, const uint16_t* __restrict__ x, int m,
+// GATEUP: w is the gate matrix and w2 the up matrix of the MLP; the block's
+// 128 staged W rows are gate rows n0 + 0..31, up rows n0 + 0..31, gate rows
+// n0 + 32..63, up rows n0 + 32..63, so each wave holds a gate and an up
+// accumulator for the same 32 columns and writes
+// act = bf16(bf16(g * sigmoid_bf(g)) * u) with g, u the bf16-rounded GEMM
+// outputs (swiglu_bf16 after the two linears), y [m, N] with N = w.n.
+template <bool GATEUP>
+__global__ __launch_bounds__(256) void k_q4_gemm(Q4 w, Q4 w2, const uint16_t* __restrict__ x, int m,
                                                  const uint16_t* residual, uint16_t* y) {
   __shared__ __attribute__((aligned(16))) uint16_t xs[2][kGemmBM][kGemmLds];
   __shared__ __attribute__((aligned(16))) uint16_t ws[2][kGemmBN][kGemmLds];
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
-  const int n0 = blockIdx.x * kGemmBN, m0 = blockIdx.y * kGemmBM;
+  const int n0 = blockIdx.x * (GATEUP ? kGemmBN / 2 : kGemmBN), m0 = blockIdx.y * kGemmBM;
   const int K = w.k, N = w.n;
   const int wpr = K >> 3, gpr = K >> 6;
   // loader roles: X row t/2, 32 columns (t&1); W row t/2, 32 nibbles (t&1)
   const int lr = t >> 1, lh = t & 1;
-  const bool xrow_ok = m0 + lr < m, wrow_ok = n0 + lr < N;
+  const Q4& wsrc = (GATEUP && ((lr >> 5) & 1)) ? w2 : w;
+  const int wr = GATEUP ? n0 + (lr >> 6) * 32 + (lr & 31) : n0 + lr;
+  const bool xrow_ok = m0 + lr < m, wrow_ok = wr < N;
   const uint16_t* xrow = x + (size_t)(xrow_ok ? m0 + lr : 0) * K + lh * 32;
-  const uint32_t* wrow = w.w + (size_t)(wrow_ok ? n0 + lr : 0) * wpr + lh * 4;
-  const uint16_t* srow = w.s + (size_t)(wrow_ok ? n0 + lr : 0) * gpr;
-  const uint16_t* brow = w.b + (size_t)(wrow_ok ? n0 + lr : 0) * gpr;
+  const uint32_t* wrow = wsrc.w + (size_t)(wrow_ok ? wr : 0) * wpr + lh * 4;
+  const uint16_t* srow = wsrc.s + (size_t)(wrow_ok ? wr : 0) * gpr;
+  const uint16_t* brow = wsrc.b + (size_t)(wrow_ok ? wr : 0) * gpr;
 
   auto load = [&](int kb, GemmStage& g) {
     const u32x4* xp = reinterpret_cast<const u32x4*>(xrow + kb * kGemmBK);
@@ -115,6 +124,22 @@ __global__ __launch_bounds__(256) void k_q4_gemm(Q4 w, const uint16_t* __restric
     __syncthreads();
   }
 
+  if (GATEUP) {
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int col = n0 + wn / 2 + fr;
+      if (col >= N) continue;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int row = m0 + wm + 32 * i + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+        if (row >= m) continue;
+        const float gb = rbf(acc[i][0][r]), ub = rbf(acc[i][1][r]);
+        const float silu = rbf(gb * sigmoid_bf(gb));
+        y[(size_t)row * N + col] = (uint16_t)f2bf(silu * ub);
+      }
+    }
+    return;
+  }
   // epilogue: bf16 output, or bf16(residual + bf16(acc))
 #pragma unroll
   for (int i = 0; i < 2; ++i)
@@ -704,7 +729,17 @@ hipError_t launch_q4_gemm(const Q4& w, const uint16_t* x, int m, const uint16_t*
   if (!w.w || !w.s || !w.b || w.n < 1 || w.k < kGemmBK || w.k % kGemmBK != 0 || !x || !y || m < 1)
     return hipErrorInvalidValue;
   const dim3 grid((w.n + kGemmBN - 1) / kGemmBN, (m + kGemmBM - 1) / kGemmBM);
-  hipLaunchKernelGGL(k_q4_gemm, grid, dim3(256), 0, s, w, x, m, residual, y);
+  hipLaunchKernelGGL(k_q4_gemm<false>, grid, dim3(256), 0, s, w, w, x, m, residual, y);
+  return hipGetLastError();
+}
+
+hipError_t launch_q4_gemm_swiglu(const Q4& gate, const Q4& up, const uint16_t* x, int m, uint16_t* act,
+                                 hipStream_t s) {
+  if (!gate.w || !gate.s || !gate.b || !up.w || !up.s || !up.b || gate.n != up.n || gate.k != up.k ||
+      gate.n < 1 || gate.k < kGemmBK || gate.k % kGemmBK != 0 || !x || !act || m < 1)
+    return hipErrorInvalidValue;
+  const dim3 grid((gate.n + kGemmBN / 2 - 1) / (kGemmBN / 2), (m + kGemmBM - 1) / kGemmBM);
+  hipLaunchKernelGGL(k_q4_gemm<true>, grid, dim3(256), 0, s, gate, up, x, m, nullptr, act);
   return hipGetLastError();
 }
 

@@ -75,6 +75,7 @@ _SIGNATURES = {
                                        POINTER(c_int)]),
     "es_weights_random": (c_int, [c_int, c_int, c_uint64, c_void_p, c_size_t, c_int]),
     "es_q4_gemm": (c_int, [POINTER(Q4), c_void_p, c_int, c_void_p, c_void_p, c_void_p]),
+    "es_q4_gemm_swiglu": (c_int, [POINTER(Q4), POINTER(Q4), c_void_p, c_int, c_void_p, c_void_p]),
     "es_embed_rows": (c_int, [POINTER(Q4), c_void_p, c_int, c_void_p, c_void_p]),
     "es_rmsnorm_rows": (c_int, [c_void_p, c_void_p, c_int, c_void_p, c_void_p]),
     "es_swiglu_rows": (c_int, [c_void_p, c_void_p, c_int, c_void_p, c_void_p]),

@@ -101,6 +101,13 @@ int es_q4_matvec_add(const es_q4* w, const uint16_t* x, const uint16_t* residual
 int es_q4_gemm(const es_q4* w, const uint16_t* x, int rows, const uint16_t* residual, uint16_t* y,
                void* stream);
 
+/* The MLP's row-batched gate and up linears and swiglu_bf16 (model.rs:
+ * 279-282; linear.metal:382-398) in one GEMM: act [rows, n] =
+ * bf16(bf16(g * sigmoid(g)) * u) with g, u the bf16 outputs es_q4_gemm gives
+ * for gate and up; bitwise the same as those three operators. */
+int es_q4_gemm_swiglu(const es_q4* gate, const es_q4* up, const uint16_t* x, int rows, uint16_t* act,
+                      void* stream);
+
 /* ------------------------------------------------------------------ */
 /* Prefill row operators (encode_forward with rows > 1, model.rs:228-343) */
 /* ------------------------------------------------------------------ */

@@ -66,3 +66,23 @@ def test_q4_gemm_rejects_bad_arguments():
     dy = E.DeviceBuffer(4096)
     assert E.lib().es_q4_gemm(W.struct, dx.ptr, 0, None, dy.ptr, None) != E.ES_OK
     assert E.lib().es_q4_gemm(W.struct, dx.ptr, 1, None, dx.ptr, None) != E.ES_OK
+
+
+@pytest.mark.parametrize("m", [1, 130, 257])
+def test_gemm_swiglu_equals_two_gemms_and_swiglu(m):
+    """The fused gate/up GEMM with the SwiGLU epilogue gives, bit for bit,
+    es_q4_gemm on gate and on up followed by es_swiglu_rows."""
+    print(f"case gemm swiglu m={m}", flush=True)
+    r = rng(6000 + m)
+    n, k = 3584, 1024
+    G = E.DeviceQ4(*random_q4(r, n, k))
+    U = E.DeviceQ4(*random_q4(r, n, k))
+    x = bf16(r.normal(0, 1, (m, k)))
+    dx = E.DeviceBuffer.from_numpy(x)
+    dg, du, da, df = (E.DeviceBuffer(m * n * 2) for _ in range(4))
+    E.check(E.lib().es_q4_gemm(G.struct, dx.ptr, m, None, dg.ptr, None))
+    E.check(E.lib().es_q4_gemm(U.struct, dx.ptr, m, None, du.ptr, None))
+    E.check(E.lib().es_swiglu_rows(dg.ptr, du.ptr, m * n, da.ptr, None))
+    E.check(E.lib().es_q4_gemm_swiglu(G.struct, U.struct, dx.ptr, m, df.ptr, None))
+    E.synchronize()
+    assert np.array_equal(da.numpy(np.uint16), df.numpy(np.uint16))
