@@ -314,7 +314,7 @@ int es_engine_generate(es_engine* e, const uint32_t* prompt, int len, int max_to
  * 4096, at most 65536; 0 replays one decode step per prompt token. Results do not depend on
  * the chunk size (except that a one-row chunk runs the decode kernels).
  * Consecutive chunks run on two streams, one layer apart. Batched prefill
- * allocates two sets of chunk buffers (about 81 KB per row each) on first
+ * allocates two sets of chunk buffers (about 67 KB per row each) on first
  * use. */
 int es_engine_set_prefill(es_engine* e, int chunk_rows);
 
