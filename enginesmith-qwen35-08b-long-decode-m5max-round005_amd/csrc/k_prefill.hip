@@ -203,53 +203,65 @@ __global__ __launch_bounds__(256) void k_swiglu_rows(const uint16_t* gate, const
 }
 
 // GDN prepare rows (gdn_conv + gdn_prepare, gdn.metal:33-120, with the decode
-// kernels' arithmetic): one wave per (row, head). Lane i takes channels i and
+// kernels' arithmetic): one wave per (4 consecutive rows, head), which loads
+// the 7 input rows the 4 rows' taps span once. Lane i takes channels i and
 // 64+i of the head's q, k and v: causal conv over taps (pos-3 .. pos) whose
 // inputs are the chunk's raw rows, or the ring for positions before the
 // chunk; SiLU; q and k L2-normalised (sum of squares tree64 over channels
 // 0..63 plus tree64 over 64..127) and scaled (q by 1/128, k by bf16(128^-1/2));
 // lane 0 forms the gates g = exp(-exp(A_log)*softplus(bf16(a+dt))), beta =
 // sigmoid_bf(b). Outputs bf16 q, k, v [m,16,128] and fp32 g, beta [m,16].
+constexpr int kPrepRows = 4;  // rows per wave: their taps span kPrepRows + 3 input rows
 __global__ __launch_bounds__(256) void k_gdn_prep_rows(const uint16_t* raw, const uint16_t* ring,
                                                        const uint16_t* conv_w, const uint16_t* a_proj,
                                                        const uint16_t* b_proj, const float* a_log,
                                                        const uint16_t* dt_bias, int pos0, int m,
                                                        uint16_t* q, uint16_t* k, uint16_t* v, float* g,
                                                        float* beta) {
-  const int lane = threadIdx.x & 63, h = blockIdx.y * 4 + (threadIdx.x >> 6), t = blockIdx.x;
-  if (t >= m) return;
-  const int pos = pos0 + t;
-  float out[3][2];
+  const int lane = threadIdx.x & 63, h = blockIdx.y * 4 + (threadIdx.x >> 6);
+  const int t0 = blockIdx.x * kPrepRows;
+  if (t0 >= m) return;
+  const int nr = min(kPrepRows, m - t0);
+  float out[3][2][kPrepRows];
 #pragma unroll
   for (int part = 0; part < 3; ++part)
 #pragma unroll
     for (int half = 0; half < 2; ++half) {
       const int c = part * 2048 + h * 128 + half * 64 + lane;
-      uint32_t x[4];
+      // input rows t0-3 .. t0+kPrepRows-1: the chunk's raw rows, or the ring
+      // for positions before the chunk; rows past the chunk are not used
+      uint32_t x[kPrepRows + 3];
 #pragma unroll
-      for (int tap = 0; tap < 4; ++tap) {
-        const int tt = t - 3 + tap;
-        x[tap] = tt >= 0 ? raw[(size_t)tt * kConv + c] : ring[(size_t)((pos - 3 + tap) & 3) * kConv + c];
+      for (int i = 0; i < kPrepRows + 3; ++i) {
+        const int tt = t0 - 3 + i;
+        x[i] = tt >= 0 ? (tt < m ? raw[(size_t)tt * kConv + c] : 0u)
+                       : ring[(size_t)((pos0 + tt) & 3) * kConv + c];
       }
       const uint2 w = *reinterpret_cast<const uint2*>(conv_w + (size_t)c * 4);
-      out[part][half] = conv4_silu(x, w);
-    }
-  const size_t o = ((size_t)t * 16 + h) * 128;
 #pragma unroll
-  for (int part = 0; part < 2; ++part) {
-    const float tot = tree64(out[part][0] * out[part][0]) + tree64(out[part][1] * out[part][1]);
-    const float inv = 1.0f / sqrtf(tot / 128.0f + 1.0e-6f / 128.0f);
-    const float scale = part == 0 ? 0.0078125f : rbf(0.08838834764831845f);
-    uint16_t* dst = part == 0 ? q : k;
-    dst[o + lane] = (uint16_t)f2bf(rbf(out[part][0] * inv) * scale);
-    dst[o + 64 + lane] = (uint16_t)f2bf(rbf(out[part][1] * inv) * scale);
-  }
-  v[o + lane] = (uint16_t)f2bf(out[2][0]);
-  v[o + 64 + lane] = (uint16_t)f2bf(out[2][1]);
-  if (lane == 0) {
-    const float ax = rbf(bf2f(a_proj[(size_t)t * 16 + h]) + bf2f(dt_bias[h]));
-    g[(size_t)t * 16 + h] = es_exp(-es_exp(a_log[h]) * softplus_bf(ax));
-    beta[(size_t)t * 16 + h] = sigmoid_bf(bf2f(b_proj[(size_t)t * 16 + h]));
+      for (int r = 0; r < kPrepRows; ++r) out[part][half][r] = conv4_silu(x + r, w);
+    }
+#pragma unroll
+  for (int r = 0; r < kPrepRows; ++r) {
+    if (r >= nr) break;
+    const int t = t0 + r;
+    const size_t o = ((size_t)t * 16 + h) * 128;
+#pragma unroll
+    for (int part = 0; part < 2; ++part) {
+      const float tot = tree64(out[part][0][r] * out[part][0][r]) + tree64(out[part][1][r] * out[part][1][r]);
+      const float inv = 1.0f / sqrtf(tot / 128.0f + 1.0e-6f / 128.0f);
+      const float scale = part == 0 ? 0.0078125f : rbf(0.08838834764831845f);
+      uint16_t* dst = part == 0 ? q : k;
+      dst[o + lane] = (uint16_t)f2bf(rbf(out[part][0][r] * inv) * scale);
+      dst[o + 64 + lane] = (uint16_t)f2bf(rbf(out[part][1][r] * inv) * scale);
+    }
+    v[o + lane] = (uint16_t)f2bf(out[2][0][r]);
+    v[o + 64 + lane] = (uint16_t)f2bf(out[2][1][r]);
+    if (lane == 0) {
+      const float ax = rbf(bf2f(a_proj[(size_t)t * 16 + h]) + bf2f(dt_bias[h]));
+      g[(size_t)t * 16 + h] = es_exp(-es_exp(a_log[h]) * softplus_bf(ax));
+      beta[(size_t)t * 16 + h] = sigmoid_bf(bf2f(b_proj[(size_t)t * 16 + h]));
+    }
   }
 }
 
@@ -770,8 +782,8 @@ hipError_t launch_gdn_prep_rows(const GdnPrepRowsArgs& a, hipStream_t s) {
   if (!a.raw || !a.ring || !a.conv_w || !a.a_proj || !a.b_proj || !a.a_log || !a.dt_bias || a.m < 1 ||
       a.pos0 < 0 || !a.q || !a.k || !a.v || !a.g || !a.beta)
     return hipErrorInvalidValue;
-  hipLaunchKernelGGL(k_gdn_prep_rows, dim3(a.m, 4), dim3(256), 0, s, a.raw, a.ring, a.conv_w, a.a_proj,
-                     a.b_proj, a.a_log, a.dt_bias, a.pos0, a.m, a.q, a.k, a.v, a.g, a.beta);
+  hipLaunchKernelGGL(k_gdn_prep_rows, dim3((a.m + kPrepRows - 1) / kPrepRows, 4), dim3(256), 0, s, a.raw, a.ring,
+                     a.conv_w, a.a_proj, a.b_proj, a.a_log, a.dt_bias, a.pos0, a.m, a.q, a.k, a.v, a.g, a.beta);
   if (hipGetLastError() != hipSuccess) return hipErrorLaunchFailure;
   hipLaunchKernelGGL(k_ring_update, dim3((4 * kConv + 255) / 256), dim3(256), 0, s, a.raw, a.pos0, a.m,
                      a.ring);
