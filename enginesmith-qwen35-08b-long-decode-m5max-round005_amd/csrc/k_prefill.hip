@@ -524,60 +524,60 @@ __global__ __launch_bounds__(256) void k_attn_gate_rows(const uint16_t* o, const
 // Causal GQA attention of m consecutive queries (positions pos0 .. pos0+m-1)
 // over the cache (attn_prefill, attention_prefill.metal:2256; model.rs:337-343):
 // o = bf16(softmax(q.K^T / 16) . V), fp32 softmax, MFMA products.
-// Block = (32 queries, KV head), wave w = query head 4*kvh + w. Per block of
-// 32 keys: S^T = K . Q^T (32x32x16 MFMA, K from LDS, the wave's Q fragments
-// held in registers), so lane l holds 16 scores of query l%32 (keys
-// 8(r/4) + 4(l/32) + r%4): the online-softmax max, sum and rescale are
-// per-lane values with one exchange between lanes l and l^32. The exp'ed
-// scores, rounded to bf16, are then directly the B operand of
-// O^T += V^T . P^T, with the MFMA's k index j of lane half h standing for key
-// (j < 4 ? 4h + j : 8 + 4h + j - 4) (+16 for the second step). Exponentials
-// are base 2 on scores scaled by log2(e)/16.
+// Block = (32 queries, KV head), 8 waves, two per SIMD: wave w serves query
+// head 4*kvh + (w & 3) for queries 16(w >> 2) .. +15 of the tile. Per block of
+// 32 keys, S^T = K . Q^T on 16x16x32 MFMAs (two 16-key tiles, K from LDS, the
+// wave's Q fragments in registers): lane l holds 8 scores of query l%16, keys
+// 4g + r and 16 + 4g + r (g = l/16, r = 0..3), so the online-softmax max and
+// sum combine 4 lanes with two row exchanges. The exp'ed scores, rounded to
+// bf16, are directly the B operand of O^T += V^T . P^T, with the MFMA's k index
+// 8g + j standing for key (j < 4 ? 4g + j : 16 + 4g + j - 4). Exponentials are
+// base 2 on scores scaled by log2(e)/16.
 //
 // K and V blocks reach LDS by DMA (global_load_lds, 16 bytes a lane, no
 // registers), kFaStages blocks deep: block kb + kFaStages - 1 is issued while
 // block kb is computed. One DMA instruction moves one 512-byte row (32
-// lanes); K rows sit 528 bytes apart and V rows 576 bytes apart, strides at
-// which the K reads (32 rows, one 16-byte column) and the transposing V reads
-// (ds_read_b64_tr_b16: 8 rows x 64 bytes) spread over the banks. The
+// lanes); K rows sit 528 bytes apart and V rows 544 bytes apart, strides at
+// which the K reads (16 rows x 4 chunks) and the transposing V reads
+// (ds_read_b64_tr_b16: 16 rows x 32 bytes) spread evenly over the banks. The
 // transposing read gives lane i of each 16-lane group element i of the 4 rows
-// x 16 columns its lanes address: lane l gets V[4 keys][d = l%32] for its
-// A-operand k indices. It is issued as inline assembly with its own
-// lgkmcnt wait, which keeps the compiler from waiting for every DMA in
-// flight before it.
-constexpr int kFaQ = 32, kFaStages = 4, kFaKs = 264, kFaVs = 288;
+// x 16 columns its lanes address: lane l gets V[4 keys][d = 16t + l%16]. It is
+// issued as inline assembly with its own lgkmcnt wait, which keeps the
+// compiler from waiting for every DMA in flight before it.
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+constexpr int kFaQ = 32, kFaStages = 4, kFaKs = 264, kFaVs = 272;
 constexpr int kFaStageHalves = 32 * kFaKs + 32 * kFaVs;
 template <int N>
 __device__ __forceinline__ void wait_vmcnt() {
   __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
 }
-// eight transposing reads: at a + 64*i and b + 64*i bytes (i = 0..3: four
-// 32-dim tiles of the two key groups), then one wait for all of them
-__device__ __forceinline__ void lds_read_tr16_x8(uint32_t a, uint32_t b, uint2 (&ra)[4], uint2 (&rb)[4]) {
-  uint64_t x0, x1, x2, x3, y0, y1, y2, y3;
+// eight transposing reads at a + 32*i bytes (i = 0..7: eight 16-dim tiles),
+// then their wait
+__device__ __forceinline__ void lds_read_tr16_x8(uint32_t a, uint2 (&r)[8]) {
+  uint64_t x0, x1, x2, x3, x4, x5, x6, x7;
   asm volatile(
       "ds_read_b64_tr_b16 %0, %8\n\t"
-      "ds_read_b64_tr_b16 %1, %8 offset:64\n\t"
-      "ds_read_b64_tr_b16 %2, %8 offset:128\n\t"
-      "ds_read_b64_tr_b16 %3, %8 offset:192\n\t"
-      "ds_read_b64_tr_b16 %4, %9\n\t"
-      "ds_read_b64_tr_b16 %5, %9 offset:64\n\t"
-      "ds_read_b64_tr_b16 %6, %9 offset:128\n\t"
-      "ds_read_b64_tr_b16 %7, %9 offset:192\n\t"
+      "ds_read_b64_tr_b16 %1, %8 offset:32\n\t"
+      "ds_read_b64_tr_b16 %2, %8 offset:64\n\t"
+      "ds_read_b64_tr_b16 %3, %8 offset:96\n\t"
+      "ds_read_b64_tr_b16 %4, %8 offset:128\n\t"
+      "ds_read_b64_tr_b16 %5, %8 offset:160\n\t"
+      "ds_read_b64_tr_b16 %6, %8 offset:192\n\t"
+      "ds_read_b64_tr_b16 %7, %8 offset:224\n\t"
       "s_waitcnt lgkmcnt(0)"
-      : "=&v"(x0), "=&v"(x1), "=&v"(x2), "=&v"(x3), "=&v"(y0), "=&v"(y1), "=&v"(y2), "=&v"(y3)
-      : "v"(a), "v"(b)
+      : "=&v"(x0), "=&v"(x1), "=&v"(x2), "=&v"(x3), "=&v"(x4), "=&v"(x5), "=&v"(x6), "=&v"(x7)
+      : "v"(a)
       : "memory");
-  ra[0] = __builtin_bit_cast(uint2, x0);
-  ra[1] = __builtin_bit_cast(uint2, x1);
-  ra[2] = __builtin_bit_cast(uint2, x2);
-  ra[3] = __builtin_bit_cast(uint2, x3);
-  rb[0] = __builtin_bit_cast(uint2, y0);
-  rb[1] = __builtin_bit_cast(uint2, y1);
-  rb[2] = __builtin_bit_cast(uint2, y2);
-  rb[3] = __builtin_bit_cast(uint2, y3);
+  r[0] = __builtin_bit_cast(uint2, x0);
+  r[1] = __builtin_bit_cast(uint2, x1);
+  r[2] = __builtin_bit_cast(uint2, x2);
+  r[3] = __builtin_bit_cast(uint2, x3);
+  r[4] = __builtin_bit_cast(uint2, x4);
+  r[5] = __builtin_bit_cast(uint2, x5);
+  r[6] = __builtin_bit_cast(uint2, x6);
+  r[7] = __builtin_bit_cast(uint2, x7);
 }
-__global__ __launch_bounds__(256, 1) void k_attn_prefill(const uint16_t* qr, const uint16_t* kcache,
+__global__ __launch_bounds__(512, 1) void k_attn_prefill(const uint16_t* qr, const uint16_t* kcache,
                                                          const uint16_t* vcache, int pos0, int m,
                                                          int capacity, uint16_t* o) {
   __shared__ __attribute__((aligned(16))) uint16_t kv[kFaStages][kFaStageHalves];
@@ -589,32 +589,32 @@ __global__ __launch_bounds__(256, 1) void k_attn_prefill(const uint16_t* qr, con
   const int b = blockIdx.x, xcd = b & 7;
   const int tile = 4 * (b >> 3) + (xcd >> 1);
   if (tile * kFaQ >= m) return;
-  const int t0 = tile * kFaQ, kvh = xcd & 1, hq = 4 * kvh + wave;
-  const int ql = lane & 31, hh = lane >> 5;
-  const int qrow = t0 + ql;
+  const int t0 = tile * kFaQ, kvh = xcd & 1, hq = 4 * kvh + (wave & 3);
+  const int qi = lane & 15, g = lane >> 4;
+  const int qrow = t0 + 16 * (wave >> 2) + qi;
   const bool qvalid = qrow < m;
   const int qpos = pos0 + (qvalid ? qrow : m - 1);
   const int last_key = pos0 + min(t0 + kFaQ, m) - 1;
   const int nkb = last_key / 32 + 1;
-  // Q fragments: B operand of step s holds Q[q][16s + 8hh .. +7]
-  bf16x8 qf[16];
+  // Q fragments: B operand of k-step s holds Q[q][32s + 8g .. +7]
+  bf16x8 qf[8];
   {
-    const uint16_t* qp = qr + ((size_t)(qvalid ? qrow : 0) * 8 + hq) * 256 + 8 * hh;
+    const uint16_t* qp = qr + ((size_t)(qvalid ? qrow : 0) * 8 + hq) * 256 + 8 * g;
 #pragma unroll
-    for (int s2 = 0; s2 < 16; ++s2) {
-      u32x4 v = *reinterpret_cast<const u32x4*>(qp + 16 * s2);
+    for (int s2 = 0; s2 < 8; ++s2) {
+      u32x4 v = *reinterpret_cast<const u32x4*>(qp + 32 * s2);
       if (!qvalid) v = u32x4{0u, 0u, 0u, 0u};
       qf[s2] = __builtin_bit_cast(bf16x8, v);
     }
   }
-  // DMA of one block of 32 keys: wave w moves rows 8w .. 8w+7 of K and V,
+  // DMA of one block of 32 keys: wave w moves rows 4w .. 4w+3 of K and V,
   // one row per instruction, lane L < 32 the row's 16-byte chunk L
   auto issue = [&](int kb) {
     uint16_t* stage = kv[kb % kFaStages];
     if (lane < 32) {
 #pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        const int r = 8 * wave + i;
+      for (int i = 0; i < 4; ++i) {
+        const int r = 4 * wave + i;
         const int key = min(kb * 32 + r, capacity - 1);
         const size_t row = ((size_t)kvh * capacity + key) * 256;  // uniform
         __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)(kcache + row + lane * 8),
@@ -626,112 +626,117 @@ __global__ __launch_bounds__(256, 1) void k_attn_prefill(const uint16_t* qr, con
     }
   };
   for (int kb = 0; kb < min(kFaStages - 1, nkb); ++kb) issue(kb);
-  f32x16 ot[8];
+  f32x4 ot[16];
 #pragma unroll
-  for (int dt = 0; dt < 8; ++dt)
+  for (int dt = 0; dt < 16; ++dt)
 #pragma unroll
-    for (int r = 0; r < 16; ++r) ot[dt][r] = 0.0f;
+    for (int r = 0; r < 4; ++r) ot[dt][r] = 0.0f;
   float mrun = -INFINITY, lrun = 0.0f;
   const float c = 0.0625f * 1.4426950408889634f;  // 1/16 * log2(e)
-  // V read roles (see above): lane address row 4(g/2) + j/4, columns
-  // 16(g%2) + 4(j%4) of the 32-dim tile, g = lane/16, j = lane%16
-  const int g16 = lane >> 4, j16 = lane & 15;
+  // V read roles (see above): lane address row K0 + (l%16)/4, columns
+  // 4((l%16)%4) of the first 16-dim tile, K0 = 4g (keys of k indices 0..3)
+  // or 16 + 4g (k indices 4..7)
   const uint32_t kv_base =
       (uint32_t)(uintptr_t)((const __attribute__((address_space(3))) uint16_t*)(&kv[0][0]));
-  const uint32_t v_lane = (uint32_t)(2 * (32 * kFaKs + (4 * (g16 >> 1) + (j16 >> 2)) * kFaVs +
-                                          16 * (g16 & 1) + 4 * (j16 & 3)));
+  const uint32_t v_lane = (uint32_t)(2 * (32 * kFaKs + (4 * g + (qi >> 2)) * kFaVs + 4 * (qi & 3)));
   for (int kb = 0; kb < nkb; ++kb) {
     // blocks issued after kb and still in flight: min(kFaStages - 2, nkb-1-kb),
-    // 16 DMA instructions each per wave
+    // 8 DMA instructions each per wave
     const int ahead = min(kFaStages - 2, nkb - 1 - kb);
     if (ahead >= 2)
-      wait_vmcnt<32>();
-    else if (ahead == 1)
       wait_vmcnt<16>();
+    else if (ahead == 1)
+      wait_vmcnt<8>();
     else
       wait_vmcnt<0>();
     __syncthreads();  // block kb visible; every wave is past block kb-1
     if (kb + kFaStages - 1 < nkb) issue(kb + kFaStages - 1);
     const uint16_t* ks = kv[kb % kFaStages];
     const uint32_t vs_addr = kv_base + (uint32_t)(2 * kFaStageHalves * (kb % kFaStages)) + v_lane;
-    // scores S^T[key][q] for the 32 keys of this block
-    f32x16 st;
+    // scores S^T[key][q] for the two 16-key tiles of this block
+    f32x4 st[2];
 #pragma unroll
-    for (int r = 0; r < 16; ++r) st[r] = 0.0f;
+    for (int kt = 0; kt < 2; ++kt) {
 #pragma unroll
-    for (int s2 = 0; s2 < 16; ++s2) {
-      const bf16x8 kf = *reinterpret_cast<const bf16x8*>(ks + ql * kFaKs + 16 * s2 + 8 * hh);
-      st = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf[s2], st, 0, 0, 0);
+      for (int r = 0; r < 4; ++r) st[kt][r] = 0.0f;
+#pragma unroll
+      for (int s2 = 0; s2 < 8; ++s2) {
+        const bf16x8 kf = *reinterpret_cast<const bf16x8*>(ks + (16 * kt + qi) * kFaKs + 32 * s2 + 8 * g);
+        st[kt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf, qf[s2], st[kt], 0, 0, 0);
+      }
     }
+    float x[8];
+#pragma unroll
+    for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) x[4 * kt + r] = st[kt][r];
     // causal mask (only blocks that reach past the tile's first query),
-    // online softmax for query ql; the maximum is taken on the raw scores
+    // online softmax for query qi; the maximum is taken on the raw scores
     // (scaling by c > 0 keeps the order) and the exponent is fma(s, c, -max)
     if (kb * 32 + 31 > pos0 + t0) {
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int key = kb * 32 + 8 * (r >> 2) + 4 * hh + (r & 3);
-        st[r] = key <= qpos ? st[r] : -INFINITY;
+      for (int e = 0; e < 8; ++e) {
+        const int key = kb * 32 + 16 * (e >> 2) + 4 * g + (e & 3);
+        x[e] = key <= qpos ? x[e] : -INFINITY;
       }
     }
-    float mloc = st[0];
+    float mloc = x[0];
 #pragma unroll
-    for (int r = 1; r < 16; ++r) mloc = fmaxf(mloc, st[r]);
-    const float2 mp = rows_xor32(mloc);
+    for (int e = 1; e < 8; ++e) mloc = fmaxf(mloc, x[e]);
+    const float2 m16 = rows_xor16(mloc);
+    const float2 m32 = rows_xor32(fmaxf(m16.x, m16.y));
     // The exponent's reference value moves only when the block's maximum
     // exceeds it by more than 8 (probabilities stay below 2^8; the output is
     // normalised by a sum taken against the same reference, so the softmax is
     // unchanged). The choice is per row, so a row's result depends on its own
     // scores only.
-    const float mblk = fmaxf(mp.x, mp.y) * c;
+    const float mblk = fmaxf(m32.x, m32.y) * c;
     const float mnew = mblk > mrun + 8.0f ? mblk : mrun;
     const float factor = __builtin_amdgcn_exp2f(mrun - mnew);
     float psum = 0.0f;
-    float pv[16];
+    float pv[8];
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      pv[r] = __builtin_amdgcn_exp2f(fmaf(st[r], c, -mnew));
-      psum += pv[r];
+    for (int e = 0; e < 8; ++e) {
+      pv[e] = __builtin_amdgcn_exp2f(fmaf(x[e], c, -mnew));
+      psum += pv[e];
     }
-    const float2 sp = rows_xor32(psum);
-    lrun = lrun * factor + (sp.x + sp.y);
+    const float2 s16 = rows_xor16(psum);
+    const float2 s32 = rows_xor32(s16.x + s16.y);
+    lrun = lrun * factor + (s32.x + s32.y);
     const float mrun_old = mrun;
     mrun = mnew;
     // factor is exactly 1 where the reference did not move: the rescale is
     // skipped unless some lane's reference moved
     if (__any(mnew > mrun_old)) {
 #pragma unroll
-      for (int dt = 0; dt < 8; ++dt)
+      for (int dt = 0; dt < 16; ++dt)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) ot[dt][r] *= factor;
+        for (int r = 0; r < 4; ++r) ot[dt][r] *= factor;
     }
-    // O^T += V^T . P^T, two 16-key steps
+    // O^T += V^T . P^T: one 32-key step per 16-dim tile
+    const u32x4 pb = u32x4{pack2(pv[0], pv[1]), pack2(pv[2], pv[3]), pack2(pv[4], pv[5]), pack2(pv[6], pv[7])};
+    const bf16x8 pf = __builtin_bit_cast(bf16x8, pb);
+    const uint32_t a_lo = vs_addr, a_hi = vs_addr + 2 * 16 * kFaVs;  // keys 4g.. and 16 + 4g..
 #pragma unroll
-    for (int ks2 = 0; ks2 < 2; ++ks2) {
-      const u32x4 pb = u32x4{pack2(pv[8 * ks2 + 0], pv[8 * ks2 + 1]), pack2(pv[8 * ks2 + 2], pv[8 * ks2 + 3]),
-                             pack2(pv[8 * ks2 + 4], pv[8 * ks2 + 5]), pack2(pv[8 * ks2 + 6], pv[8 * ks2 + 7])};
-      const bf16x8 pf = __builtin_bit_cast(bf16x8, pb);
-      // rows 16ks2 + (0..7) hold the keys of k indices 0..3, rows + 8 those of 4..7
-      const uint32_t a_lo = vs_addr + 2 * 16 * ks2 * kFaVs, a_hi = a_lo + 2 * 8 * kFaVs;
+    for (int d8 = 0; d8 < 2; ++d8) {
+      uint2 lo[8], hi[8];
+      lds_read_tr16_x8(a_lo + 256 * d8, lo);
+      lds_read_tr16_x8(a_hi + 256 * d8, hi);
 #pragma unroll
-      for (int d4 = 0; d4 < 2; ++d4) {
-        uint2 lo[4], hi[4];
-        lds_read_tr16_x8(a_lo + 256 * d4, a_hi + 256 * d4, lo, hi);
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int dt = 4 * d4 + i;
-          const bf16x8 vf = __builtin_bit_cast(bf16x8, u32x4{lo[i].x, lo[i].y, hi[i].x, hi[i].y});
-          ot[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf, pf, ot[dt], 0, 0, 0);
-        }
+      for (int i = 0; i < 8; ++i) {
+        const int dt = 8 * d8 + i;
+        const bf16x8 vf = __builtin_bit_cast(bf16x8, u32x4{lo[i].x, lo[i].y, hi[i].x, hi[i].y});
+        ot[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vf, pf, ot[dt], 0, 0, 0);
       }
     }
   }
   if (!qvalid) return;
   const float inv = 1.0f / lrun;
-  uint16_t* op = o + ((size_t)qrow * 8 + hq) * 256;
+  uint16_t* op = o + ((size_t)qrow * 8 + hq) * 256 + 4 * g;
 #pragma unroll
-  for (int dt = 0; dt < 8; ++dt)
-#pragma unroll
-    for (int r = 0; r < 16; ++r) op[32 * dt + 8 * (r >> 2) + 4 * hh + (r & 3)] = (uint16_t)f2bf(ot[dt][r] * inv);
+  for (int dt = 0; dt < 16; ++dt)
+    *reinterpret_cast<uint2*>(op + 16 * dt) =
+        make_uint2(pack2(ot[dt][0] * inv, ot[dt][1] * inv), pack2(ot[dt][2] * inv, ot[dt][3] * inv));
 }
 
 }  // namespace
@@ -817,7 +822,7 @@ hipError_t launch_attn_prefill(const uint16_t* qr, const uint16_t* kcache, const
                                int m, int capacity, uint16_t* o, hipStream_t s) {
   if (!qr || !kcache || !vcache || !o || m < 1 || pos0 < 0 || pos0 + m > capacity) return hipErrorInvalidValue;
   const int tiles = (m + kFaQ - 1) / kFaQ;
-  hipLaunchKernelGGL(k_attn_prefill, dim3(8 * ((tiles + 3) / 4)), dim3(256), 0, s, qr, kcache, vcache, pos0, m,
+  hipLaunchKernelGGL(k_attn_prefill, dim3(8 * ((tiles + 3) / 4)), dim3(512), 0, s, qr, kcache, vcache, pos0, m,
                      capacity, o);
   return hipGetLastError();
 }
