@@ -156,6 +156,35 @@ int es_q4_matvec_add(const es_q4* w, const uint16_t* x, const uint16_t* residual
   return hip_status(es::launch_qmv(m, x, residual, y, nullptr, S(stream)), "es_q4_matvec_add");
 }
 
+int es_q4_matvec_rows(const es_q4* w, const uint16_t* x, int rows, const uint16_t* residual, uint16_t* y,
+                      void* stream) {
+  es::Q4 m;
+  if (!to_q4(w, &m) || !x || !y) return fail(ES_ERR_INVALID, "es_q4_matvec_rows: null argument");
+  if (rows < 1 || rows > 65535) return fail(ES_ERR_INVALID, "es_q4_matvec_rows: rows must be 1 .. 65535");
+  if (x == y) return fail(ES_ERR_INVALID, "es_q4_matvec_rows: x must not alias y");
+  return hip_status(es::launch_qmv_rows(m, x, rows, residual, y, nullptr, S(stream)), "es_q4_matvec_rows");
+}
+
+int es_linear_row_limit(int n, int k) {
+  if (n < 1 || k < 1) return fail(ES_ERR_INVALID, "es_linear_row_limit: n and k must be positive") * -1;
+  return es::qmv_row_limit(n, k);
+}
+
+int es_add_bf16(const uint16_t* a, const uint16_t* b, int count, uint16_t* out, void* stream) {
+  if (!a || !b || !out || count < 1) return fail(ES_ERR_INVALID, "es_add_bf16: null argument or count < 1");
+  return hip_status(es::launch_add_bf16(a, b, count, out, S(stream)), "es_add_bf16");
+}
+
+int es_greedy_bf16(const uint16_t* logits, int count, void* scratch, size_t scratch_bytes, uint32_t* token,
+                   float* lse, void* stream) {
+  if (!logits || !token || !scratch) return fail(ES_ERR_INVALID, "es_greedy_bf16: null argument");
+  if (count < 1 || count >= (1 << 22)) return fail(ES_ERR_INVALID, "es_greedy_bf16: count must be 1 .. 2^22-1");
+  if (scratch_bytes < es::head_scratch_bytes(count))
+    return fail(ES_ERR_INVALID, "es_greedy_bf16: scratch smaller than es_head_scratch_bytes(count)");
+  return hip_status(es::launch_greedy(logits, count, static_cast<float*>(scratch), token, lse, S(stream)),
+                    "es_greedy_bf16");
+}
+
 int es_q4_gemm(const es_q4* w, const uint16_t* x, int rows, const uint16_t* residual, uint16_t* y,
                void* stream) {
   es::Q4 m;
@@ -209,6 +238,34 @@ int es_gdn_recur_rows(const uint16_t* q, const uint16_t* k, const uint16_t* v, c
   if (!q || !k || !v || !g || !beta || !state || !y || rows < 1)
     return fail(ES_ERR_INVALID, "es_gdn_recur_rows: null argument or rows < 1");
   return hip_status(es::launch_gdn_recur_rows(q, k, v, g, beta, rows, state, y, S(stream)), "es_gdn_recur_rows");
+}
+
+int es_gdn_conv(const uint16_t* raw, const uint16_t* history, const uint16_t* conv_w, int rows, uint16_t* conv,
+                void* stream) {
+  if (!raw || !history || !conv_w || !conv) return fail(ES_ERR_INVALID, "es_gdn_conv: null argument");
+  if (rows < 1 || rows > (1 << 18)) return fail(ES_ERR_INVALID, "es_gdn_conv: rows must be 1 .. 2^18");
+  if (raw == conv) return fail(ES_ERR_INVALID, "es_gdn_conv: raw and conv must be distinct");
+  return hip_status(es::launch_gdn_conv_hist(raw, history, conv_w, rows, conv, S(stream)), "es_gdn_conv");
+}
+
+int es_gdn_history(const uint16_t* raw, int rows, uint16_t* history, void* stream) {
+  if (!raw || !history || rows < 1) return fail(ES_ERR_INVALID, "es_gdn_history: null argument or rows < 1");
+  return hip_status(es::launch_gdn_history(raw, rows, history, S(stream)), "es_gdn_history");
+}
+
+int es_gdn_prepare(uint16_t* conv, const uint16_t* a_proj, const uint16_t* b_proj, const float* a_log,
+                   const uint16_t* dt_bias, int rows, float* g, uint16_t* beta, void* stream) {
+  if (!conv || !a_proj || !b_proj || !a_log || !dt_bias || !g || !beta)
+    return fail(ES_ERR_INVALID, "es_gdn_prepare: null argument");
+  if (rows < 1 || rows > (1 << 24)) return fail(ES_ERR_INVALID, "es_gdn_prepare: rows must be 1 .. 2^24");
+  return hip_status(es::launch_gdn_prepare_hist(conv, a_proj, b_proj, a_log, dt_bias, rows, g, beta, S(stream)),
+                    "es_gdn_prepare");
+}
+
+int es_gdn_recur(const uint16_t* conv, const float* g, const uint16_t* beta, int rows, float* state, uint16_t* y,
+                 void* stream) {
+  if (!conv || !g || !beta || !state || !y || rows < 1) return fail(ES_ERR_INVALID, "es_gdn_recur: null argument or rows < 1");
+  return hip_status(es::launch_gdn_recur_conv(conv, g, beta, rows, state, y, S(stream)), "es_gdn_recur");
 }
 
 int es_gdn_norm_gate_rows(const uint16_t* y, const uint16_t* z, const uint16_t* norm_w, int rows, uint16_t* out,
@@ -471,6 +528,16 @@ int es_engine_set_prefill(es_engine* e, int chunk_rows) {
   if (!e) return fail(ES_ERR_INVALID, "null engine");
   std::string err;
   return engine_rc(e->impl->set_prefill(chunk_rows, &err), err);
+}
+
+int es_engine_prompt_split(const es_engine* e, int* chunks, int* routed_rows, int* decode_rows) {
+  if (!e || !e->impl || !chunks || !routed_rows || !decode_rows)
+    return fail(ES_ERR_INVALID, "es_engine_prompt_split: null argument");
+  const es::Engine::PromptSplit p = e->impl->last_prompt_split();
+  *chunks = p.chunks;
+  *routed_rows = p.routed_rows;
+  *decode_rows = p.decode_rows;
+  return ES_OK;
 }
 
 void es_engine_cancel(es_engine* e) {

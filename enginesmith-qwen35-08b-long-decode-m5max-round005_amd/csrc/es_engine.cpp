@@ -465,7 +465,9 @@ int Engine::set_prefill(int chunk_rows, std::string* err) {
 }
 
 int Engine::ensure_prefill_buffers(std::string* err) {
-  const int rows = std::min(prefill_rows_, capacity_);
+  // chunks of prefill_rows_ and a routed last forward of fewer than
+  // kMaxRowLimit rows
+  const int rows = std::min(std::max(prefill_rows_, kMaxRowLimit), capacity_);
   if (prefill_alloc_rows_ >= rows) return 0;
   // buffers are kept until the engine is destroyed; a larger chunk size adds a
   // second, larger set
@@ -515,7 +517,17 @@ int Engine::ensure_prefill_buffers(std::string* err) {
 // cache, causal flash attention, output gate), the output linear with the
 // residual add, post RMSNorm rows, gate/up linears, SwiGLU, down linear with
 // the residual add.
-int Engine::prefill_rows(int pos0, int m, int slot, bool wait_prev, std::string* err) {
+// A linear over m token rows. With `routed` (the reference's last, shorter
+// forward) it takes qmv_q4 rows below the shape's row limit, as Model::linear
+// does (model.rs:189-198); otherwise the GEMM (qmm_q4_nax), as for every row
+// of a full 2048-row forward.
+static hipError_t linear_rows(const Q4& w, const uint16_t* x, int m, bool routed,
+                              const uint16_t* residual, uint16_t* y, hipStream_t s) {
+  if (routed && m < qmv_row_limit(w.n, w.k)) return launch_qmv_rows(w, x, m, residual, y, nullptr, s);
+  return launch_q4_gemm(w, x, m, residual, y, s);
+}
+
+int Engine::prefill_rows(int pos0, int m, int slot, bool wait_prev, bool routed, std::string* err) {
   const PrefillBuffers& b = pf_[slot];
   hipStream_t s = pstream_[slot];
   ES_HIP(launch_embed_rows(embed_, prompt_ + pos0, m, b.h, s), "prefill embedding");
@@ -528,21 +540,21 @@ int Engine::prefill_rows(int pos0, int m, int slot, bool wait_prev, std::string*
       ES_HIP(hipStreamWaitEvent(s, state_done_[(slot + kPrefillStreams - 1) % kPrefillStreams][l], 0),
              "prefill wait");
     if (!L.attention) {
-      ES_HIP(launch_q4_gemm(L.qkv, b.u, m, nullptr, b.raw, s), "prefill qkv");
-      ES_HIP(launch_q4_gemm(L.z, b.u, m, nullptr, b.z, s), "prefill z");
-      ES_HIP(launch_q4_gemm(L.a, b.u, m, nullptr, b.a, s), "prefill a");
-      ES_HIP(launch_q4_gemm(L.b, b.u, m, nullptr, b.b, s), "prefill b");
+      ES_HIP(linear_rows(L.qkv, b.u, m, routed, nullptr, b.raw, s), "prefill qkv");
+      ES_HIP(linear_rows(L.z, b.u, m, routed, nullptr, b.z, s), "prefill z");
+      ES_HIP(linear_rows(L.a, b.u, m, routed, nullptr, b.a, s), "prefill a");
+      ES_HIP(linear_rows(L.b, b.u, m, routed, nullptr, b.b, s), "prefill b");
       GdnPrepRowsArgs g{b.raw, L.ring, L.conv_w, b.a, b.b, L.a_log, L.dt_bias, pos0, m,
                         b.q, b.k, b.v, b.g, b.beta};
       ES_HIP(launch_gdn_prep_rows(g, s), "prefill gdn prepare");
       ES_HIP(launch_gdn_recur_rows(b.q, b.k, b.v, b.g, b.beta, m, L.state, b.y, s), "prefill gdn recurrence");
       ES_HIP(hipEventRecord(state_done_[slot][l], s), "prefill record");
       ES_HIP(launch_gdn_norm_gate_rows(b.y, b.z, L.gdn_norm, m, b.gated, s), "prefill gdn norm gate");
-      ES_HIP(launch_q4_gemm(L.out, b.gated, m, b.h, b.h, s), "prefill out_proj");
+      ES_HIP(linear_rows(L.out, b.gated, m, routed, b.h, b.h, s), "prefill out_proj");
     } else {
-      ES_HIP(launch_q4_gemm(L.q, b.u, m, nullptr, b.qp, s), "prefill q");
-      ES_HIP(launch_q4_gemm(L.k, b.u, m, nullptr, b.kp, s), "prefill k");
-      ES_HIP(launch_q4_gemm(L.v, b.u, m, nullptr, b.vp, s), "prefill v");
+      ES_HIP(linear_rows(L.q, b.u, m, routed, nullptr, b.qp, s), "prefill q");
+      ES_HIP(linear_rows(L.k, b.u, m, routed, nullptr, b.kp, s), "prefill k");
+      ES_HIP(linear_rows(L.v, b.u, m, routed, nullptr, b.vp, s), "prefill v");
       AttnPrepRowsArgs a{b.qp, b.kp, b.vp, L.q_norm, L.k_norm, inv_freq_, pos0, m,
                          b.query, L.kcache, L.vcache, capacity_};
       ES_HIP(launch_attn_prep_rows(a, s), "prefill attention prepare");
@@ -551,26 +563,45 @@ int Engine::prefill_rows(int pos0, int m, int slot, bool wait_prev, std::string*
       // next chunk's rows (masked, but read)
       ES_HIP(hipEventRecord(state_done_[slot][l], s), "prefill record");
       ES_HIP(launch_attn_gate_rows(b.o, b.qp, m, b.gated, s), "prefill attention gate");
-      ES_HIP(launch_q4_gemm(L.o, b.gated, m, b.h, b.h, s), "prefill o_proj");
+      ES_HIP(linear_rows(L.o, b.gated, m, routed, b.h, b.h, s), "prefill o_proj");
     }
     ES_HIP(launch_rmsnorm_rows(b.h, L.post_norm, m, b.u, s), "prefill post norm");
-    ES_HIP(launch_q4_gemm_swiglu(L.gate, L.up, b.u, m, b.act, s), "prefill gate/up/swiglu");
-    ES_HIP(launch_q4_gemm(L.down, b.act, m, b.h, b.h, s), "prefill down");
+    if (routed && m < qmv_row_limit(L.gate.n, L.gate.k)) {
+      // gate and up as qmv_q4 rows, then swiglu_bf16 (model.rs:279-282); the
+      // q|gate and raw-qkv buffers are free by now and hold the two outputs
+      ES_HIP(launch_qmv_rows(L.gate, b.u, m, nullptr, b.raw, nullptr, s), "prefill gate");
+      ES_HIP(launch_qmv_rows(L.up, b.u, m, nullptr, b.qp, nullptr, s), "prefill up");
+      ES_HIP(launch_swiglu_rows(b.raw, b.qp, m * L.gate.n, b.act, s), "prefill swiglu");
+    } else {
+      ES_HIP(launch_q4_gemm_swiglu(L.gate, L.up, b.u, m, b.act, s), "prefill gate/up/swiglu");
+    }
+    ES_HIP(linear_rows(L.down, b.act, m, routed, b.h, b.h, s), "prefill down");
   }
   return 0;
 }
 
-// The prompt loop of Model::generate (model.rs:106-109): chunks of at most
-// prefill_rows_ rows until n tokens are consumed, a cancellation check before
-// each chunk (forward, model.rs:182).
+// The prompt loop of Model::generate (model.rs:106-109): forwards of
+// CHUNK = 2048 rows (model.rs:7) from position 0, so only the last one may be
+// shorter. That last forward's row count r selects its routes: r == 1 runs the
+// decode kernels (forward with rows == 1), and each linear with r below its
+// row limit runs qmv_q4 rows (model.rs:189-198). Every other row takes the
+// GEMM and the flash attention, whose per-row results do not depend on how
+// rows are grouped into chunks, so those rows run in chunks of prefill_rows_.
+// A cancellation check precedes each chunk (forward, model.rs:182).
 int Engine::consume_prompt(const uint32_t* prompt, int n, std::string* err) {
+  split_ = PromptSplit{};
   if (n <= 0) return 0;
   if (prefill_rows_ == 0) {
+    split_.decode_rows = n;
     // each prompt step advances the step state to the next prompt token
     if (int rc = upload_state(0, 0, prompt[0], err)) return rc;
     return run_steps(kKindPrompt, 0, n, nullptr, nullptr, err);
   }
+  int tail = n % kRefChunk;
+  if (tail >= kMaxRowLimit) tail = 0;  // routes like a full forward
+  const int body = n - tail;
   if (int rc = ensure_prefill_buffers(err)) return rc;
+  const int chunk_rows = std::min(prefill_rows_, prefill_alloc_rows_);
   // the prefill streams start after the reset and the prompt upload on stream_
   ES_HIP(hipEventRecord(join_ev_[0], stream_), "prefill join");
   for (hipStream_t ps : pstream_) ES_HIP(hipStreamWaitEvent(ps, join_ev_[0], 0), "prefill join");
@@ -581,28 +612,41 @@ int Engine::consume_prompt(const uint32_t* prompt, int n, std::string* err) {
     }
     return 0;
   };
+  auto cancelled = [&]() -> bool {
+    if (!cancelled_.load()) return false;
+    for (hipStream_t ps : pstream_) (void)hipStreamSynchronize(ps);
+    (void)hipStreamSynchronize(stream_);
+    if (err) *err = "input disconnected";
+    return true;
+  };
   int pos = 0, chunk = 0;
-  while (pos < n) {
-    if (cancelled_.load()) {
-      for (hipStream_t ps : pstream_) (void)hipStreamSynchronize(ps);
-      (void)hipStreamSynchronize(stream_);
-      if (err) *err = "input disconnected";
-      return 3;
-    }
-    const int m = std::min(prefill_alloc_rows_, n - pos);
-    if (m == 1) {
-      // a one-row chunk runs the decode kernels on stream_, after the chunks
-      if (int rc = join_back()) return rc;
-      if (int rc = upload_state(pos, 0, prompt[pos], err)) return rc;
-      if (int rc = run_steps(kKindPrompt, pos, 1, nullptr, nullptr, err)) return rc;
-    } else if (int rc = prefill_rows(pos, m, chunk % kPrefillStreams, chunk > 0, err)) {
+  while (pos < body) {
+    if (cancelled()) return 3;
+    const int m = std::min(chunk_rows, body - pos);
+    if (int rc = prefill_rows(pos, m, chunk % kPrefillStreams, chunk > 0, false, err)) {
       for (hipStream_t ps : pstream_) (void)hipStreamSynchronize(ps);
       return rc;
     }
     pos += m;
     ++chunk;
+    ++split_.chunks;
+  }
+  if (tail > 0 && cancelled()) return 3;
+  if (tail >= 2) {
+    if (int rc = prefill_rows(pos, tail, chunk % kPrefillStreams, chunk > 0, true, err)) {
+      for (hipStream_t ps : pstream_) (void)hipStreamSynchronize(ps);
+      return rc;
+    }
+    pos += tail;
+    split_.routed_rows = tail;
   }
   if (int rc = join_back()) return rc;
+  if (tail == 1) {
+    split_.decode_rows = 1;
+    // the decode kernels on stream_, after the chunks
+    if (int rc = upload_state(pos, 0, prompt[pos], err)) return rc;
+    if (int rc = run_steps(kKindPrompt, pos, 1, nullptr, nullptr, err)) return rc;
+  }
   ES_HIP(hipStreamSynchronize(stream_), "prefill sync");
   return 0;
 }
@@ -643,6 +687,8 @@ int Engine::read_kv(int layer, int which, int pos0, int count, void* host, std::
     return 1;
   }
   const uint16_t* base = which == 0 ? layers_[layer].kcache : layers_[layer].vcache;
+  // the copies run on the null stream: finish the engine stream's work first
+  ES_HIP(hipStreamSynchronize(stream_), "sync");
   for (int h = 0; h < 2; ++h)
     ES_HIP(hipMemcpy(static_cast<uint16_t*>(host) + (size_t)h * count * 256,
                      base + ((size_t)h * capacity_ + pos0) * 256, (size_t)count * 256 * 2,
@@ -659,6 +705,8 @@ int Engine::write_kv(int layer, int which, int pos0, int count, const void* host
     return 1;
   }
   uint16_t* base = which == 0 ? layers_[layer].kcache : layers_[layer].vcache;
+  // the copies run on the null stream: finish the engine stream's work first
+  ES_HIP(hipStreamSynchronize(stream_), "sync");
   for (int h = 0; h < 2; ++h)
     ES_HIP(hipMemcpy(base + ((size_t)h * capacity_ + pos0) * 256,
                      static_cast<const uint16_t*>(host) + (size_t)h * count * 256,

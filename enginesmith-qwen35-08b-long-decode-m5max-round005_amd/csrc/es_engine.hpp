@@ -53,11 +53,17 @@ class Engine {
   int forced_decode(const uint32_t* tokens, int n, uint32_t* argmax_out, uint16_t* logits_out,
                     std::string* err);
   // Prompt consumption (model.rs:106-109): chunk_rows >= 2 consumes the
-  // prompt in batched chunks of at most chunk_rows rows (a chunk of one row
-  // runs the decode kernels, as forward(rows = 1) does); 0 replays one decode
-  // step per prompt token. Results do not depend on the chunk size.
+  // prompt as the reference's 2048-row forwards do, running the rows of full
+  // forwards in batched chunks of at most chunk_rows rows (results do not
+  // depend on chunk_rows); 0 replays one decode step per prompt token.
   int set_prefill(int chunk_rows, std::string* err);
   int prefill_chunk_rows() const { return prefill_rows_; }
+  // How the last reset request consumed its prompt: batched chunks of
+  // full-forward rows, rows of a routed last forward, decode-kernel rows.
+  struct PromptSplit {
+    int chunks = 0, routed_rows = 0, decode_rows = 0;
+  };
+  PromptSplit last_prompt_split() const { return split_; }
   void cancel() { cancelled_.store(true); }
   void clear_cancel() { cancelled_.store(false); }
   int position() const { return position_; }
@@ -106,7 +112,9 @@ class Engine {
   // mod kPrefillStreams); with wait_prev, each layer's state update waits for
   // the previous chunk's update of the same layer, so consecutive chunks
   // overlap one layer apart.
-  int prefill_rows(int pos0, int m, int slot, bool wait_prev, std::string* err);
+  // With `routed`, linears below their row limit run qmv_q4 rows (the
+  // reference's last, shorter forward); otherwise every linear is a GEMM.
+  int prefill_rows(int pos0, int m, int slot, bool wait_prev, bool routed, std::string* err);
   int ensure_prefill_buffers(std::string* err);
   // Consume the first n prompt tokens (host copy `prompt`, device copy
   // prompt_) in chunks or steps; the state then stands at position n.
@@ -145,6 +153,8 @@ class Engine {
 
   // batched prefill buffers, rows = prefill_rows_ (allocated on first use)
   static constexpr int kDefaultPrefillRows = 4096;
+  static constexpr int kRefChunk = 2048;    // the reference's forward rows (model.rs:7)
+  static constexpr int kMaxRowLimit = 33;   // largest qmv_q4 row limit (model.rs:191)
   int prefill_rows_ = kDefaultPrefillRows;
   int prefill_alloc_rows_ = 0;
   struct PrefillBuffers {
@@ -166,6 +176,7 @@ class Engine {
   };
   std::vector<GraphEntry> graphs_;
 
+  PromptSplit split_{};
   int position_ = 0;
   bool has_pending_ = false;
   uint32_t pending_ = 0;

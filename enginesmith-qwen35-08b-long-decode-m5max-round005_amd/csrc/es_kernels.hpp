@@ -46,6 +46,18 @@ hipError_t launch_norm_gate_up_parts(const Q4& gate, const Q4& up, const uint16_
 // K == 1024 or 1024 < K <= 4096 with K % 64 == 0. y may alias residual.
 hipError_t launch_qmv(const Q4& w, const uint16_t* x, const uint16_t* residual, uint16_t* y,
                       float* y_f32, hipStream_t s);
+// The same for `rows` token rows (qmv_q4 with M rows): x [rows, K], residual
+// and y [rows, N]; each row has the M = 1 arithmetic. y_f32 only for rows == 1.
+hipError_t launch_qmv_rows(const Q4& w, const uint16_t* x, int rows, const uint16_t* residual,
+                           uint16_t* y, float* y_f32, hipStream_t s);
+// Row count from which a batched linear of an [n, k] matrix takes the GEMM
+// (qmm_q4_nax) instead of qmv_q4 rows: 33, 25 or 13 by shape (model.rs:189-192,
+// MLX 0.32.4 get_qmv_batch_limit for the reference's GPU family).
+int qmv_row_limit(int n, int k);
+
+// add_bf16 (linear.metal:372-379): out = bf16(a + b) over count elements;
+// out may alias a or b.
+hipError_t launch_add_bf16(const uint16_t* a, const uint16_t* b, int count, uint16_t* out, hipStream_t s);
 
 // Embedding row: out = bf16(scale*q + bias) for token *token_dev.
 hipError_t launch_embedding(const Q4& table, const uint32_t* token_dev, uint16_t* out,
@@ -156,6 +168,18 @@ hipError_t launch_gdn_prep_rows(const GdnPrepRowsArgs& a, hipStream_t s);
 // Delta-rule recurrence over the m rows in order; y [m, 2048] bf16.
 hipError_t launch_gdn_recur_rows(const uint16_t* q, const uint16_t* k, const uint16_t* v, const float* g,
                                  const float* beta, int m, float* state, uint16_t* y, hipStream_t s);
+// The reference's GDN interface over a history [3, 6144] (GDN_INTERFACE.md:
+// 12-18): gdn_conv (conv [rows,6144]), gdn_history (history takes the last
+// three raw rows), gdn_prepare (q, k normalised in place in conv; g fp32 and
+// beta bf16 [rows,16]) and gdn_recur over the normalised conv buffer.
+hipError_t launch_gdn_conv_hist(const uint16_t* raw, const uint16_t* history, const uint16_t* conv_w,
+                                int rows, uint16_t* conv, hipStream_t s);
+hipError_t launch_gdn_history(const uint16_t* raw, int rows, uint16_t* history, hipStream_t s);
+hipError_t launch_gdn_prepare_hist(uint16_t* conv, const uint16_t* a_proj, const uint16_t* b_proj,
+                                   const float* a_log, const uint16_t* dt_bias, int rows, float* g,
+                                   uint16_t* beta, hipStream_t s);
+hipError_t launch_gdn_recur_conv(const uint16_t* conv, const float* g, const uint16_t* beta, int rows,
+                                 float* state, uint16_t* y, hipStream_t s);
 hipError_t launch_gdn_norm_gate_rows(const uint16_t* y, const uint16_t* z, const uint16_t* norm_w, int m,
                                      uint16_t* out, hipStream_t s);
 struct AttnPrepRowsArgs {
@@ -195,6 +219,10 @@ struct HeadArgs {
 int head_blocks(int vocab);
 size_t head_scratch_bytes(int vocab);
 hipError_t launch_head(const HeadArgs& a, hipStream_t s);
+// greedy_bf16 over bf16 logits in memory: the head's LSE and tie rule
+// (part: head_scratch_bytes(count)); token and lse (optional) on the device.
+hipError_t launch_greedy(const uint16_t* logits, int count, float* part, uint32_t* token, float* lse,
+                         hipStream_t s);
 
 // Prompt step epilogue: pos += 1, token = prompt[pos].
 hipError_t launch_advance(StepState* st, const uint32_t* prompt, hipStream_t s);

@@ -1,6 +1,6 @@
 // Host weight blob: one contiguous buffer holding every tensor of the model,
 // named as in the reference checkpoint under language_model.model.*
-// (model.rs:41-78, weights.rs:104-106). The same byte layout is uploaded to
+// (model.rs:41-78, weights.rs:50-52). The same byte layout is uploaded to
 // the GPU in one copy, so device tensor addresses are base + offset.
 #pragma once
 #include <cstddef>

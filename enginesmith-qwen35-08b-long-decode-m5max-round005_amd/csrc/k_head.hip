@@ -57,6 +57,24 @@ __device__ __forceinline__ void head_load(const HeadRsrc& rs, int voff_c, int vo
   }
 }
 
+// Block (max, sum exp) over the 256 bf16 logits held one per thread (-inf
+// past the vocabulary): max exact, sum = (t0 + t1) + (t2 + t3) of the four
+// waves' tree64 sums of exp(logit - max).
+__device__ __forceinline__ void block_lse_part(float v, float* wred, float* wred2, float* part) {
+  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+  float bm = wave_max(v);
+  if (lane == 0) wred[wave] = bm;
+  __syncthreads();
+  bm = fmaxf(fmaxf(wred[0], wred[1]), fmaxf(wred[2], wred[3]));
+  const float se = tree64(v == -INFINITY ? 0.0f : es_exp(v - bm));
+  if (lane == 0) wred2[wave] = se;
+  __syncthreads();
+  if (t == 0) {
+    part[2 * blockIdx.x] = bm;
+    part[2 * blockIdx.x + 1] = (wred2[0] + wred2[1]) + (wred2[2] + wred2[3]);
+  }
+}
+
 __global__ __launch_bounds__(256) void k_head(HeadArgs a) {
   __shared__ float lg[kRowsPerBlock];
   __shared__ float wred[4];
@@ -106,20 +124,17 @@ __global__ __launch_bounds__(256) void k_head(HeadArgs a) {
     if (it + 1 < kBatches) cur = nxt;
   }
   __syncthreads();
+  block_lse_part(lg[t], wred, wred2, a.part);
+}
 
-  // block (max, sum exp) over its bf16 logits
-  const float v = lg[t];
-  float bm = wave_max(v);
-  if (lane == 0) wred[wave] = bm;
-  __syncthreads();
-  bm = fmaxf(fmaxf(wred[0], wred[1]), fmaxf(wred[2], wred[3]));
-  const float se = tree64(v == -INFINITY ? 0.0f : es_exp(v - bm));
-  if (lane == 0) wred2[wave] = se;
-  __syncthreads();
-  if (t == 0) {
-    a.part[2 * blockIdx.x] = bm;
-    a.part[2 * blockIdx.x + 1] = (wred2[0] + wred2[1]) + (wred2[2] + wred2[3]);
-  }
+// greedy_bf16's first stage (linear.metal:400-449) over logits in memory:
+// the (max, sum exp) of each block of 256, in k_head's order. The second
+// stage is k_head_tail.
+__global__ __launch_bounds__(256) void k_logits_part(const uint16_t* logits, int count, float* part) {
+  __shared__ float wred[4];
+  __shared__ float wred2[4];
+  const int r = blockIdx.x * kRowsPerBlock + threadIdx.x;
+  block_lse_part(r < count ? bf2f(logits[r]) : -INFINITY, wred, wred2, part);
 }
 
 __global__ __launch_bounds__(256) void k_head_tail(HeadArgs a, int nb) {
@@ -243,6 +258,21 @@ __global__ __launch_bounds__(256) void k_read16(const u32x4* __restrict__ src, s
 }
 
 }  // namespace
+
+hipError_t launch_greedy(const uint16_t* logits, int count, float* part, uint32_t* token, float* lse,
+                         hipStream_t s) {
+  if (!logits || !part || !token || count <= 0 || count >= (1 << 22)) return hipErrorInvalidValue;
+  const int nb = head_blocks(count);
+  HeadArgs a{};
+  a.embed.n = count;
+  a.logits = const_cast<uint16_t*>(logits);  // the tail only reads them
+  a.part = part;
+  a.token_out = token;
+  a.lse_out = lse;
+  hipLaunchKernelGGL(k_logits_part, dim3(nb), dim3(256), 0, s, logits, count, part);
+  hipLaunchKernelGGL(k_head_tail, dim3(1), dim3(256), 0, s, a, nb);
+  return hipGetLastError();
+}
 
 size_t read16_out_bytes() { return (size_t)8192 * 256 * 4; }
 

@@ -120,7 +120,7 @@ __global__ __launch_bounds__(256) void k_norm_multi(MultiDev a) {
 }
 
 // RMSNorm + gate/up projections + SwiGLU with the MLX bf16 graph boundaries
-// (linear_norm.metal:214-222). A wave owns 2*NP output rows; lane 0 of each
+// (linear_norm.metal:88-102). A wave owns 2*NP output rows; lane 0 of each
 // half holds a row's gate and up sums and applies the activation in place.
 template <int NP>
 __global__ __launch_bounds__(256) void k_norm_gate_up(Q4 gate, Q4 up, const uint16_t* x,
@@ -267,11 +267,16 @@ __global__ __launch_bounds__(256) void k_norm_gate_up_parts(Q4 gate, Q4 up, cons
 }
 
 // Plain / residual QMV for K == 1024 (half-wave rows).
+// Token rows (qmv_q4 with M rows, linear.metal:28-73) are grid.y: row t reads
+// x[t] and residual[t] and writes y[t]; every row has the M = 1 arithmetic.
 template <int P, bool ADD>
 __global__ __launch_bounds__(256) void k_qmv_narrow(Q4 m, const uint16_t* x,
                                                     const uint16_t* residual, uint16_t* y,
                                                     float* y_f32) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, half = lane >> 5, sl = lane & 31;
+  x += (size_t)blockIdx.y * m.k;
+  y += (size_t)blockIdx.y * m.n;
+  if (ADD) residual += (size_t)blockIdx.y * m.n;
   const int base = (blockIdx.x * 4 + wave) * (2 * P);
   u32x4 c[P];
   uint32_t sv[P], bv[P];
@@ -312,6 +317,9 @@ __global__ __launch_bounds__(256) void k_qmv_wide(Q4 m, const uint16_t* x,
                                                   const uint16_t* residual, uint16_t* y,
                                                   float* y_f32) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  x += (size_t)blockIdx.y * m.k;  // token row (see k_qmv_narrow)
+  y += (size_t)blockIdx.y * m.n;
+  if (ADD) residual += (size_t)blockIdx.y * m.n;
   const int ns = m.k >> 5;
   const bool v1 = lane < ns, v2 = lane + 64 < ns;
   const int wpr = m.k >> 3, gpr = m.k >> 6;
@@ -459,6 +467,12 @@ __global__ __launch_bounds__(256) void k_embedding(Q4 e, const uint32_t* token, 
   }
 }
 
+__global__ __launch_bounds__(256) void k_add_bf16(const uint16_t* a, const uint16_t* b, int count,
+                                                  uint16_t* out) {
+  const int i = blockIdx.x * 256 + threadIdx.x;
+  if (i < count) out[i] = (uint16_t)f2bf(bf2f(a[i]) + bf2f(b[i]));
+}
+
 bool q4_ok(const Q4& m) { return m.w && m.s && m.b && m.n > 0 && m.k > 0 && m.k % 64 == 0; }
 
 }  // namespace
@@ -536,31 +550,39 @@ hipError_t launch_norm_gate_up_parts(const Q4& gate, const Q4& up, const uint16_
   return hipGetLastError();
 }
 
-hipError_t launch_qmv(const Q4& w, const uint16_t* x, const uint16_t* residual, uint16_t* y,
-                      float* y_f32, hipStream_t s) {
-  if (!q4_ok(w) || !x || !y) return hipErrorInvalidValue;
+hipError_t launch_qmv_rows(const Q4& w, const uint16_t* x, int rows, const uint16_t* residual,
+                           uint16_t* y, float* y_f32, hipStream_t s) {
+  if (!q4_ok(w) || !x || !y || rows < 1 || rows > 65535 || (y_f32 && rows != 1))
+    return hipErrorInvalidValue;
   if (w.k == kHidden) {
     const int rpb = 4 * 2 * kNarrowP;
-    const int blocks = (w.n + rpb - 1) / rpb;
+    const dim3 grid((w.n + rpb - 1) / rpb, rows);
     if (residual)
-      hipLaunchKernelGGL((k_qmv_narrow<kNarrowP, true>), dim3(blocks), dim3(256), 0, s, w, x,
-                         residual, y, y_f32);
+      hipLaunchKernelGGL((k_qmv_narrow<kNarrowP, true>), grid, dim3(256), 0, s, w, x, residual, y, y_f32);
     else
-      hipLaunchKernelGGL((k_qmv_narrow<kNarrowP, false>), dim3(blocks), dim3(256), 0, s, w, x,
-                         residual, y, y_f32);
+      hipLaunchKernelGGL((k_qmv_narrow<kNarrowP, false>), grid, dim3(256), 0, s, w, x, residual, y, y_f32);
   } else if (w.k > kHidden && w.k <= 4096) {
     const int rpb = 4 * kWideP;
-    const int blocks = (w.n + rpb - 1) / rpb;
+    const dim3 grid((w.n + rpb - 1) / rpb, rows);
     if (residual)
-      hipLaunchKernelGGL((k_qmv_wide<kWideP, true>), dim3(blocks), dim3(256), 0, s, w, x,
-                         residual, y, y_f32);
+      hipLaunchKernelGGL((k_qmv_wide<kWideP, true>), grid, dim3(256), 0, s, w, x, residual, y, y_f32);
     else
-      hipLaunchKernelGGL((k_qmv_wide<kWideP, false>), dim3(blocks), dim3(256), 0, s, w, x,
-                         residual, y, y_f32);
+      hipLaunchKernelGGL((k_qmv_wide<kWideP, false>), grid, dim3(256), 0, s, w, x, residual, y, y_f32);
   } else {
     return hipErrorInvalidValue;
   }
   return hipGetLastError();
+}
+
+hipError_t launch_qmv(const Q4& w, const uint16_t* x, const uint16_t* residual, uint16_t* y,
+                      float* y_f32, hipStream_t s) {
+  return launch_qmv_rows(w, x, 1, residual, y, y_f32, s);
+}
+
+int qmv_row_limit(int n, int k) {
+  if (k <= 2048 && n <= 2048) return 33;
+  if (k <= 4096 && n <= 4096) return 25;
+  return 13;
 }
 
 hipError_t launch_gdn_gate_out(const Q4& w, const uint16_t* y, const uint16_t* z,
@@ -572,6 +594,12 @@ hipError_t launch_gdn_gate_out(const Q4& w, const uint16_t* y, const uint16_t* z
   const int blocks = (w.n + rpb - 1) / rpb;
   hipLaunchKernelGGL(k_gdn_gate_out<kGateOutP>, dim3(blocks), dim3(256), 0, s, w, y, z, norm_w, h,
                      gated_out);
+  return hipGetLastError();
+}
+
+hipError_t launch_add_bf16(const uint16_t* a, const uint16_t* b, int count, uint16_t* out, hipStream_t s) {
+  if (!a || !b || !out || count < 1) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(k_add_bf16, dim3((count + 255) / 256), dim3(256), 0, s, a, b, count, out);
   return hipGetLastError();
 }
 

@@ -2,7 +2,7 @@
 // model.rs:228-350): the row-batched forms of the decode path's operators.
 //
 // k_q4_gemm: Y[M,N] = bf16(X[M,K] . dequant(W)[N,K]^T), optionally
-//   Y = bf16(R + that), as qmm_q4_nax (linear_nax.metal:1096-1140) computes
+//   Y = bf16(R + that), as qmm_q4_nax (linear_nax.metal:1096-1139) computes
 //   it: each weight is dequantised to bf16, bf16(scale*q + bias), and the
 //   products accumulate in fp32 (MFMA). Block = 128 rows x 128 features,
 //   four waves of 64 x 64, each a 2 x 2 grid of v_mfma_f32_32x32x16_bf16
@@ -275,6 +275,67 @@ __global__ __launch_bounds__(256) void k_ring_update(const uint16_t* raw, int po
   ring[(size_t)((pos0 + t) & 3) * kConv + c] = raw[(size_t)t * kConv + c];
 }
 
+// The reference's GDN interface kernels over a history [3, 6144] (oldest row
+// first, GDN_INTERFACE.md:12-18), with the arithmetic of the kernels above.
+// gdn_conv (gdn.metal:31-51): conv [T,6144] = SiLU(bf16(4-tap conv)), taps
+// before the first row from the history.
+__global__ __launch_bounds__(256) void k_gdn_conv_hist(const uint16_t* raw, const uint16_t* history,
+                                                       const uint16_t* conv_w, int rows, uint16_t* conv) {
+  const int i = blockIdx.x * 256 + threadIdx.x;
+  if (i >= rows * kConv) return;
+  const int t = i / kConv, c = i % kConv;
+  uint32_t x[4];
+#pragma unroll
+  for (int tap = 0; tap < 4; ++tap) {
+    const int r = t + tap - 3;
+    x[tap] = r < 0 ? history[(size_t)(r + 3) * kConv + c] : raw[(size_t)r * kConv + c];
+  }
+  conv[i] = (uint16_t)f2bf(conv4_silu(x, *reinterpret_cast<const uint2*>(conv_w + (size_t)c * 4)));
+}
+
+// gdn_history (gdn.metal:53-73): the history takes the last three raw rows,
+// keeping older history rows when rows < 3.
+__global__ __launch_bounds__(256) void k_gdn_history(const uint16_t* raw, int rows, uint16_t* history) {
+  const int c = blockIdx.x * 256 + threadIdx.x;
+  if (c >= kConv) return;
+  const uint16_t h0 = history[c], h1 = history[kConv + c], h2 = history[2 * kConv + c];
+#pragma unroll
+  for (int j = 0; j < 3; ++j) {
+    const int r = rows + j - 3;  // row j of the new history; r < 0 keeps history row r + 3
+    const uint16_t keep = r == -3 ? h0 : r == -2 ? h1 : h2;
+    history[(size_t)j * kConv + c] = r < 0 ? keep : raw[(size_t)r * kConv + c];
+  }
+}
+
+// gdn_prepare (gdn.metal:75-114): one wave per (row, head) normalises the
+// head's q and k in place in conv (lane i: channels i and 64 + i, sum of
+// squares tree64 + tree64, as k_gdn_prep_rows) and lane 0 forms g (fp32) and
+// beta (bf16).
+__global__ __launch_bounds__(256) void k_gdn_prepare_hist(uint16_t* conv, const uint16_t* a_proj,
+                                                          const uint16_t* b_proj, const float* a_log,
+                                                          const uint16_t* dt_bias, int rows, float* g,
+                                                          uint16_t* beta) {
+  const int lane = threadIdx.x & 63;
+  const int wid = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (wid >= rows * 16) return;
+  const int t = wid >> 4, h = wid & 15;
+#pragma unroll
+  for (int part = 0; part < 2; ++part) {
+    uint16_t* p = conv + (size_t)t * kConv + part * 2048 + h * 128;
+    const float x0 = bf2f(p[lane]), x1 = bf2f(p[64 + lane]);
+    const float tot = tree64(x0 * x0) + tree64(x1 * x1);
+    const float inv = 1.0f / sqrtf(tot / 128.0f + 1.0e-6f / 128.0f);
+    const float scale = part == 0 ? 0.0078125f : rbf(0.08838834764831845f);
+    p[lane] = (uint16_t)f2bf(rbf(x0 * inv) * scale);
+    p[64 + lane] = (uint16_t)f2bf(rbf(x1 * inv) * scale);
+  }
+  if (lane == 0) {
+    const float ax = rbf(bf2f(a_proj[wid]) + bf2f(dt_bias[h]));
+    g[wid] = es_exp(-es_exp(a_log[h]) * softplus_bf(ax));
+    beta[wid] = (uint16_t)f2bf(sigmoid_bf(bf2f(b_proj[wid])));
+  }
+}
+
 // GDN recurrence over the rows of a chunk (gdn_recur with rows > 1,
 // gdn.metal:176-228), the decode kernel's arithmetic and order per token:
 // block = (16 value rows, head), thread = (row, 8 keys), state in registers
@@ -290,23 +351,35 @@ struct RecurTileRegs {
   uint2 v;
   float gb;
 };
-__device__ __forceinline__ void recur_tile_load(const uint16_t* q, const uint16_t* k, const uint16_t* v,
-                                                const float* g, const float* beta, int h, int r0, int t0,
-                                                int nt, RecurTileRegs& R) {
+// q, k, v rows are `ld` elements apart (2048 for [m,16,128] arrays, 6144 for
+// the reference's normalised conv buffer [T,6144]); beta is fp32 or, when
+// beta_bf is set, the reference's bf16 [T,16].
+struct RecurIn {
+  const uint16_t *q, *k, *v;
+  int ld;
+  const float* g;
+  const float* beta;
+  const uint16_t* beta_bf;
+};
+__device__ __forceinline__ void recur_tile_load(const RecurIn& in, int h, int r0, int t0, int nt,
+                                                RecurTileRegs& R) {
   const int t = threadIdx.x;
   const int tt = t >> 2, c = (t & 3) * 32;
   if (tt < nt) {
-    const size_t o = ((size_t)(t0 + tt) * 16 + h) * 128 + c;
-    const u32x4* qp = reinterpret_cast<const u32x4*>(q + o);
-    const u32x4* kp = reinterpret_cast<const u32x4*>(k + o);
+    const size_t o = (size_t)(t0 + tt) * in.ld + h * 128 + c;
+    const u32x4* qp = reinterpret_cast<const u32x4*>(in.q + o);
+    const u32x4* kp = reinterpret_cast<const u32x4*>(in.k + o);
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       R.q[i] = qp[i];
       R.k[i] = kp[i];
     }
-    R.v = *reinterpret_cast<const uint2*>(v + ((size_t)(t0 + tt) * 16 + h) * 128 + r0 + (t & 3) * 4);
+    R.v = *reinterpret_cast<const uint2*>(in.v + (size_t)(t0 + tt) * in.ld + h * 128 + r0 + (t & 3) * 4);
   }
-  if (t < 2 * kRecurTile && (t & 63) < nt) R.gb = (t < 64 ? g : beta)[(size_t)(t0 + (t & 63)) * 16 + h];
+  if (t < 2 * kRecurTile && (t & 63) < nt) {
+    const size_t gi = (size_t)(t0 + (t & 63)) * 16 + h;
+    R.gb = t < 64 ? in.g[gi] : in.beta_bf ? bf2f(in.beta_bf[gi]) : in.beta[gi];
+  }
 }
 // LDS tile rows: 132 floats apart (the 16 rows a store instruction covers
 // fall in different banks); within a row, channel c of 8-channel group j sits
@@ -338,10 +411,7 @@ __device__ __forceinline__ void recur_tile_store(const RecurTileRegs& R, int nt,
   }
   if (t < 2 * kRecurTile && (t & 63) < nt) gs[t & 63][t >> 6] = R.gb;
 }
-__global__ __launch_bounds__(256, 1) void k_gdn_recur_rows(const uint16_t* q, const uint16_t* k,
-                                                           const uint16_t* v, const float* g,
-                                                           const float* beta, int m, float* state,
-                                                           uint16_t* y) {
+__global__ __launch_bounds__(256, 1) void k_gdn_recur_rows(RecurIn in, int m, float* state, uint16_t* y) {
   __shared__ __attribute__((aligned(16))) float qs[2][kRecurTile][kRecurRow];
   __shared__ __attribute__((aligned(16))) float ks[2][kRecurTile][kRecurRow];
   __shared__ float vs[2][kRecurTile][16];
@@ -356,14 +426,14 @@ __global__ __launch_bounds__(256, 1) void k_gdn_recur_rows(const uint16_t* q, co
   const float4 s_hi = reinterpret_cast<const float4*>(sp)[1];
   float S[8] = {s_lo.x, s_lo.y, s_lo.z, s_lo.w, s_hi.x, s_hi.y, s_hi.z, s_hi.w};
   RecurTileRegs R;
-  recur_tile_load(q, k, v, g, beta, h, r0, 0, min(kRecurTile, m), R);
+  recur_tile_load(in, h, r0, 0, min(kRecurTile, m), R);
   recur_tile_store(R, min(kRecurTile, m), qs[0], ks[0], vs[0], gs[0]);
   __syncthreads();
   uint16_t* yrow = y + h * 128 + row;
   for (int t0 = 0, buf = 0; t0 < m; t0 += kRecurTile, buf ^= 1) {
     const int nt = min(kRecurTile, m - t0);
     const int nt_next = min(kRecurTile, m - t0 - kRecurTile);
-    if (nt_next > 0) recur_tile_load(q, k, v, g, beta, h, r0, t0 + kRecurTile, nt_next, R);
+    if (nt_next > 0) recur_tile_load(in, h, r0, t0 + kRecurTile, nt_next, R);
     // one token: lane j of the row keeps the readout of token index j
     // within its group of 16; its operands are read one token ahead
     struct TokOps {
@@ -798,7 +868,40 @@ hipError_t launch_gdn_prep_rows(const GdnPrepRowsArgs& a, hipStream_t s) {
 hipError_t launch_gdn_recur_rows(const uint16_t* q, const uint16_t* k, const uint16_t* v, const float* g,
                                  const float* beta, int m, float* state, uint16_t* y, hipStream_t s) {
   if (!q || !k || !v || !g || !beta || !state || !y || m < 1) return hipErrorInvalidValue;
-  hipLaunchKernelGGL(k_gdn_recur_rows, dim3(kGdnHeads, 8), dim3(256), 0, s, q, k, v, g, beta, m, state, y);
+  const RecurIn in{q, k, v, 2048, g, beta, nullptr};
+  hipLaunchKernelGGL(k_gdn_recur_rows, dim3(kGdnHeads, 8), dim3(256), 0, s, in, m, state, y);
+  return hipGetLastError();
+}
+
+hipError_t launch_gdn_conv_hist(const uint16_t* raw, const uint16_t* history, const uint16_t* conv_w,
+                                int rows, uint16_t* conv, hipStream_t s) {
+  if (!raw || !history || !conv_w || !conv || rows < 1 || rows > (1 << 18)) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(k_gdn_conv_hist, dim3((rows * kConv + 255) / 256), dim3(256), 0, s, raw, history, conv_w,
+                     rows, conv);
+  return hipGetLastError();
+}
+
+hipError_t launch_gdn_history(const uint16_t* raw, int rows, uint16_t* history, hipStream_t s) {
+  if (!raw || !history || rows < 1) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(k_gdn_history, dim3(kConv / 256), dim3(256), 0, s, raw, rows, history);
+  return hipGetLastError();
+}
+
+hipError_t launch_gdn_prepare_hist(uint16_t* conv, const uint16_t* a_proj, const uint16_t* b_proj,
+                                   const float* a_log, const uint16_t* dt_bias, int rows, float* g,
+                                   uint16_t* beta, hipStream_t s) {
+  if (!conv || !a_proj || !b_proj || !a_log || !dt_bias || !g || !beta || rows < 1 || rows > (1 << 24))
+    return hipErrorInvalidValue;
+  hipLaunchKernelGGL(k_gdn_prepare_hist, dim3((rows * 16 + 3) / 4), dim3(256), 0, s, conv, a_proj, b_proj, a_log,
+                     dt_bias, rows, g, beta);
+  return hipGetLastError();
+}
+
+hipError_t launch_gdn_recur_conv(const uint16_t* conv, const float* g, const uint16_t* beta, int rows,
+                                 float* state, uint16_t* y, hipStream_t s) {
+  if (!conv || !g || !beta || !state || !y || rows < 1) return hipErrorInvalidValue;
+  const RecurIn in{conv, conv + 2048, conv + 4096, kConv, g, nullptr, beta};
+  hipLaunchKernelGGL(k_gdn_recur_rows, dim3(kGdnHeads, 8), dim3(256), 0, s, in, rows, state, y);
   return hipGetLastError();
 }
 

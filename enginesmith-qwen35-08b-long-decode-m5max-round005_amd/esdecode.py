@@ -74,6 +74,14 @@ _SIGNATURES = {
     "es_weights_tensor_info": (c_int, [c_int, c_int, c_int, c_char_p, c_int, POINTER(c_uint64), POINTER(c_uint64),
                                        POINTER(c_int)]),
     "es_weights_random": (c_int, [c_int, c_int, c_uint64, c_void_p, c_size_t, c_int]),
+    "es_q4_matvec_rows": (c_int, [POINTER(Q4), c_void_p, c_int, c_void_p, c_void_p, c_void_p]),
+    "es_linear_row_limit": (c_int, [c_int, c_int]),
+    "es_add_bf16": (c_int, [c_void_p, c_void_p, c_int, c_void_p, c_void_p]),
+    "es_greedy_bf16": (c_int, [c_void_p, c_int, c_void_p, c_size_t, c_void_p, c_void_p, c_void_p]),
+    "es_gdn_conv": (c_int, [c_void_p, c_void_p, c_void_p, c_int, c_void_p, c_void_p]),
+    "es_gdn_history": (c_int, [c_void_p, c_int, c_void_p, c_void_p]),
+    "es_gdn_prepare": (c_int, [c_void_p] * 5 + [c_int, c_void_p, c_void_p, c_void_p]),
+    "es_gdn_recur": (c_int, [c_void_p, c_void_p, c_void_p, c_int, c_void_p, c_void_p, c_void_p]),
     "es_q4_gemm": (c_int, [POINTER(Q4), c_void_p, c_int, c_void_p, c_void_p, c_void_p]),
     "es_q4_gemm_swiglu": (c_int, [POINTER(Q4), POINTER(Q4), c_void_p, c_int, c_void_p, c_void_p]),
     "es_embed_rows": (c_int, [POINTER(Q4), c_void_p, c_int, c_void_p, c_void_p]),
@@ -92,6 +100,7 @@ _SIGNATURES = {
     "es_engine_destroy": (None, [c_void_p]),
     "es_engine_generate": (c_int, [c_void_p, c_void_p, c_int, c_int, c_int, c_void_p]),
     "es_engine_set_prefill": (c_int, [c_void_p, c_int]),
+    "es_engine_prompt_split": (c_int, [c_void_p, POINTER(c_int), POINTER(c_int), POINTER(c_int)]),
     "es_engine_cancel": (None, [c_void_p]),
     "es_engine_clear_cancel": (None, [c_void_p]),
     "es_engine_position": (c_int, [c_void_p]),
@@ -317,6 +326,12 @@ class Engine:
         """Prompt consumption: batched chunks of at most chunk_rows rows (>= 2),
         or 0 for one decode step per prompt token."""
         check(lib().es_engine_set_prefill(self.h, int(chunk_rows)))
+
+    def prompt_split(self):
+        """(batched chunks, routed rows, decode rows) of the last reset request."""
+        c, r, d = c_int(), c_int(), c_int()
+        check(lib().es_engine_prompt_split(self.h, ctypes.byref(c), ctypes.byref(r), ctypes.byref(d)))
+        return c.value, r.value, d.value
 
     def cancel(self):
         lib().es_engine_cancel(self.h)

@@ -5,7 +5,7 @@
  *  1. the kernel/operator boundary: the LINEAR, GDN and ATTENTION kernel
  *     interfaces (source/LINEAR_INTERFACE.md, source/GDN_INTERFACE.md,
  *     source/ATTENTION_INTERFACE.md) that the reference reaches through
- *     Gpu::dispatch (source/src/gpu.rs:177-187);
+ *     Gpu::dispatch (source/src/gpu.rs:69-80);
  *  2. the engine boundary: Model::load / Model::generate / cancelled
  *     (source/src/model.rs:28-122), which the EngineSmith protocol server
  *     (source/src/main.rs:10-53, docs/protocol.md) drives.
@@ -17,7 +17,7 @@
  * are asynchronous on it. Every function returns 0 (ES_OK) or an error code,
  * with a message from es_last_error() (thread-local). Launch failures are
  * reported when detected; asynchronous device faults surface at the next
- * synchronising call, as Gpu::wait reports them (gpu.rs:169-173).
+ * synchronising call, as Gpu::wait reports them (gpu.rs:61-64).
  * An engine instance is not thread-safe, except es_engine_cancel.
  */
 #ifndef ES_DECODE_H
@@ -39,7 +39,7 @@ const char* es_last_error(void);
 
 /* Q4 affine group-64 weight: codes u32 [n, k/8] (nibble j of word w is column
  * 8w+j), bf16 scales and biases [n, k/64]. Replaces `Linear` (weights.rs:8,
- * 104-106). */
+ * 50-52). */
 typedef struct es_q4 {
   const uint32_t* codes;
   const uint16_t* scales;
@@ -50,7 +50,7 @@ typedef struct es_q4 {
 
 /* ------------------------------------------------------------------ */
 /* Device plumbing (stands in for Gpu::new/buffer/zero/finish,         */
-/* gpu.rs:126-176)                                                     */
+/* gpu.rs:18-68)                                                       */
 /* ------------------------------------------------------------------ */
 int es_device_count(int* count);
 int es_device_name(int device, char* buf, int len);
@@ -93,8 +93,35 @@ int es_q4_matvec(const es_q4* w, const uint16_t* x, uint16_t* y, float* y_f32, v
 int es_q4_matvec_add(const es_q4* w, const uint16_t* x, const uint16_t* residual, uint16_t* y,
                      void* stream);
 
+/* qmv_q4 with M = rows token rows (LINEAR_INTERFACE.md:19; linear.metal:28-73):
+ * y[r] = bf16(W x[r]), or with residual (may alias y) bf16(residual[r] +
+ * bf16(W x[r])). x [rows, k], y and residual [rows, n]; each row has the
+ * M = 1 arithmetic of es_q4_matvec. k as for es_q4_matvec; rows 1 .. 65535;
+ * x must not alias y. */
+int es_q4_matvec_rows(const es_q4* w, const uint16_t* x, int rows, const uint16_t* residual, uint16_t* y,
+                      void* stream);
+
+/* Row count from which the reference's batched linear of an [n, k] matrix
+ * leaves qmv_q4 for the GEMM (Model::linear, model.rs:189-192): 33 when
+ * k <= 2048 and n <= 2048, else 25 when k <= 4096 and n <= 4096, else 13.
+ * A forward of fewer rows runs that linear as es_q4_matvec_rows. Returns
+ * -ES_ERR_INVALID for non-positive shapes. */
+int es_linear_row_limit(int n, int k);
+
+/* add_bf16 (LINEAR_INTERFACE.md:23; linear.metal:372-379): out[i] =
+ * bf16(a[i] + b[i]) for count elements; out may alias a or b. */
+int es_add_bf16(const uint16_t* a, const uint16_t* b, int count, uint16_t* out, void* stream);
+
+/* greedy_bf16 (LINEAR_INTERFACE.md:25,38-42; linear.metal:400-449) over bf16
+ * logits[count]: lse = bf16(log(sum exp) + max), *token = lowest index of the
+ * maximum of bf16(logit - lse), in the order es_head_greedy uses (token and
+ * lse are device pointers; lse optional). scratch: es_head_scratch_bytes(count)
+ * bytes of device memory. count 1 .. 2^22-1. */
+int es_greedy_bf16(const uint16_t* logits, int count, void* scratch, size_t scratch_bytes, uint32_t* token,
+                   float* lse, void* stream);
+
 /* Row-batched LINEAR (prefill, rows > 1; model.rs:189-199 routes it to
- * qmm_q4_nax, linear_nax.metal:1096-1140): y[r,n] = bf16(sum_k x[r,k] *
+ * qmm_q4_nax, linear_nax.metal:1096-1139): y[r,n] = bf16(sum_k x[r,k] *
  * bf16(scale*q + bias)) with fp32 accumulation, or with residual (may alias
  * y) bf16(residual[r,n] + that). x is [rows, k], y [rows, n]; k % 64 == 0;
  * x must not alias y. */
@@ -140,6 +167,32 @@ int es_gdn_prepare_rows(const uint16_t* raw, uint16_t* ring, const uint16_t* con
  * [16, 128v, 128k] fp32 (in place) for each row in order; y [rows, 2048]. */
 int es_gdn_recur_rows(const uint16_t* q, const uint16_t* k, const uint16_t* v, const float* g, const float* beta,
                       int rows, float* state, uint16_t* y, void* stream);
+
+/* The reference's GDN kernels over its history form (GDN_INTERFACE.md:8-18):
+ * history [3, 6144] bf16, oldest row first, zero after a reset; row-major
+ * [rows, ...] tensors with tokens outer. Call in the order gdn_conv,
+ * gdn_history, gdn_prepare, gdn_recur, gdn_norm_gate (es_gdn_norm_gate_rows)
+ * on one stream. Arithmetic as the decode step's (es_gdn_recur_step). */
+
+/* gdn_conv (gdn.metal:31-51): conv [rows, 6144] = bf16(x * sigmoid_bf(x)),
+ * x = bf16(four-tap fma chain over the raw rows, taps before row 0 from the
+ * history). raw and conv must be distinct; rows 1 .. 2^18. */
+int es_gdn_conv(const uint16_t* raw, const uint16_t* history, const uint16_t* conv_w, int rows, uint16_t* conv,
+                void* stream);
+/* gdn_history (gdn.metal:53-73): history (in place) takes the last three raw
+ * rows; with rows < 3 its newest rows shift down. Run after es_gdn_conv. */
+int es_gdn_history(const uint16_t* raw, int rows, uint16_t* history, void* stream);
+/* gdn_prepare (gdn.metal:75-114): q and k of each head normalised in place in
+ * conv (bf16(bf16(x * rsqrt(mean(x^2) + 1e-6/128)) * scale), scale 1/128 for
+ * q, bf16(128^-1/2) for k); g [rows,16] fp32 = exp(-exp(A_log) *
+ * softplus(bf16(a + dt_bias))), beta [rows,16] bf16 = sigmoid_bf(b). */
+int es_gdn_prepare(uint16_t* conv, const uint16_t* a_proj, const uint16_t* b_proj, const float* a_log,
+                   const uint16_t* dt_bias, int rows, float* g, uint16_t* beta, void* stream);
+/* gdn_recur (gdn.metal:176-228) over the normalised conv buffer [rows, 6144]
+ * (q | k | v blocks of 2048): the delta-rule update of state [16,128v,128k]
+ * fp32 (in place) for each row in order; y [rows, 2048] bf16. */
+int es_gdn_recur(const uint16_t* conv, const float* g, const uint16_t* beta, int rows, float* state, uint16_t* y,
+                 void* stream);
 
 /* gdn_norm_gate (gdn.metal:230-255): out [rows, 2048] =
  * bf16(SiLU(z) * bf16(bf16(y * rsqrt(mean(y^2) + 1e-6)) * norm_w)) per head. */
@@ -307,16 +360,26 @@ void es_engine_destroy(es_engine* e);
 int es_engine_generate(es_engine* e, const uint32_t* prompt, int len, int max_tokens, int reset,
                        uint32_t* out);
 
-/* Prompt consumption of es_engine_generate (model.rs:106-109, CHUNK
- * model.rs:7): chunk_rows >= 2 consumes prompt[0 .. len-1) in batched
- * forwards of at most chunk_rows rows (the row operators above; a chunk of
- * one row runs the decode kernels, as forward with rows == 1 does), default
- * 4096, at most 65536; 0 replays one decode step per prompt token. Results do not depend on
- * the chunk size (except that a one-row chunk runs the decode kernels).
- * Consecutive chunks run on two streams, one layer apart. Batched prefill
- * allocates two sets of chunk buffers (about 67 KB per row each) on first
- * use. */
+/* Prompt consumption of es_engine_generate (model.rs:106-109, CHUNK 2048
+ * model.rs:7). With chunk_rows >= 2 (default 4096, at most 65536) the
+ * n = len-1 prompt tokens are consumed as the reference's forwards of 2048
+ * rows from position 0 would be: the rows of full forwards take the batched
+ * GEMM and flash attention, run here in chunks of at most chunk_rows rows
+ * (their results do not depend on the grouping); the last, shorter forward of
+ * r = n mod 2048 rows, when r < 33, is routed as Model::linear routes it
+ * (model.rs:189-198): r == 1 runs the decode kernels (forward with rows == 1),
+ * otherwise each linear with r below es_linear_row_limit runs as
+ * es_q4_matvec_rows. chunk_rows 0 instead replays one decode step per prompt
+ * token (not the reference's arithmetic). Consecutive chunks run on two
+ * streams, one layer apart. Batched prefill allocates two sets of chunk
+ * buffers (about 67 KB per row each) on first use. */
 int es_engine_set_prefill(es_engine* e, int chunk_rows);
+
+/* How the last reset request consumed its prompt: batched chunks of
+ * full-forward rows, rows of the routed last forward (0 or 2 .. 32), and
+ * rows run on the decode kernels (0 or 1; every row with chunk_rows 0). No
+ * reference counterpart: lets tests and callers see the routing. */
+int es_engine_prompt_split(const es_engine* e, int* chunks, int* routed_rows, int* decode_rows);
 
 /* cancelled.store(true) (main.rs:24): the running request stops at its next
  * step boundary, drains, resets and fails with ES_ERR_CANCELLED. */

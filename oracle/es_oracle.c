@@ -270,6 +270,7 @@ void eo_rms_norm(const uint16_t* x, const uint16_t* gain, int cols, float eps, u
 
 /* swiglu_bf16, linear.metal:388-395 */
 void eo_swiglu(const uint16_t* gate, const uint16_t* up, int n, uint16_t* out) {
+#pragma omp parallel for schedule(static) if (n > 65536)
   for (int i = 0; i < n; ++i) {
     float g = F(gate[i]);
     float s = eo_sigmoid_bf(g);
@@ -281,42 +282,44 @@ void eo_swiglu(const uint16_t* gate, const uint16_t* up, int n, uint16_t* out) {
 /* ------------------------------------------------------------------ */
 /* Gated DeltaNet                                                      */
 /* ------------------------------------------------------------------ */
-void eo_gdn_conv_prepare(const uint16_t* raw, uint16_t* history, const uint16_t* conv_w,
-                         const uint16_t* a, const uint16_t* b, const float* a_log,
-                         const uint16_t* dt_bias, uint16_t* conv_out, float* g, uint16_t* beta) {
+/* Convolution, SiLU and (for Q and K) normalisation of the 128 channels of
+ * one (block, head) group for one token; the group's history channels are
+ * touched by no other group. */
+static void gdn_conv_group(const uint16_t* raw, uint16_t* history, const uint16_t* conv_w,
+                           int block, int h, uint16_t* conv_out) {
   const float q_scale = 0.0078125f;
   const float k_scale = BF(0.08838834764831845f);
-  for (int block = 0; block < 3; ++block) {
-    for (int h = 0; h < 16; ++h) {
-      float v[128];
-      for (int d = 0; d < 128; ++d) {
-        int c = block * 2048 + h * 128 + d;
-        uint16_t old0 = history[c], old1 = history[6144 + c], old2 = history[12288 + c];
-        float acc = 0.0f;
-        acc = fmaf(F(old0), F(conv_w[c * 4 + 0]), acc);
-        acc = fmaf(F(old1), F(conv_w[c * 4 + 1]), acc);
-        acc = fmaf(F(old2), F(conv_w[c * 4 + 2]), acc);
-        acc = fmaf(F(raw[c]), F(conv_w[c * 4 + 3]), acc);
-        float xr = BF(acc);
-        v[d] = BF(xr * eo_sigmoid_bf(xr));
-        history[c] = old1;
-        history[6144 + c] = old2;
-        history[12288 + c] = raw[c];
-      }
-      if (block < 2) {
-        /* sum of squares: tree over channels 0..63 plus tree over 64..127 */
-        float sq[128];
-        for (int d = 0; d < 128; ++d) sq[d] = v[d] * v[d];
-        float ss = tree(sq, 64) + tree(sq + 64, 64);
-        float inv = 1.0f / sqrtf(ss / 128.0f + 1.0e-6f / 128.0f);
-        float scale = block == 0 ? q_scale : k_scale;
-        for (int d = 0; d < 128; ++d)
-          conv_out[block * 2048 + h * 128 + d] = eo_f32_to_bf16(BF(v[d] * inv) * scale);
-      } else {
-        for (int d = 0; d < 128; ++d) conv_out[block * 2048 + h * 128 + d] = eo_f32_to_bf16(v[d]);
-      }
-    }
+  float v[128];
+  for (int d = 0; d < 128; ++d) {
+    int c = block * 2048 + h * 128 + d;
+    uint16_t old0 = history[c], old1 = history[6144 + c], old2 = history[12288 + c];
+    float acc = 0.0f;
+    acc = fmaf(F(old0), F(conv_w[c * 4 + 0]), acc);
+    acc = fmaf(F(old1), F(conv_w[c * 4 + 1]), acc);
+    acc = fmaf(F(old2), F(conv_w[c * 4 + 2]), acc);
+    acc = fmaf(F(raw[c]), F(conv_w[c * 4 + 3]), acc);
+    float xr = BF(acc);
+    v[d] = BF(xr * eo_sigmoid_bf(xr));
+    history[c] = old1;
+    history[6144 + c] = old2;
+    history[12288 + c] = raw[c];
   }
+  if (block < 2) {
+    /* sum of squares: tree over channels 0..63 plus tree over 64..127 */
+    float sq[128];
+    for (int d = 0; d < 128; ++d) sq[d] = v[d] * v[d];
+    float ss = tree(sq, 64) + tree(sq + 64, 64);
+    float inv = 1.0f / sqrtf(ss / 128.0f + 1.0e-6f / 128.0f);
+    float scale = block == 0 ? q_scale : k_scale;
+    for (int d = 0; d < 128; ++d)
+      conv_out[block * 2048 + h * 128 + d] = eo_f32_to_bf16(BF(v[d] * inv) * scale);
+  } else {
+    for (int d = 0; d < 128; ++d) conv_out[block * 2048 + h * 128 + d] = eo_f32_to_bf16(v[d]);
+  }
+}
+
+static void gdn_gates(const uint16_t* a, const uint16_t* b, const float* a_log,
+                      const uint16_t* dt_bias, float* g, uint16_t* beta) {
   for (int h = 0; h < 16; ++h) {
     float ax = BF(F(a[h]) + F(dt_bias[h]));
     g[h] = eo_exp(-eo_exp(a_log[h]) * eo_softplus_bf(ax));
@@ -324,44 +327,91 @@ void eo_gdn_conv_prepare(const uint16_t* raw, uint16_t* history, const uint16_t*
   }
 }
 
+void eo_gdn_conv_prepare(const uint16_t* raw, uint16_t* history, const uint16_t* conv_w,
+                         const uint16_t* a, const uint16_t* b, const float* a_log,
+                         const uint16_t* dt_bias, uint16_t* conv_out, float* g, uint16_t* beta) {
+  for (int block = 0; block < 3; ++block)
+    for (int h = 0; h < 16; ++h) gdn_conv_group(raw, history, conv_w, block, h, conv_out);
+  gdn_gates(a, b, a_log, dt_bias, g, beta);
+}
+
 /* gdn_recur, gdn.metal:185-227 with T=1: decay, memory = S.k, delta =
  * (v - memory)*beta, S += k*delta, readout = S.q; fp32 state. Fixed order: a
  * value row is 16 lanes of 8 keys; memory and readout are fma chains over the
  * lane's 8 keys and a tree over the 16 lanes. */
+/* One token's update of value row `row` of head h (the state row st). */
+static uint16_t gdn_recur_row(const uint16_t* conv, float gt, float bt, int h, int row, float* st) {
+  const uint16_t* qv = conv + h * 128;
+  const uint16_t* kv = conv + 2048 + h * 128;
+  float vv = F(conv[4096 + h * 128 + row]);
+  float lane[16];
+  for (int j = 0; j < 16; ++j) {
+    float acc = 0.0f;
+    for (int i = 0; i < 8; ++i) {
+      int e = 8 * j + i;
+      st[e] = st[e] * gt;
+      acc = fmaf(st[e], F(kv[e]), acc);
+    }
+    lane[j] = acc;
+  }
+  float memory = tree(lane, 16);
+  float delta = (vv - memory) * bt;
+  for (int j = 0; j < 16; ++j) {
+    float acc = 0.0f;
+    for (int i = 0; i < 8; ++i) {
+      int e = 8 * j + i;
+      st[e] = fmaf(F(kv[e]), delta, st[e]);
+      acc = fmaf(st[e], F(qv[e]), acc);
+    }
+    lane[j] = acc;
+  }
+  return eo_f32_to_bf16(tree(lane, 16));
+}
+
 void eo_gdn_recur(const uint16_t* conv, const float* g, const uint16_t* beta,
                   float* state, uint16_t* y) {
 #pragma omp parallel for schedule(static)
   for (int hr = 0; hr < 16 * 128; ++hr) {
     int h = hr / 128, row = hr % 128;
-    float gt = g[h];
-    float bt = F(beta[h]);
-    float* st = state + ((size_t)h * 128 + row) * 128;
-    const uint16_t* qv = conv + h * 128;
-    const uint16_t* kv = conv + 2048 + h * 128;
-    float vv = F(conv[4096 + h * 128 + row]);
-    float lane[16];
-    for (int j = 0; j < 16; ++j) {
-      float acc = 0.0f;
-      for (int i = 0; i < 8; ++i) {
-        int e = 8 * j + i;
-        st[e] = st[e] * gt;
-        acc = fmaf(st[e], F(kv[e]), acc);
-      }
-      lane[j] = acc;
-    }
-    float memory = tree(lane, 16);
-    float delta = (vv - memory) * bt;
-    for (int j = 0; j < 16; ++j) {
-      float acc = 0.0f;
-      for (int i = 0; i < 8; ++i) {
-        int e = 8 * j + i;
-        st[e] = fmaf(F(kv[e]), delta, st[e]);
-        acc = fmaf(st[e], F(qv[e]), acc);
-      }
-      lane[j] = acc;
-    }
-    y[h * 128 + row] = eo_f32_to_bf16(tree(lane, 16));
+    y[h * 128 + row] = gdn_recur_row(conv, g[h], F(beta[h]), h, row, state + (size_t)hr * 128);
   }
+}
+
+/* A state row sees only its own value element and the head's shared q, k,
+ * g, beta, so the token loop runs inside the row loop with the same updates
+ * in the same order as T calls of eo_gdn_recur. */
+void eo_gdn_recur_rows(const uint16_t* conv, const float* g, const uint16_t* beta, int T,
+                       float* state, uint16_t* y) {
+#pragma omp parallel for schedule(static)
+  for (int hr = 0; hr < 16 * 128; ++hr) {
+    int h = hr / 128, row = hr % 128;
+    for (int t = 0; t < T; ++t)
+      y[(size_t)t * 2048 + h * 128 + row] =
+          gdn_recur_row(conv + (size_t)t * 6144, g[t * 16 + h], F(beta[t * 16 + h]), h, row,
+                        state + (size_t)hr * 128);
+  }
+}
+
+void eo_gdn_conv_prepare_rows(const uint16_t* raw, uint16_t* history, const uint16_t* conv_w,
+                              const uint16_t* a, const uint16_t* b, const float* a_log,
+                              const uint16_t* dt_bias, int T, uint16_t* conv_out, float* g,
+                              uint16_t* beta) {
+  /* a group's channels and history evolve on their own, so each group runs
+   * its tokens in order, groups in parallel */
+#pragma omp parallel for schedule(static)
+  for (int grp = 0; grp < 48; ++grp)
+    for (int t = 0; t < T; ++t)
+      gdn_conv_group(raw + (size_t)t * 6144, history, conv_w, grp / 16, grp % 16,
+                     conv_out + (size_t)t * 6144);
+  for (int t = 0; t < T; ++t)
+    gdn_gates(a + t * 16, b + t * 16, a_log, dt_bias, g + t * 16, beta + t * 16);
+}
+
+void eo_gdn_norm_gate_rows(const uint16_t* y, const uint16_t* z, const uint16_t* w, int T,
+                           uint16_t* out) {
+#pragma omp parallel for schedule(static)
+  for (int t = 0; t < T; ++t)
+    eo_gdn_norm_gate(y + (size_t)t * 2048, z + (size_t)t * 2048, w, out + (size_t)t * 2048);
 }
 
 /* gdn_norm_gate, gdn.metal:238-254 (fp32 sigmoid, unlike the MLX unary one).

@@ -78,7 +78,7 @@ void eo_q4_matvec(const uint32_t* codes, const uint16_t* scales, const uint16_t*
 void eo_q4_matvec_add(const uint32_t* codes, const uint16_t* scales, const uint16_t* biases,
                       int N, int K, const uint16_t* x, const uint16_t* residual, uint16_t* y);
 /* rms_norm_bf16, linear.metal:300-331 (and the RMS prologue of
- * linear_input_norm.metal:38-63 / linear_norm.metal:145-170) */
+ * linear_input_norm.metal:38-63 / linear_norm.metal:26-50) */
 void eo_rms_norm(const uint16_t* x, const uint16_t* gain, int cols, float eps, uint16_t* out);
 /* swiglu_bf16, linear.metal:382-396 */
 void eo_swiglu(const uint16_t* gate, const uint16_t* up, int n, uint16_t* out);
@@ -95,6 +95,18 @@ void eo_gdn_recur(const uint16_t* conv, const float* g, const uint16_t* beta,
                   float* state, uint16_t* y);
 /* gdn_norm_gate, gdn.metal:230-255 */
 void eo_gdn_norm_gate(const uint16_t* y, const uint16_t* z, const uint16_t* w, uint16_t* out);
+/* The same three steps over T consecutive tokens (gdn_conv + gdn_history +
+ * gdn_prepare, gdn_recur, gdn_norm_gate with rows = T): token t's results are
+ * those of the single-token functions called in token order. raw, conv_out
+ * [T,6144]; a, b, beta [T,16] bf16; g [T,16]; y, z, out [T,2048]. */
+void eo_gdn_conv_prepare_rows(const uint16_t* raw, uint16_t* history, const uint16_t* conv_w,
+                              const uint16_t* a, const uint16_t* b, const float* a_log,
+                              const uint16_t* dt_bias, int T, uint16_t* conv_out, float* g,
+                              uint16_t* beta);
+void eo_gdn_recur_rows(const uint16_t* conv, const float* g, const uint16_t* beta, int T,
+                       float* state, uint16_t* y);
+void eo_gdn_norm_gate_rows(const uint16_t* y, const uint16_t* z, const uint16_t* w, int T,
+                           uint16_t* out);
 
 /* ---- attention ---- */
 /* attn_prepare_qkv_decode, attention.metal:262-313. q_proj[8*512], k[512], v[512];

@@ -74,6 +74,9 @@ def lib():
             "eo_gdn_conv_prepare": (None, [vp, vp, vp, vp, vp, vp, vp, vp, vp, vp]),
             "eo_gdn_recur": (None, [vp, vp, vp, vp, vp]),
             "eo_gdn_norm_gate": (None, [vp, vp, vp, vp]),
+            "eo_gdn_conv_prepare_rows": (None, [vp, vp, vp, vp, vp, vp, vp, c_int, vp, vp, vp]),
+            "eo_gdn_recur_rows": (None, [vp, vp, vp, c_int, vp, vp]),
+            "eo_gdn_norm_gate_rows": (None, [vp, vp, vp, c_int, vp]),
             "eo_attn_prepare": (None, [vp, vp, vp, vp, vp, vp, vp, vp, c_int, c_int]),
             "eo_attn_decode_single": (None, [vp, vp, vp, c_int, c_int, vp]),
             "eo_attn_decode_split": (None, [vp, vp, vp, c_int, c_int, vp, vp, vp]),
@@ -141,6 +144,50 @@ def q4_matvec(codes, scales, biases, x, want_f32=False):
 
 
 # ---- row-batched linear (prefill) ----
+REF_CHUNK = 2048  # rows per prompt forward (model.rs:7, :106-109)
+
+
+def linear_row_limit(n: int, k: int) -> int:
+    """Model::linear's route switch (model.rs:189-192; MLX 0.32.4
+    get_qmv_batch_limit for the reference's GPU): a forward of fewer rows runs
+    the [n, k] linear as qmv_q4 rows (the decode matvec arithmetic, weights
+    not rounded), otherwise as qmm_q4_nax (bf16-dequantised weights)."""
+    if k <= 2048 and n <= 2048:
+        return 33
+    if k <= 4096 and n <= 4096:
+        return 25
+    return 13
+
+
+def q4_matvec_rows(codes, scales, biases, x, residual=None):
+    """qmv_q4 with M rows (linear.metal:28-73): each row is q4_matvec (with
+    a residual, q4_matvec_add). x [rows, k] bf16 bits."""
+    x = np.asarray(x, dtype=np.uint16)
+    if residual is None:
+        return np.stack([q4_matvec(codes, scales, biases, x[i]) for i in range(x.shape[0])])
+    residual = np.asarray(residual, dtype=np.uint16)
+    return np.stack([q4_matvec_add(codes, scales, biases, x[i], residual[i]) for i in range(x.shape[0])])
+
+
+_DEQUANT_CACHE: dict = {}
+_DEQUANT_CACHE_BYTES = 1 << 30
+
+
+def _dequant_cached(codes, scales, biases):
+    """q4_dequant_bf16 of a weight as fp64, kept (the codes array with it, so
+    its address stays unique) until the cache passes 1 GiB, oldest first."""
+    key = (codes.__array_interface__["data"][0], codes.shape, scales.__array_interface__["data"][0],
+           biases.__array_interface__["data"][0])
+    hit = _DEQUANT_CACHE.get(key)
+    if hit is not None:
+        return hit[0]
+    w = q4_dequant_bf16(codes, scales, biases).astype(np.float64)
+    _DEQUANT_CACHE[key] = (w, codes, scales, biases)
+    while sum(v[0].nbytes for v in _DEQUANT_CACHE.values()) > _DEQUANT_CACHE_BYTES and len(_DEQUANT_CACHE) > 1:
+        del _DEQUANT_CACHE[next(iter(_DEQUANT_CACHE))]
+    return w
+
+
 def q4_dequant_bf16(codes, scales, biases):
     """qmm_q4_nax's staged weights (linear_nax.metal:1118-1123): each weight
     dequantised as bf16(fp32(scale) * q + fp32(bias)). scale * q is exact in
@@ -162,7 +209,7 @@ def q4_gemm(codes, scales, biases, x, residual=None):
     the bf16 round (the kernel accumulates in fp32 in its own order, so
     results agree to within the fp32 rounding of the sum); with a residual,
     bf16(residual + bf16(sum)). x: [rows, k] bf16 bits."""
-    w = q4_dequant_bf16(codes, scales, biases).astype(np.float64)
+    w = _dequant_cached(codes, scales, biases)
     xf = bf16_to_f32(np.asarray(x, dtype=np.uint16)).astype(np.float64)
     acc = (xf @ w.T).astype(np.float32)
     y = f32_to_bf16(acc)
@@ -180,19 +227,24 @@ def attn_prefill(query, kcache, vcache, position, rows):
     unrounded probabilities; output rounded to bf16. query [rows, 2048] bf16
     bits, caches [2, capacity, 256]; returns [rows, 2048] bf16 bits. The
     kernel keeps a running maximum per block of keys, so its probabilities
-    carry different rounding: results agree to a stated tolerance."""
+    carry different rounding: results agree to a stated tolerance. Rows are
+    taken 256 at a time to bound the score matrix."""
     qf = bf16_to_f32(np.asarray(query, dtype=np.uint16)).astype(np.float64).reshape(rows, 8, 256)
     out = np.empty((rows, 8, 256), dtype=np.float64)
+    n_all = position + rows
     for kvh in range(2):
-        n_all = position + rows
         K = bf16_to_f32(kcache[kvh, :n_all]).astype(np.float64)
         V = bf16_to_f32(vcache[kvh, :n_all]).astype(np.float64)
-        s = np.einsum("rhd,nd->rhn", qf[:, 4 * kvh:4 * kvh + 4], K) / 16.0
-        mask = np.arange(n_all)[None, :] > (position + np.arange(rows))[:, None]
-        s[np.broadcast_to(mask[:, None, :], s.shape)] = -np.inf
-        p = np.exp(s - s.max(axis=-1, keepdims=True))
-        pb = bf16_to_f32(f32_to_bf16(p.astype(np.float32))).astype(np.float64)
-        out[:, 4 * kvh:4 * kvh + 4] = (pb @ V) / p.sum(axis=-1, keepdims=True)
+        for r0 in range(0, rows, 256):
+            r1 = min(rows, r0 + 256)
+            q = qf[r0:r1, 4 * kvh:4 * kvh + 4].reshape(-1, 256)           # [(r, h), d]
+            s = (q @ K.T).reshape(r1 - r0, 4, n_all) / 16.0
+            mask = np.arange(n_all)[None, :] > (position + np.arange(r0, r1))[:, None]
+            s[np.broadcast_to(mask[:, None, :], s.shape)] = -np.inf
+            p = np.exp(s - s.max(axis=-1, keepdims=True))
+            pb = bf16_to_f32(f32_to_bf16(p.astype(np.float32))).astype(np.float64)
+            o = (pb.reshape(-1, n_all) @ V).reshape(r1 - r0, 4, 256)
+            out[r0:r1, 4 * kvh:4 * kvh + 4] = o / p.sum(axis=-1, keepdims=True)
     return f32_to_bf16(out.astype(np.float32).reshape(rows, 2048))
 
 
@@ -236,6 +288,34 @@ def gdn_recur(conv, g, beta, state):
     y = np.empty(2048, dtype=np.uint16)
     lib().eo_gdn_recur(P(conv), P(g), P(beta), P(state), P(y))
     return y
+
+
+def gdn_conv_prepare_rows(raw, history, conv_w, a, b, a_log, dt_bias):
+    """gdn_conv_prepare over T tokens in order (history updated in place);
+    returns conv [T,6144], g [T,16], beta [T,16]."""
+    raw = np.ascontiguousarray(raw, dtype=np.uint16)
+    T = raw.shape[0]
+    conv = np.empty((T, 6144), dtype=np.uint16)
+    g = np.empty((T, 16), dtype=np.float32)
+    beta = np.empty((T, 16), dtype=np.uint16)
+    lib().eo_gdn_conv_prepare_rows(P(raw), P(history), P(conv_w), P(np.ascontiguousarray(a)),
+                                   P(np.ascontiguousarray(b)), P(a_log), P(dt_bias), T, P(conv), P(g), P(beta))
+    return conv, g, beta
+
+
+def gdn_recur_rows(conv, g, beta, state):
+    """gdn_recur over T tokens in order (state updated in place); y [T,2048]."""
+    T = conv.shape[0]
+    y = np.empty((T, 2048), dtype=np.uint16)
+    lib().eo_gdn_recur_rows(P(conv), P(g), P(beta), T, P(state), P(y))
+    return y
+
+
+def gdn_norm_gate_rows(y, z, w):
+    T = y.shape[0]
+    out = np.empty((T, 2048), dtype=np.uint16)
+    lib().eo_gdn_norm_gate_rows(P(np.ascontiguousarray(y)), P(np.ascontiguousarray(z)), P(w), T, P(out))
+    return out
 
 
 def gdn_norm_gate(y, z, w):
@@ -376,34 +456,71 @@ class OracleModel:
         return (int(tok), logits) if want_logits else int(tok)
 
     def generate(self, prompt, count: int):
-        """Reference generate(reset=True): consume prompt, emit count greedy ids."""
+        """Model::generate(reset=True) (model.rs:97-122): consume prompt[:-1]
+        as the reference's prompt loop does, then emit count greedy ids."""
+        self.reset()
+        self.consume_prompt(list(prompt[:-1]))
+        return self.decode(prompt[-1], count)
+
+    def generate_stepwise(self, prompt, count: int):
+        """As generate, but the prompt is replayed one decode step per token
+        (the engine's es_engine_set_prefill(0) mode)."""
         self.reset()
         for t in prompt[:-1]:
             self.step(t, want_head=False)
+        return self.decode(prompt[-1], count)
+
+    def decode(self, token: int, count: int):
         out = []
-        tok = prompt[-1]
+        tok = token
         for _ in range(count):
             tok = self.step(tok)
             out.append(tok)
         return out
+
+    def consume_prompt(self, tokens):
+        """The prompt loop of Model::generate (model.rs:106-109): forwards of
+        REF_CHUNK rows from the current position, the last one shorter; a
+        one-row forward runs the decode step without the head."""
+        pos = 0
+        while pos < len(tokens):
+            r = min(REF_CHUNK, len(tokens) - pos)
+            self.prefill(tokens[pos:pos + r])
+            pos += r
 
     def _q4(self, name, n, k):
         v = self.views
         return (v[name + ".weight"].reshape(n, k // 8), v[name + ".scales"].reshape(n, k // 64),
                 v[name + ".biases"].reshape(n, k // 64))
 
-    def prefill(self, tokens):
-        """Reference forward over a chunk of rows > 1 prompt tokens from the
-        current position, no output (model.rs:181-188 and encode_forward
-        rows != 1, model.rs:228-343): embedding rows; per layer RMSNorm rows,
-        the row-batched linears (q4_gemm), GDN conv/prepare/recurrence/gated
-        norm token by token or attention prepare/attn_prefill/gate, the
-        residual add bf16(h + bf16(out)) fused into the output linear as
-        add_bf16 follows it, post-norm, gate/up linears, SwiGLU, down linear
-        with its residual. Updates histories, states, caches and position."""
+    def _linear(self, name, n, k, x, residual=None, gemm_only=False):
+        """Model::linear over x.shape[0] rows (model.rs:189-198): qmv_q4 rows
+        below the shape's row limit, else qmm_q4_nax; with a residual, the
+        add_bf16 that follows it."""
+        w = self._q4(name, n, k)
+        if not gemm_only and x.shape[0] < linear_row_limit(n, k):
+            return q4_matvec_rows(*w, x, residual)
+        return q4_gemm(*w, x, residual=residual)
+
+    def prefill(self, tokens, gemm_only=False):
+        """Reference forward over len(tokens) prompt tokens from the current
+        position, no output (model.rs:181-188 and encode_forward, model.rs:
+        228-343). One row runs the decode step without the head (rows == 1).
+        Otherwise: embedding rows; per layer RMSNorm rows, the linears routed
+        by Model::linear (see _linear; gemm_only forces qmm_q4_nax for every
+        linear, the route of every row of a full REF_CHUNK forward), GDN
+        conv/prepare/recurrence/gated norm token by token or attention
+        prepare/attn_prefill/gate, the residual add bf16(h + bf16(out)) of
+        add_bf16 after the output linear, post-norm, gate/up linears, SwiGLU,
+        down linear with its residual. Updates histories, states, caches and
+        position."""
+        if len(tokens) == 1 and not gemm_only:
+            self.step(int(tokens[0]), want_head=False)
+            return None
         v = self.views
         m = len(tokens)
         pos0 = self.position
+        lin = lambda name, n, k, x, residual=None: self._linear(name, n, k, x, residual, gemm_only)
         emb = self._q4("embed_tokens", self.vocab, 1024)
         h = np.stack([embedding(*emb, int(t)) for t in tokens])
         for l in range(self.n_layers):
@@ -412,33 +529,31 @@ class OracleModel:
             u = np.stack([rms_norm(h[i], gain) for i in range(m)])
             if l % 4 != 3:
                 g = p + ".linear_attn"
-                raw = q4_gemm(*self._q4(g + ".in_proj_qkv", 6144, 1024), u)
-                z = q4_gemm(*self._q4(g + ".in_proj_z", 2048, 1024), u)
-                a = q4_gemm(*self._q4(g + ".in_proj_a", 16, 1024), u)
-                b = q4_gemm(*self._q4(g + ".in_proj_b", 16, 1024), u)
-                gated = np.empty((m, 2048), dtype=np.uint16)
-                for t in range(m):
-                    conv, gg, beta = gdn_conv_prepare(raw[t], self.history[l], v[g + ".conv1d.weight"], a[t], b[t],
-                                                      v[g + ".A_log"], v[g + ".dt_bias"])
-                    y = gdn_recur(conv, gg, beta, self.state[l])
-                    gated[t] = gdn_norm_gate(y, z[t], v[g + ".norm.weight"])
-                h = q4_gemm(*self._q4(g + ".out_proj", 1024, 2048), gated, residual=h)
+                raw = lin(g + ".in_proj_qkv", 6144, 1024, u)
+                z = lin(g + ".in_proj_z", 2048, 1024, u)
+                a = lin(g + ".in_proj_a", 16, 1024, u)
+                b = lin(g + ".in_proj_b", 16, 1024, u)
+                conv, gg, beta = gdn_conv_prepare_rows(raw, self.history[l], v[g + ".conv1d.weight"], a, b,
+                                                       v[g + ".A_log"], v[g + ".dt_bias"])
+                y = gdn_recur_rows(conv, gg, beta, self.state[l])
+                gated = gdn_norm_gate_rows(y, z, v[g + ".norm.weight"])
+                h = lin(g + ".out_proj", 1024, 2048, gated, residual=h)
             else:
                 a = p + ".self_attn"
-                qp = q4_gemm(*self._q4(a + ".q_proj", 4096, 1024), u)
-                kp = q4_gemm(*self._q4(a + ".k_proj", 512, 1024), u)
-                vp = q4_gemm(*self._q4(a + ".v_proj", 512, 1024), u)
+                qp = lin(a + ".q_proj", 4096, 1024, u)
+                kp = lin(a + ".k_proj", 512, 1024, u)
+                vp = lin(a + ".v_proj", 512, 1024, u)
                 query = np.stack([attn_prepare(qp[t], kp[t], vp[t], v[a + ".q_norm.weight"], v[a + ".k_norm.weight"],
                                                self.kcache[l], self.vcache[l], pos0 + t, self.capacity)
                                   for t in range(m)])
                 o = attn_prefill(query, self.kcache[l], self.vcache[l], pos0, m)
                 gated = np.stack([attn_gate(o[t], qp[t]) for t in range(m)])
-                h = q4_gemm(*self._q4(a + ".o_proj", 1024, 2048), gated, residual=h)
+                h = lin(a + ".o_proj", 1024, 2048, gated, residual=h)
             gain = v[p + ".post_attention_layernorm.weight"]
             u = np.stack([rms_norm(h[i], gain) for i in range(m)])
-            act = swiglu(q4_gemm(*self._q4(p + ".mlp.gate_proj", 3584, 1024), u),
-                         q4_gemm(*self._q4(p + ".mlp.up_proj", 3584, 1024), u)).reshape(m, 3584)
-            h = q4_gemm(*self._q4(p + ".mlp.down_proj", 1024, 3584), act, residual=h)
+            act = swiglu(lin(p + ".mlp.gate_proj", 3584, 1024, u),
+                         lin(p + ".mlp.up_proj", 3584, 1024, u)).reshape(m, 3584)
+            h = lin(p + ".mlp.down_proj", 1024, 3584, act, residual=h)
         self.position += m
         return h
 

@@ -21,10 +21,10 @@ def token_rank(logits_f32, token):
 
 
 def judge(orc, prompt, tokens):
-    """[(step, margin, reference token, rank)] for each mismatching step."""
+    """[(step, margin, reference token, rank)] for each mismatching step; the
+    oracle consumes the prompt as Model::generate does (consume_prompt)."""
     orc.reset()
-    for t in prompt[:-1]:
-        orc.step(t, want_head=False)
+    orc.consume_prompt(list(prompt[:-1]))
     return judge_from(orc, prompt[-1], tokens)
 
 

@@ -102,9 +102,16 @@ def test_attention_position_inside_capacity():
     assert np.array_equal(got["vc"][:, 2000:], x["vc"][:, 2000:])
 
 
-def test_attention_131072():
-    print("case attention length=131072", flush=True)
-    x = make_inputs(131072, 901)
+@pytest.mark.parametrize("length", [65536, 131072])
+def test_attention_long_contexts(length):
+    """The isolated attention at the 64K and 128K contexts (32K is above):
+    gated output and the 8 x 64 chain states bit for bit."""
+    print(f"case attention length={length}", flush=True)
+    x = make_inputs(length, 901 if length == 131072 else 902)
     got, want = run_gpu(x), run_oracle(x)
     assert_bits_equal(got["gated"], want["gated"], what="gated")
-    assert np.array_equal(got["vc"][:, 131071], want["vc"][:, 131071])
+    assert np.array_equal(got["vc"][:, length - 1], want["vc"][:, length - 1])
+    partials, sums, maxs = O.attn_decode_split(want["query"], want["kc"], want["vc"], length, x["cap"])
+    assert np.array_equal(got["part_ml"][:, :, 0].view(np.uint32), maxs.reshape(8, 64).view(np.uint32)), "chain max"
+    assert np.array_equal(got["part_ml"][:, :, 1].view(np.uint32), sums.reshape(8, 64).view(np.uint32)), "chain sum"
+    assert_bits_equal(bf16(got["part_o"]).ravel(), partials.ravel(), what="chain outputs")

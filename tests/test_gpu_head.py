@@ -22,7 +22,7 @@ def run_head(table, h, gain):
     scratch = E.DeviceBuffer.zeros(E.lib().es_head_scratch_bytes(n))
     tok = E.DeviceBuffer(4)
     lse = E.DeviceBuffer(4)
-    for _ in range(2):  # the arrival counter must be left at zero for the next call
+    for _ in range(2):  # a second call on the same scratch gives the same results
         E.check(E.lib().es_head_greedy(dT.struct, dh.ptr, dg.ptr, norm.ptr, logits.ptr, scratch.ptr, scratch.nbytes,
                                        tok.ptr, lse.ptr, None))
     E.synchronize()

@@ -40,10 +40,15 @@ def handoff(eng, orc, position):
     orc.position = position
 
 
+MAX_MISMATCH_FRACTION = 0.01  # the >= 99% greedy agreement bar, per case and overall
+
+
 def judge(orc, first_input, tokens, want_margins=False):
     """Teacher-forced replay; returns mismatching steps and their top-2 gaps."""
     inp, bad = first_input, []
     for i, t in enumerate(tokens):
+        if i and i % 32 == 0:
+            print(f"  judged {i} of {len(tokens)} steps", flush=True)
         tok, logits = orc.step(inp, want_logits=True)
         if tok != t:
             lf = f32(logits)
@@ -68,15 +73,17 @@ def test_full_model_teacher_forced_agreement(full):
     print(f"teacher-forced agreement {rate:.4f} ({len(bad)} mismatches of {len(stream)}): {bad}")
     for (_, _, _, gap, _) in bad:
         assert gap <= 0.1, "a mismatch must be a near tie"
-    assert rate >= 0.95
+    assert len(bad) <= MAX_MISMATCH_FRACTION * len(stream)
 
 
-@pytest.mark.parametrize("ctx,steps", [(32768, 24), (131072, 12)])
+@pytest.mark.timeout(900)
+@pytest.mark.parametrize("ctx,steps", [(32768, 257), (65536, 64), (131072, 64)])
 def test_long_context_agreement_after_batched_prefill(ctx, steps):
-    """Full model: a prompt of `ctx` uniform-random ids consumed by the
-    batched prefill, then greedy tokens; the post-prefill state is handed to
-    the oracle and the stream judged teacher-forced (the harness's gates;
-    every mismatch a near tie)."""
+    """Full model (the 257-token decode at 32K, 64 steps at 64K and 128K): a
+    prompt of `ctx` uniform-random ids consumed by the batched prefill, then
+    greedy tokens; the post-prefill state is handed to the oracle and the
+    stream judged teacher-forced: at most 1% of the steps mismatch (the >= 99%
+    agreement bar), every mismatch a near tie, and the harness's gates hold."""
     from judge import gates
     print(f"case long context {ctx}", flush=True)
     blob = E.random_weights(N_LAYERS, VOCAB, seed=20260101, threads=16)
@@ -97,3 +104,4 @@ def test_long_context_agreement_after_batched_prefill(ctx, steps):
     assert gates(cases) == []
     for (_, _, _, gap, _) in bad:
         assert gap <= 0.1, "a mismatch must be a near tie"
+    assert len(bad) <= MAX_MISMATCH_FRACTION * steps

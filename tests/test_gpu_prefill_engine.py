@@ -51,7 +51,7 @@ def test_batched_prefill_matches_the_oracle_prefill(small):
     first = eng.generate(prompt, 1, reset=True)[0]
     gdn, kv = engine_state(eng, 301)
     orc = O.OracleModel(E.tensor_views(blob, **SMALL), **SMALL, capacity=320)
-    orc.prefill(prompt[:-1])
+    orc.consume_prompt(prompt[:-1])  # one forward of 300 rows
     tok, logits = orc.step(prompt[-1], want_logits=True)
     errs = {}
     for l, (ring, state) in gdn.items():
@@ -70,18 +70,19 @@ def test_batched_prefill_matches_the_oracle_prefill(small):
 
 
 def test_chunk_size_does_not_change_results(small):
-    """Every row operator is independent of the chunk's row count and
-    position in it (GEMM rows, attention rows over aligned key blocks), so
-    700 prompt rows in one chunk, in chunks of 256 and in chunks of 37 leave
-    identical states, caches and tokens."""
+    """Every row operator of a full forward's route is independent of the
+    chunk's row count and position in it (GEMM rows, attention rows over
+    aligned key blocks), so 700 prompt rows in one chunk, in chunks of 256
+    and in chunks of 37 leave identical states, caches and tokens."""
     eng, _ = small
     prompt = rng(700).integers(0, SMALL["vocab"], 701).tolist()
     runs = []
     try:
-        for rows in (8192, 256, 37):
+        for rows, chunks in ((8192, 1), (256, 3), (37, 19)):
             print(f"case chunk rows {rows}", flush=True)
             eng.set_prefill(rows)
             toks = eng.generate(prompt, 6, reset=True)
+            assert eng.prompt_split() == (chunks, 0, 0)
             runs.append((toks, engine_state(eng, 706)))
     finally:
         eng.set_prefill(4096)
@@ -106,15 +107,16 @@ def test_prompt_steps_mode_is_the_decode_replay(small):
     finally:
         eng.set_prefill(4096)
     orc = O.OracleModel(E.tensor_views(blob, **SMALL), **SMALL, capacity=64)
-    assert first == orc.generate(prompt, 1)[0]
+    assert first == orc.generate_stepwise(prompt, 1)[0]
     ring, state = eng.read_gdn(0)
     assert np.array_equal(state.view(np.uint32), orc.state[0].view(np.uint32))
     assert np.array_equal(eng.read_kv(3, 0, 0, 41), orc.kcache[3][:, :41])
 
 
 def test_tokens_after_batched_prefill_pass_the_harness_gates(small):
-    """Prompts of 2 .. 2000 tokens consumed in chunks of 512; 16 greedy tokens
-    each judged teacher-forced from the oracle's own batched prefill state."""
+    """Prompts of 2 .. 2000 tokens, the full-forward rows in chunks of 512;
+    16 greedy tokens each judged teacher-forced from the oracle's
+    consume_prompt state."""
     eng, blob = small
     r = rng(77)
     orc = O.OracleModel(E.tensor_views(blob, **SMALL), **SMALL, capacity=2100)
@@ -126,12 +128,7 @@ def test_tokens_after_batched_prefill_pass_the_harness_gates(small):
             prompt = r.integers(0, SMALL["vocab"], n).tolist()
             toks = eng.generate(prompt, 16, reset=True)
             orc.reset()
-            for i in range(0, n - 1, 512):
-                part = prompt[i:min(n - 1, i + 512)]
-                if len(part) == 1:
-                    orc.step(part[0], want_head=False)
-                else:
-                    orc.prefill(part)
+            orc.consume_prompt(prompt[:-1])
             cases.append((16, judge_from(orc, prompt[-1], toks)))
     finally:
         eng.set_prefill(4096)
@@ -188,3 +185,69 @@ def test_prompt_filling_the_whole_capacity(small):
         assert np.array_equal(k0[l][0], k1[l][0]) and np.array_equal(k0[l][1], k1[l][1])
     with pytest.raises(E.EsError, match="capacity"):
         eng.generate(prompt + [1], 1, reset=True)
+
+
+@pytest.mark.timeout(900)
+def test_multi_chunk_prompts_on_two_streams():
+    """Prompts spanning several chunks on the two prefill streams (chunk c
+    runs layer l while chunk c-1 runs later layers), at the default chunk of
+    4096 rows and at 1000: prompts of 2C+2, C+3 and 3C+2 tokens. Each run is
+    bitwise equal to the same prompt in one chunk, the split is read back, and
+    the C = 4096 runs (4096 + 2 routed rows; 8192 rows + one on the decode
+    kernels) are judged against the oracle's independent consume_prompt,
+    32 tokens each."""
+    blob = E.random_weights(SMALL["n_layers"], SMALL["vocab"], seed=6)
+    cap = 3 * 4096 + 40
+    eng = E.Engine(blob, SMALL["n_layers"], SMALL["vocab"], capacity=cap)
+    base = rng(12290).integers(0, SMALL["vocab"], 3 * 4096 + 2).tolist()
+    judged = {}
+    most_chunks = 0
+    try:
+        for C in (4096, 1000):
+            for n in (2 * C + 2, C + 3, 3 * C + 2):
+                print(f"case multi-chunk C={C} prompt {n}", flush=True)
+                prompt = base[:n]
+                runs = []
+                for rows in (C, 65536):
+                    eng.set_prefill(rows)
+                    toks = eng.generate(prompt, 32, reset=True)
+                    runs.append((toks, eng.prompt_split(), engine_state(eng, n - 1 + 32)))
+                (t0, s0, (g0, k0)), (t1, s1, (g1, k1)) = runs
+                tail = (n - 1) % 2048 if (n - 1) % 2048 < 33 else 0
+                assert s0[0] == -(-(n - 1 - tail) // C), s0
+                assert s1[0] == 1 and s0[1:] == s1[1:], (s0, s1)
+                most_chunks = max(most_chunks, s0[0])
+                assert t0 == t1
+                for l in g0:
+                    assert np.array_equal(g0[l][0], g1[l][0])
+                    assert np.array_equal(g0[l][1].view(np.uint32), g1[l][1].view(np.uint32))
+                for l in k0:
+                    assert np.array_equal(k0[l][0], k1[l][0]) and np.array_equal(k0[l][1], k1[l][1])
+                if C == 4096 and n < 3 * C:
+                    judged[n] = t0
+    finally:
+        eng.set_prefill(4096)
+        eng.close()
+    assert most_chunks >= 4
+    # the oracle's forwards of the shared prompt, in order: prompt 4099 is
+    # two full forwards and a routed 2-row forward, prompt 8194 four full
+    # forwards and a decode-kernel row
+    orc = O.OracleModel(E.tensor_views(blob, **SMALL), **SMALL, capacity=cap)
+    cases = []
+    done = 0
+    for n in sorted(judged):
+        print(f"case oracle prompt {n}", flush=True)
+        full = (n - 1) // 2048 * 2048
+        if done:
+            orc.restore(snap)
+        while done < full:
+            orc.prefill(base[done:done + 2048])
+            done += 2048
+        snap = orc.snapshot()
+        orc.consume_prompt(base[full:n - 1])
+        m = judge_from(orc, base[n - 1], judged[n])
+        print(f"prompt {n}: {m}", flush=True)
+        for step, margin, ref, rank in m:  # near ties of bf16(logit - lse), as in the control prompts
+            assert margin <= 0.1 and rank <= 2, (step, margin, ref, rank)
+        cases.append((len(judged[n]), m))
+    assert gates(cases) == []

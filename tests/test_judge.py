@@ -31,8 +31,7 @@ def test_oracle_stream_has_no_mismatch_and_planted_one_is_found(orc):
     bad = list(ref)
     # plant the oracle's second choice at step 4
     orc.reset()
-    for t in prompt[:-1]:
-        orc.step(t, want_head=False)
+    orc.consume_prompt(prompt[:-1])
     inp = prompt[-1]
     for i in range(5):
         tok, logits = orc.step(inp, want_logits=True)
@@ -58,7 +57,7 @@ def test_snapshot_restore_branches_like_a_fresh_run(orc):
     """A branch taken from a snapshot (steps that are then undone) leaves the
     oracle exactly where an uninterrupted run would be."""
     p = rng(9).integers(0, SMALL["vocab"], 20).tolist()
-    want = orc.generate(p, 4)
+    want = orc.generate_stepwise(p, 4)
     orc.reset()
     for t in p[:10]:
         orc.step(t, want_head=False)

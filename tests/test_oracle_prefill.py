@@ -75,16 +75,18 @@ def _state(orc):
 
 
 def test_prefill_chunks_compose(small_model):
-    """Rows are independent in every batched operator except the recurrence
-    and the cache, which carry across chunks: prefill(A + B) leaves the same
-    state as prefill(A) then prefill(B), bit for bit."""
+    """On the route of a full forward (every linear a GEMM), rows are
+    independent in every batched operator except the recurrence and the
+    cache, which carry across chunks: prefill(A + B) leaves the same state as
+    prefill(A) then prefill(B), bit for bit. This is what lets the engine
+    group full-forward rows into chunks of any size."""
     _, views = small_model
     toks = rng(7).integers(0, SMALL["vocab"], 45).tolist()
     a = O.OracleModel(views, **SMALL, capacity=64)
-    ha = a.prefill(toks)
+    ha = a.prefill(toks, gemm_only=True)
     b = O.OracleModel(views, **SMALL, capacity=64)
-    b.prefill(toks[:17])
-    hb = b.prefill(toks[17:])
+    b.prefill(toks[:17], gemm_only=True)
+    hb = b.prefill(toks[17:], gemm_only=True)
     assert a.position == b.position == 45
     assert np.array_equal(ha[17:], hb)
     for x, y in zip(_state(a), _state(b)):
@@ -166,7 +168,7 @@ def test_prefill_wrong_residual_is_caught(small_model, monkeypatch):
     projection in the oracle's prefill moves the state far outside those
     bounds."""
     _, views = small_model
-    toks = rng(8).integers(0, SMALL["vocab"], 21).tolist()
+    toks = rng(8).integers(0, SMALL["vocab"], 41).tolist()  # 40 rows: every linear on the GEMM
     real = O.q4_gemm
 
     def no_down_residual(codes, scales, biases, x, residual=None):
@@ -175,12 +177,119 @@ def test_prefill_wrong_residual_is_caught(small_model, monkeypatch):
         return real(codes, scales, biases, x, residual)
 
     monkeypatch.setattr(O, "q4_gemm", no_down_residual)
-    a = O.OracleModel(views, **SMALL, capacity=32)
+    a = O.OracleModel(views, **SMALL, capacity=48)
     a.prefill(toks[:-1])
     monkeypatch.setattr(O, "q4_gemm", real)
-    b = O.OracleModel(views, **SMALL, capacity=32)
+    b = O.OracleModel(views, **SMALL, capacity=48)
     for t in toks[:-1]:
         b.step(t, want_head=False)
     rel = max(np.linalg.norm(a.state[l] - b.state[l]) / np.linalg.norm(b.state[l]) for l in a.state)
     print(f"relative state error with the residual dropped: {rel:.3f}")
     assert rel > 0.3
+
+
+# ---- the reference's prompt routing (model.rs:106-109, 189-198) ----
+# Every linear shape of the model with the row limit model.rs:191-192 gives it.
+MODEL_SHAPES = {(6144, 1024): 13, (2048, 1024): 33, (16, 1024): 33, (1024, 2048): 33, (4096, 1024): 25,
+                (512, 1024): 33, (3584, 1024): 25, (1024, 3584): 25, (248320, 1024): 13}
+
+
+def test_linear_row_limit_table():
+    """The three limits of Model::linear: k <= 2048 and n <= 2048 -> 33;
+    otherwise k <= 4096 and n <= 4096 -> 25; otherwise 13 (including the
+    6144-row in_proj_qkv and the head). The engine's table (C ABI) agrees."""
+    for (n, k), want in MODEL_SHAPES.items():
+        assert O.linear_row_limit(n, k) == want, (n, k)
+        assert E.lib().es_linear_row_limit(n, k) == want, (n, k)
+    for n, k in ((2048, 2048), (2049, 2048), (2048, 2049), (4096, 4096), (4097, 4096), (4096, 4097), (1, 1)):
+        assert E.lib().es_linear_row_limit(n, k) == O.linear_row_limit(n, k)
+    assert E.lib().es_linear_row_limit(0, 1024) < 0
+
+
+def _record_routes(monkeypatch):
+    calls = []
+    gemm, rows = O.q4_gemm, O.q4_matvec_rows
+
+    def rec_gemm(codes, scales, biases, x, residual=None):
+        calls.append(("gemm", codes.shape[0], codes.shape[1] * 8, x.shape[0]))
+        return gemm(codes, scales, biases, x, residual)
+
+    def rec_rows(codes, scales, biases, x, residual=None):
+        calls.append(("qmv", codes.shape[0], codes.shape[1] * 8, x.shape[0]))
+        return rows(codes, scales, biases, x, residual)
+
+    monkeypatch.setattr(O, "q4_gemm", rec_gemm)
+    monkeypatch.setattr(O, "q4_matvec_rows", rec_rows)
+    return calls
+
+
+@pytest.mark.parametrize("rows", [2, 12, 13, 24, 25, 32, 33])
+def test_short_forward_routes_each_linear_by_its_limit(small_model, monkeypatch, rows):
+    """A forward of r rows sends each linear to qmv_q4 rows when r is below
+    its shape's limit and to the GEMM otherwise; every linear of every layer
+    is called once."""
+    _, views = small_model
+    calls = _record_routes(monkeypatch)
+    toks = rng(rows).integers(0, SMALL["vocab"], rows).tolist()
+    O.OracleModel(views, **SMALL, capacity=40).prefill(toks)
+    # GDN layers: qkv z a b out gate up down; the attention layer: q k v o gate up down
+    assert len(calls) == 3 * 8 + 1 * 7
+    for route, n, k, m in calls:
+        assert m == rows
+        want = "qmv" if rows < MODEL_SHAPES[(n, k)] else "gemm"
+        assert route == want, (n, k, rows, route)
+
+
+@pytest.mark.parametrize("n,forwards", [
+    (1, [1]), (2, [2]), (33, [33]), (2047, [2047]), (2048, [2048]), (2049, [2048, 1]), (2050, [2048, 2]),
+    (4096, [2048, 2048]), (4097, [2048, 2048, 1]), (4130, [2048, 2048, 34])])
+def test_consume_prompt_forwards(small_model, monkeypatch, n, forwards):
+    """Model::generate's prompt loop: forwards of 2048 rows from position 0,
+    the last one shorter; a one-row forward is the decode step."""
+    _, views = small_model
+    seen = []
+    orc = O.OracleModel(views, **SMALL, capacity=8)
+    monkeypatch.setattr(orc, "prefill", lambda toks, gemm_only=False: seen.append(len(toks)))
+    orc.consume_prompt(list(range(n)))
+    assert seen == forwards
+
+
+def test_routed_forward_with_decode_attention_is_the_decode_replay(monkeypatch):
+    """A forward of 12 rows takes qmv_q4 rows for every linear (12 is below
+    every limit). With the decode attention substituted for the flash
+    attention, it is the decode replay of the same tokens bit for bit: the
+    routed linears have the decode matvec's arithmetic, weights not rounded."""
+    blob = E.random_weights(8, 4096, seed=9)
+    views = E.tensor_views(blob, 8, 4096)
+
+    def decode_attention_rows(query, kcache, vcache, position, rows):
+        return np.stack([O.attn_decode_single(np.ascontiguousarray(query[t]), kcache, vcache, position + t + 1,
+                                              kcache.shape[1]) for t in range(rows)])
+
+    monkeypatch.setattr(O, "attn_prefill", decode_attention_rows)
+    toks = rng(12).integers(0, 4096, 13).tolist()
+    a = O.OracleModel(views, 8, 4096, capacity=16)
+    a.prefill(toks[:-1])
+    ta, la = a.step(toks[-1], want_logits=True)
+    b = O.OracleModel(views, 8, 4096, capacity=16)
+    for t in toks[:-1]:
+        b.step(t, want_head=False)
+    tb, lb = b.step(toks[-1], want_logits=True)
+    assert ta == tb and np.array_equal(la, lb)
+    for x, y in zip(_state(a), _state(b)):
+        for l in x:
+            assert np.array_equal(x[l].view(np.uint16) if x[l].dtype == np.uint16 else x[l].view(np.uint32),
+                                  y[l].view(np.uint16) if y[l].dtype == np.uint16 else y[l].view(np.uint32)), l
+
+
+def test_routed_forward_differs_from_the_gemm_route(small_model):
+    """Control for the routing: the same 20-row forward with every linear on
+    the GEMM (bf16-rounded weights) leaves different bits in the states, so
+    the tests above would see a wrong route."""
+    _, views = small_model
+    toks = rng(20).integers(0, SMALL["vocab"], 20).tolist()
+    a = O.OracleModel(views, **SMALL, capacity=24)
+    a.prefill(toks)
+    b = O.OracleModel(views, **SMALL, capacity=24)
+    b.prefill(toks, gemm_only=True)
+    assert not np.array_equal(a.state[0].view(np.uint32), b.state[0].view(np.uint32))
