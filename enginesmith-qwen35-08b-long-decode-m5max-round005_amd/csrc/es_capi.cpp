@@ -439,6 +439,25 @@ int es_head_greedy(const es_q4* embed, const uint16_t* h, const uint16_t* gain,
   return hip_status(es::launch_head(a, S(stream)), "es_head_greedy");
 }
 
+int es_head_greedy_noalloc(const es_q4* embed, const uint16_t* h, const uint16_t* gain, uint16_t* norm_out,
+                           uint16_t* logits, uint32_t* token, float* lse, void* stream) {
+  es::HeadArgs a{};
+  if (!to_q4(embed, &a.embed) || a.embed.k != 1024)
+    return fail(ES_ERR_INVALID, "es_head_greedy_noalloc: table must be [vocab,1024] Q4");
+  if (a.embed.n > ES_HEAD_NOALLOC_MAX_VOCAB || a.embed.n > es::head_noalloc_max_vocab())
+    return fail(ES_ERR_INVALID, "es_head_greedy_noalloc: vocab " + std::to_string(a.embed.n) +
+                                    " exceeds the in-library scratch limit of " +
+                                    std::to_string(ES_HEAD_NOALLOC_MAX_VOCAB) + " rows");
+  if (!h || !gain || !logits || !token) return fail(ES_ERR_INVALID, "es_head_greedy_noalloc: null argument");
+  a.h = h;
+  a.gain = gain;
+  a.norm_out = norm_out;
+  a.logits = logits;
+  a.token_out = token;
+  a.lse_out = lse;
+  return hip_status(es::launch_head_noalloc(a, S(stream)), "es_head_greedy_noalloc");
+}
+
 // ---- weights ----
 size_t es_weights_total_bytes(int n_layers, int vocab) {
   if (n_layers < 1 || vocab < 1) return 0;

@@ -219,6 +219,10 @@ struct HeadArgs {
 int head_blocks(int vocab);
 size_t head_scratch_bytes(int vocab);
 hipError_t launch_head(const HeadArgs& a, hipStream_t s);
+// launch_head with the block partials in a file-scope device array instead
+// of a.part (ignored): allocates nothing; vocab <= head_noalloc_max_vocab().
+int head_noalloc_max_vocab();
+hipError_t launch_head_noalloc(HeadArgs a, hipStream_t s);
 // greedy_bf16 over bf16 logits in memory: the head's LSE and tie rule
 // (part: head_scratch_bytes(count)); token and lse (optional) on the device.
 hipError_t launch_greedy(const uint16_t* logits, int count, float* part, uint32_t* token, float* lse,

@@ -16,6 +16,8 @@
 // reaches it holds the answer. The tail also advances the device cursor.
 #include "es_kernels.hpp"
 
+#include <mutex>
+
 namespace es {
 namespace {
 
@@ -257,7 +259,49 @@ __global__ __launch_bounds__(256) void k_read16(const u32x4* __restrict__ src, s
   out[(size_t)blockIdx.x * blockDim.x + threadIdx.x] = acc[0] ^ acc[1] ^ acc[2] ^ acc[3];
 }
 
+// Block partials of launch_head_noalloc, for callers that cannot allocate:
+// one copy per device, held until the process ends, shared by every such call
+// on that device (calls that overlap on one device race). Each launch writes
+// every partial it reads, so the array needs no clearing between calls.
+constexpr int kNoAllocMaxVocab = 1 << 20;
+
 }  // namespace
+
+static __device__ __align__(256) float scratch[2 * ((kNoAllocMaxVocab + kRowsPerBlock - 1) / kRowsPerBlock)];
+
+int head_noalloc_max_vocab() { return kNoAllocMaxVocab; }
+
+// Device address of `scratch` on the current device. The host-side name of a
+// __device__ array is only a handle: kernels must be given this address.
+// Looked up once per device (with that device current) and kept.
+static hipError_t noalloc_scratch(float** out) {
+  constexpr int kMaxDevices = 64;
+  static std::mutex mu;
+  static void* addr[kMaxDevices] = {};
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return e;
+  if (dev < 0 || dev >= kMaxDevices) return hipErrorInvalidDevice;
+  std::lock_guard<std::mutex> lock(mu);
+  if (!addr[dev]) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return e;
+    if (!p) return hipErrorInvalidSymbol;
+    addr[dev] = p;
+  }
+  *out = static_cast<float*>(addr[dev]);
+  return hipSuccess;
+}
+
+hipError_t launch_head_noalloc(HeadArgs a, hipStream_t s) {
+  if (a.embed.n <= 0 || a.embed.n > kNoAllocMaxVocab) return hipErrorInvalidValue;
+  float* part = nullptr;
+  hipError_t e = noalloc_scratch(&part);
+  if (e != hipSuccess) return e;
+  a.part = part;
+  return launch_head(a, s);
+}
 
 hipError_t launch_greedy(const uint16_t* logits, int count, float* part, uint32_t* token, float* lse,
                          hipStream_t s) {

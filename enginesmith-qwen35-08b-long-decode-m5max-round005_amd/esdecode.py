@@ -69,6 +69,8 @@ _SIGNATURES = {
     "es_head_scratch_bytes": (c_size_t, [c_int]),
     "es_head_greedy": (c_int, [POINTER(Q4), c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_size_t, c_void_p,
                                c_void_p, c_void_p]),
+    "es_head_greedy_noalloc": (c_int, [POINTER(Q4), c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
+                                       c_void_p]),
     "es_weights_total_bytes": (c_size_t, [c_int, c_int]),
     "es_weights_tensor_count": (c_int, [c_int]),
     "es_weights_tensor_info": (c_int, [c_int, c_int, c_int, c_char_p, c_int, POINTER(c_uint64), POINTER(c_uint64),

@@ -308,6 +308,18 @@ int es_head_greedy(const es_q4* embed, const uint16_t* h, const uint16_t* gain,
                    uint16_t* norm_out, uint16_t* logits, void* scratch, size_t scratch_bytes,
                    uint32_t* token, float* lse, void* stream);
 
+/* es_head_greedy for callers that cannot allocate (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc). No
+ * counterpart in the reference. The same results as es_head_greedy, with the
+ * per-block partials in a device array inside the library (32 KiB per GPU,
+ * held until the process ends) instead of caller scratch; allocates nothing.
+ * vocab <= ES_HEAD_NOALLOC_MAX_VOCAB, else ES_ERR_INVALID. Every call on one
+ * GPU shares that GPU's array: calls that overlap on one GPU (concurrent
+ * streams or threads) race. The stream must belong to the current device. */
+#define ES_HEAD_NOALLOC_MAX_VOCAB 1048576
+int es_head_greedy_noalloc(const es_q4* embed, const uint16_t* h, const uint16_t* gain, uint16_t* norm_out,
+                           uint16_t* logits, uint32_t* token, float* lse, void* stream);
+
 /* ------------------------------------------------------------------ */
 /* Model weights (weights.rs:11-44 checks; model.rs:41-78 names)        */
 /* ------------------------------------------------------------------ */
