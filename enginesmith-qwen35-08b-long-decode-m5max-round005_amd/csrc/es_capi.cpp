@@ -549,6 +549,11 @@ int es_engine_set_prefill(es_engine* e, int chunk_rows) {
   return engine_rc(e->impl->set_prefill(chunk_rows, &err), err);
 }
 
+int es_engine_xcd_kernels(const es_engine* e) {
+  if (!e || !e->impl) return fail(ES_ERR_INVALID, "es_engine_xcd_kernels: null engine") * -1;
+  return e->impl->fused_mlp() ? 1 : 0;
+}
+
 int es_engine_prompt_split(const es_engine* e, int* chunks, int* routed_rows, int* decode_rows) {
   if (!e || !e->impl || !chunks || !routed_rows || !decode_rows)
     return fail(ES_ERR_INVALID, "es_engine_prompt_split: null argument");

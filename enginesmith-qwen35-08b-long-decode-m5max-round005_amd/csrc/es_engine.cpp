@@ -155,6 +155,10 @@ int Engine::init(const void* blob, uint64_t bytes, std::string* err) {
   attn_scratch_ = alloc(attn_scratch_bytes(capacity_));
   proj_part_ = static_cast<float*>(alloc((size_t)kGdnHeads * kHidden * sizeof(float)));
   hmid_ = static_cast<uint16_t*>(alloc(1024 * 2));
+  dpart_ = static_cast<float*>(alloc(8 * 1024 * sizeof(float)));
+  xact_ = static_cast<uint16_t*>(alloc(8 * 512 * 2));
+  xflags_ = static_cast<uint32_t*>(alloc(8 * 32 * sizeof(uint32_t)));
+  err_ = static_cast<uint32_t*>(alloc(256 * sizeof(uint32_t)));
   inv_freq_ = static_cast<float*>(alloc(32 * sizeof(float)));
   st_ = static_cast<StepState*>(alloc(sizeof(StepState)));
   prompt_ = static_cast<uint32_t*>(alloc((size_t)capacity_ * 4));
@@ -162,7 +166,8 @@ int Engine::init(const void* blob, uint64_t bytes, std::string* err) {
   forced_ = static_cast<uint32_t*>(alloc((size_t)capacity_ * 4));
   for (void* p : {(void*)h_, (void*)z_, (void*)ab_, (void*)y_, (void*)q_, (void*)k_, (void*)v_,
                   (void*)act_, (void*)logits_, (void*)head_part_,
-                  attn_scratch_, (void*)proj_part_, (void*)hmid_, (void*)inv_freq_, (void*)st_,
+                  attn_scratch_, (void*)proj_part_, (void*)hmid_, (void*)dpart_, (void*)xact_,
+                  (void*)xflags_, (void*)err_, (void*)inv_freq_, (void*)st_,
                   (void*)prompt_,
                   (void*)out_, (void*)forced_}) {
     if (!p) {
@@ -184,8 +189,33 @@ int Engine::init(const void* blob, uint64_t bytes, std::string* err) {
       ES_HIP(hipMemsetAsync(L.vcache, 0, cache, stream_), "memset kv");
     }
   reset_state();
+  // Placement probe for the XCD-cooperative kernels: the blocks of a
+  // 256-block launch must be dealt to the 8 XCDs in turn (from any start),
+  // 32 to each (err_ doubles as the probe's output)
+  ES_HIP(launch_xcc_probe(err_, stream_), "placement probe");
+  uint32_t xcc[256];
+  ES_HIP(hipMemcpyAsync(xcc, err_, sizeof(xcc), hipMemcpyDeviceToHost, stream_), "placement probe");
+  ES_HIP(hipStreamSynchronize(stream_), "init sync");
+  fused_mlp_ = xcc[0] < 8;
+  for (int b = 0; b < 256; ++b) fused_mlp_ = fused_mlp_ && xcc[b] == (xcc[0] + (uint32_t)b) % 8;
+  ES_HIP(hipMemsetAsync(err_, 0, 256 * sizeof(uint32_t), stream_), "memset");
+  ES_HIP(hipMemsetAsync(xflags_, 0, 8 * 32 * sizeof(uint32_t), stream_), "memset");
   ES_HIP(hipStreamSynchronize(stream_), "init sync");
   return 0;
+}
+
+// The cooperative kernels report an exhausted barrier wait in err_; the
+// step's results are then not to be trusted.
+int Engine::check_device_error(std::string* err) {
+  if (!fused_mlp_) return 0;
+  uint32_t e = 0;
+  ES_HIP(hipMemcpyAsync(&e, err_, sizeof(e), hipMemcpyDeviceToHost, stream_), "error word");
+  ES_HIP(hipStreamSynchronize(stream_), "error word");
+  if (e == 0) return 0;
+  ES_HIP(hipMemsetAsync(err_, 0, sizeof(uint32_t), stream_), "error word");
+  ES_HIP(hipStreamSynchronize(stream_), "error word");
+  if (err) *err = "decode kernels: an XCD group barrier timed out";
+  return 2;
 }
 
 // model.rs:93-96: position 0, no pending token, zeroed GDN history and state.
@@ -237,7 +267,34 @@ hipError_t Engine::enqueue_layers(hipStream_t s, int splits) {
     if (l == 0) {
       nm.embed = embed_;
       nm.h_out = h_;
+    } else if (fused_mlp_) {
+      // the previous layer's MLP left the stream after its mixer and the down
+      // projection's octet partials: their sum is this layer's input
+      nm.x = hmid_;
+      nm.dpart = dpart_;
+      nm.h_out = h_;
     }
+    auto mlp = [&](int nparts) -> hipError_t {
+      if (fused_mlp_) {
+        MlpXcdArgs m{};
+        m.gate = L.gate;
+        m.up = L.up;
+        m.down = L.down;
+        m.h_old = h_;
+        m.part = proj_part_;
+        m.h_mid = hmid_;
+        m.gain = L.post_norm;
+        m.dpart = dpart_;
+        m.xact = xact_;
+        m.flags = xflags_;
+        m.err = err_;
+        return launch_mlp_xcd(m, nparts, s);
+      }
+      hipError_t r = launch_norm_gate_up_parts(L.gate, L.up, h_, proj_part_, nparts, hmid_, L.post_norm, act_, s);
+      if (r != hipSuccess) return r;
+      // MLP down projection; its residual is the stream after the mixer (hmid_)
+      return launch_qmv(L.down, act_, hmid_, h_, nullptr, s);
+    };
     if (!L.attention) {
       nm.count = 4;
       nm.m[0] = L.qkv; nm.y[0] = L.ring;
@@ -261,9 +318,7 @@ hipError_t Engine::enqueue_layers(hipStream_t s, int splits) {
       go.out = L.out;
       go.part = proj_part_;
       if ((e = launch_gdn_recur_out(go, s)) != hipSuccess) return e;
-      if ((e = launch_norm_gate_up_parts(L.gate, L.up, h_, proj_part_, kGdnHeads, hmid_,
-                                         L.post_norm, act_, s)) != hipSuccess)
-        return e;
+      if ((e = mlp(kGdnHeads)) != hipSuccess) return e;
     } else {
       nm.count = 3;
       nm.m[0] = L.q; nm.y[0] = q_;
@@ -273,12 +328,8 @@ hipError_t Engine::enqueue_layers(hipStream_t s, int splits) {
       const AttnArgs a = attn_args(L, splits);
       if ((e = launch_attn_fused(a, s)) != hipSuccess) return e;
       if ((e = launch_attn_merge_out(a, L.o, proj_part_, s)) != hipSuccess) return e;
-      if ((e = launch_norm_gate_up_parts(L.gate, L.up, h_, proj_part_, kQHeads, hmid_,
-                                         L.post_norm, act_, s)) != hipSuccess)
-        return e;
+      if ((e = mlp(kQHeads)) != hipSuccess) return e;
     }
-    // MLP down projection; its residual is the stream after the mixer (hmid_)
-    if ((e = launch_qmv(L.down, act_, hmid_, h_, nullptr, s)) != hipSuccess) return e;
   }
   return hipSuccess;
 }
@@ -290,6 +341,10 @@ hipError_t Engine::enqueue_step(hipStream_t s, int splits, bool with_head) {
     HeadArgs h{};
     h.embed = embed_;
     h.h = h_;
+    if (fused_mlp_) {
+      h.h = hmid_;
+      h.dpart = dpart_;
+    }
     h.gain = final_norm_;
     h.logits = logits_;
     h.part = head_part_;
@@ -372,6 +427,7 @@ int Engine::run_steps(int kind, int first_pos, int count, const uint32_t* forced
       if (int rc = launch_steps(kind, first_pos + launched, batch, err)) return rc;
       launched += batch;
       ES_HIP(hipStreamSynchronize(stream_), "step sync");
+      if (int rc = check_device_error(err)) return rc;
       continue;
     }
     for (int i = 0; i < batch; ++i) {
@@ -391,6 +447,7 @@ int Engine::run_steps(int kind, int first_pos, int count, const uint32_t* forced
     }
     launched += batch;
     ES_HIP(hipStreamSynchronize(stream_), "step sync");
+    if (int rc = check_device_error(err)) return rc;
   }
   return 0;
 }
@@ -817,7 +874,7 @@ int Engine::time_decode(int steps, int warmup, double* ms_total, std::string* er
   ES_HIP(hipMemcpy(&last, out_ + (steps + warmup - 1), 4, hipMemcpyDeviceToHost), "readback");
   position_ += steps + warmup;
   pending_ = last;
-  return 0;
+  return check_device_error(err);
 }
 
 hipError_t Engine::launch_attention_part(const AttnArgs& a, int which) {
@@ -870,6 +927,10 @@ int Engine::time_head(int reps, double* ms_avg, std::string* err) {
   HeadArgs h{};
   h.embed = embed_;
   h.h = h_;
+  if (fused_mlp_) {  // the step's variant of the head
+    h.h = hmid_;
+    h.dpart = dpart_;
+  }
   h.gain = final_norm_;
   h.logits = logits_;
   h.part = head_part_;

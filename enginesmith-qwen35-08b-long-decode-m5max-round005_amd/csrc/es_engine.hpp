@@ -87,6 +87,7 @@ class Engine {
   int time_attention(int layer, int reps, int which, double* ms_avg, std::string* err);
   int time_head(int reps, double* ms_avg, std::string* err);
 
+  bool fused_mlp() const { return fused_mlp_; }
   int n_layers() const { return shape_.n_layers; }
   int vocab() const { return shape_.vocab; }
   int capacity() const { return capacity_; }
@@ -145,6 +146,14 @@ class Engine {
   void* attn_scratch_ = nullptr;  // chain outputs, chain (max, sum)
   float* proj_part_ = nullptr;    // [16, 1024] head partials of out_proj / o_proj
   uint16_t* hmid_ = nullptr;      // [1024] residual after the attention / GDN mixer
+  // XCD-cooperative MLP (k_mlp_xcd), used when the start-up probe finds the
+  // 256 blocks of a launch on XCD b % 8
+  bool fused_mlp_ = false;
+  float* dpart_ = nullptr;        // [8, 1024] down-projection octet partials
+  uint16_t* xact_ = nullptr;      // [8, 512] activation exchange
+  uint32_t* xflags_ = nullptr;    // [8, 32] barrier flags
+  uint32_t* err_ = nullptr;       // device error word of the cooperative kernels
+  int check_device_error(std::string* err);
   float* inv_freq_ = nullptr;
   StepState* st_ = nullptr;
   uint32_t* prompt_ = nullptr;  // [capacity]

@@ -20,6 +20,7 @@ struct NormMultiArgs {
   int count;
   int ring0;
   const uint16_t* x;
+  const float* dpart;       // optional [8, 1024]: x := bf16(x + bf16(pairwise sum of dpart)), written to h_out
   const uint16_t* gain;
   uint16_t* norm_out;
   Q4 embed;
@@ -134,6 +135,29 @@ hipError_t launch_attn_merge(const AttnArgs& a, hipStream_t s);
 // the next launch adds the 8 partials pairwise.
 hipError_t launch_attn_merge_out(const AttnArgs& a, const Q4& o, float* part, hipStream_t s);
 
+// ---- XCD-cooperative decode kernels, k_fused.hip ----
+// The MLP of a layer in one 256-block launch (blocks of one XCD exchange
+// activations through its L2): h_mid = bf16(h_old + bf16(pairwise sum of the
+// nparts mixer partials)) (16: GDN out_proj heads, 8: o_proj heads), post
+// RMSNorm, gate/up, SwiGLU, then dpart[x][r] = octet x's share of the down
+// row r's sum (x = 0..7). The consumer adds them: h = bf16(h_mid +
+// bf16(pairwise sum over x of dpart[x][r])), the down projection's residual
+// epilogue bit for bit.
+struct MlpXcdArgs {
+  Q4 gate, up, down;
+  const uint16_t* h_old;    // [1024] residual stream before the mixer
+  const float* part;        // [nparts, 1024] mixer partials
+  uint16_t* h_mid;          // [1024] written: stream after the mixer
+  const uint16_t* gain;     // post-attention norm [1024]
+  float* dpart;             // [8, 1024] down partials
+  uint16_t* xact;           // [8, 512] activation exchange
+  uint32_t* flags;          // [8, 32] barrier flags (zero at start-up)
+  uint32_t* err;            // error word: 2 = a barrier wait hit its limit
+};
+hipError_t launch_mlp_xcd(const MlpXcdArgs& a, int nparts, hipStream_t s);
+// out[b] = XCC_ID of block b of a 256-block launch.
+hipError_t launch_xcc_probe(uint32_t* out, hipStream_t s);
+
 // ---- batched prefill, k_prefill.hip ----
 // Y[m,N] = bf16(X[m,K] . W^T) with W dequantised to bf16 per weight, fp32
 // accumulation (qmm_q4_nax); with residual: Y = bf16(R + bf16(X . W^T)).
@@ -207,6 +231,7 @@ hipError_t launch_attn_gate_rows(const uint16_t* o, const uint16_t* qg, int m, u
 struct HeadArgs {
   Q4 embed;                 // tied table [vocab, 1024]
   const uint16_t* h;        // [1024]
+  const float* dpart;       // optional [8, 1024]: h := bf16(h + bf16(pairwise sum of dpart))
   const uint16_t* gain;     // final norm [1024]
   uint16_t* norm_out;       // optional
   uint16_t* logits;         // [vocab] bf16

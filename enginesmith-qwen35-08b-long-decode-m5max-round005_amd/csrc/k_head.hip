@@ -77,6 +77,7 @@ __device__ __forceinline__ void block_lse_part(float v, float* wred, float* wred
   }
 }
 
+template <bool PARTS>
 __global__ __launch_bounds__(256) void k_head(HeadArgs a) {
   __shared__ float lg[kRowsPerBlock];
   __shared__ float wred[4];
@@ -96,12 +97,40 @@ __global__ __launch_bounds__(256) void k_head(HeadArgs a) {
   head_load(rs, voff_c, voff_s, 0, cur);
 
   // normalised input slice (rms_norm_bf16 with the final norm gain)
-  const Raw64 xraw = load_raw64(a.h + sl * 32);
-  const uint2 x4 = reinterpret_cast<const uint2*>(a.h)[t];
+  const Raw64 xraw = PARTS ? Raw64{} : load_raw64(a.h + sl * 32);
+  uint2 x4 = reinterpret_cast<const uint2*>(a.h)[t];
   const uint2 g4 = reinterpret_cast<const uint2*>(a.gain)[t];
+  float4 dp[PARTS ? 8 : 1];
+  if (PARTS) {
+#pragma unroll
+    for (int k = 0; k < 8; ++k) dp[k] = reinterpret_cast<const float4*>(a.dpart + k * kHidden)[t];
+  }
   issue_fence();
   float xv[32], xn[32], xr[32];
-  unpack_bf16x32(xraw, xv);
+  if (PARTS) {
+    // h = bf16(h + bf16(pairwise sum of the down projection's octet partials))
+    __shared__ float hs[kNormLds];
+    const float hf[4] = {bf_lo(x4.x), bf_hi(x4.x), bf_lo(x4.y), bf_hi(x4.y)};
+    float hn[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      float c[8];
+#pragma unroll
+      for (int k = 0; k < 8; ++k) c[k] = e == 0 ? dp[k].x : e == 1 ? dp[k].y : e == 2 ? dp[k].z : dp[k].w;
+      hn[e] = bf2f(f2bf(hf[e] + rbf(((c[0] + c[1]) + (c[2] + c[3])) + ((c[4] + c[5]) + (c[6] + c[7])))));
+    }
+    x4 = make_uint2(pack_bf2(hn[0], hn[1]), pack_bf2(hn[2], hn[3]));
+    *reinterpret_cast<float4*>(hs + (t >> 3) * 36 + (t & 7) * 4) = make_float4(hn[0], hn[1], hn[2], hn[3]);
+    __syncthreads();
+    const float4* rp = reinterpret_cast<const float4*>(hs + sl * 36);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const float4 q = rp[i];
+      xv[4 * i] = q.x; xv[4 * i + 1] = q.y; xv[4 * i + 2] = q.z; xv[4 * i + 3] = q.w;
+    }
+  } else {
+    unpack_bf16x32(xraw, xv);
+  }
   norm_block_1024(xv, x4, g4, norm_lds, xn);
   if (a.norm_out && blockIdx.x == 0 && t < 32) {
 #pragma unroll
@@ -347,7 +376,10 @@ hipError_t launch_head(const HeadArgs& a, hipStream_t s) {
       a.embed.n >= (1 << 22) || !a.h || !a.gain || !a.logits || !a.part)
     return hipErrorInvalidValue;
   const int nb = head_blocks(a.embed.n);
-  hipLaunchKernelGGL(k_head, dim3(nb), dim3(256), 0, s, a);
+  if (a.dpart)
+    hipLaunchKernelGGL(k_head<true>, dim3(nb), dim3(256), 0, s, a);
+  else
+    hipLaunchKernelGGL(k_head<false>, dim3(nb), dim3(256), 0, s, a);
   hipLaunchKernelGGL(k_head_tail, dim3(1), dim3(256), 0, s, a, nb);
   return hipGetLastError();
 }

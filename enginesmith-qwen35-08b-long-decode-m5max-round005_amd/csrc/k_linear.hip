@@ -41,6 +41,7 @@ struct MultiDev {
   int total;
   int ring0;
   const uint16_t* x;
+  const float* dpart;
   const uint16_t* gain;
   uint16_t* norm_out;
   Q4 embed;
@@ -50,8 +51,13 @@ struct MultiDev {
   int pos_val;
 };
 
-template <int P, bool EMBED>
+// Input modes of k_norm_multi: the vector x; the embedding row of the step's
+// token; x plus the down projection's eight octet partials (k_mlp_xcd).
+constexpr int kInX = 0, kInEmbed = 1, kInParts = 2;
+
+template <int P, int IN>
 __global__ __launch_bounds__(256) void k_norm_multi(MultiDev a) {
+  constexpr bool EMBED = IN == kInEmbed, PARTS = IN == kInParts;
   const int lane = threadIdx.x & 63, half = lane >> 5, sl = lane & 31;
   // A wave's 2P rows lie in one matrix (every matrix has a multiple of 2P
   // rows), so the matrix and its pointers are wave-uniform (scalar registers).
@@ -75,15 +81,21 @@ __global__ __launch_bounds__(256) void k_norm_multi(MultiDev a) {
   // so that the other layer weights (about 200 MB) stay in it from one step
   // to the next.
   __shared__ float norm_lds[kNormLds];
+  __shared__ float hs[PARTS ? kNormLds : 1];
   const Raw64 graw = EMBED ? load_raw64(a.gain + sl * 32) : Raw64{};
-  const uint2 x4 = EMBED ? uint2{0u, 0u} : reinterpret_cast<const uint2*>(a.x)[threadIdx.x];
+  uint2 x4 = EMBED ? uint2{0u, 0u} : reinterpret_cast<const uint2*>(a.x)[threadIdx.x];
   const uint2 g4 = EMBED ? uint2{0u, 0u} : reinterpret_cast<const uint2*>(a.gain)[threadIdx.x];
+  float4 dp[PARTS ? 8 : 1];
+  if (PARTS) {
+#pragma unroll
+    for (int k = 0; k < 8; ++k) dp[k] = reinterpret_cast<const float4*>(a.dpart + k * kHidden)[threadIdx.x];
+  }
   // Ring slot of the first output: the step's position (read early, used at the store).
   int zero;
   asm volatile("v_mov_b32 %0, 0" : "=v"(zero));
   const int* pos_src = a.st ? &a.st->pos : reinterpret_cast<const int*>(a.gain);
   const int pos_raw = pos_src[zero];
-  const Raw64 xraw = EMBED ? Raw64{} : load_raw64(a.x + sl * 32);
+  const Raw64 xraw = EMBED || PARTS ? Raw64{} : load_raw64(a.x + sl * 32);
   issue_fence();
   u32x4 c[P];
   uint32_t sv[P], bv[P];
@@ -100,6 +112,30 @@ __global__ __launch_bounds__(256) void k_norm_multi(MultiDev a) {
     const uint32_t tok = a.st ? a.st->token : a.token_val;
     embed_slice(a.embed, tok, sl, xv);
     if (a.h_out && blockIdx.x == 0 && threadIdx.x < 32) store_bf16x32(a.h_out + sl * 32, xv);
+  } else if (PARTS) {
+    // x = bf16(x + bf16(pairwise sum of the eight octet partials)), the down
+    // projection's residual epilogue; thread t forms elements 4t..4t+3 and
+    // they pass through LDS so every lane also has its 32-element slice
+    const int t = threadIdx.x;
+    const float hf[4] = {bf_lo(x4.x), bf_hi(x4.x), bf_lo(x4.y), bf_hi(x4.y)};
+    float hn[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      float c[8];
+#pragma unroll
+      for (int k = 0; k < 8; ++k) c[k] = e == 0 ? dp[k].x : e == 1 ? dp[k].y : e == 2 ? dp[k].z : dp[k].w;
+      hn[e] = bf2f(f2bf(hf[e] + rbf(((c[0] + c[1]) + (c[2] + c[3])) + ((c[4] + c[5]) + (c[6] + c[7])))));
+    }
+    x4 = make_uint2(pack_bf2(hn[0], hn[1]), pack_bf2(hn[2], hn[3]));
+    if (a.h_out && blockIdx.x == 0) reinterpret_cast<uint2*>(a.h_out)[t] = x4;
+    *reinterpret_cast<float4*>(hs + (t >> 3) * 36 + (t & 7) * 4) = make_float4(hn[0], hn[1], hn[2], hn[3]);
+    __syncthreads();
+    const float4* rp = reinterpret_cast<const float4*>(hs + sl * 36);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const float4 q = rp[i];
+      xv[4 * i] = q.x; xv[4 * i + 1] = q.y; xv[4 * i + 2] = q.z; xv[4 * i + 3] = q.w;
+    }
   } else {
     unpack_bf16x32(xraw, xv);
   }
@@ -498,10 +534,12 @@ hipError_t launch_norm_multi(const NormMultiArgs& a, hipStream_t s) {
   if (a.ring0 && !a.st) {
     if (a.pos_val < 0) return hipErrorInvalidValue;
   }
+  if (a.dpart && (a.embed.w || !a.x)) return hipErrorInvalidValue;
   d.count = a.count;
   d.total = total;
   d.ring0 = a.ring0;
   d.x = a.x;
+  d.dpart = a.dpart;
   d.gain = a.gain;
   d.norm_out = a.norm_out;
   d.embed = a.embed;
@@ -512,9 +550,11 @@ hipError_t launch_norm_multi(const NormMultiArgs& a, hipStream_t s) {
   const int rows_per_block = 4 * 2 * kMultiP;
   const int blocks = (total + rows_per_block - 1) / rows_per_block;
   if (a.embed.w)
-    hipLaunchKernelGGL((k_norm_multi<kMultiP, true>), dim3(blocks), dim3(256), 0, s, d);
+    hipLaunchKernelGGL((k_norm_multi<kMultiP, kInEmbed>), dim3(blocks), dim3(256), 0, s, d);
+  else if (a.dpart)
+    hipLaunchKernelGGL((k_norm_multi<kMultiP, kInParts>), dim3(blocks), dim3(256), 0, s, d);
   else
-    hipLaunchKernelGGL((k_norm_multi<kMultiP, false>), dim3(blocks), dim3(256), 0, s, d);
+    hipLaunchKernelGGL((k_norm_multi<kMultiP, kInX>), dim3(blocks), dim3(256), 0, s, d);
   return hipGetLastError();
 }
 

@@ -103,6 +103,7 @@ _SIGNATURES = {
     "es_engine_generate": (c_int, [c_void_p, c_void_p, c_int, c_int, c_int, c_void_p]),
     "es_engine_set_prefill": (c_int, [c_void_p, c_int]),
     "es_engine_prompt_split": (c_int, [c_void_p, POINTER(c_int), POINTER(c_int), POINTER(c_int)]),
+    "es_engine_xcd_kernels": (c_int, [c_void_p]),
     "es_engine_cancel": (None, [c_void_p]),
     "es_engine_clear_cancel": (None, [c_void_p]),
     "es_engine_position": (c_int, [c_void_p]),
@@ -328,6 +329,13 @@ class Engine:
         """Prompt consumption: batched chunks of at most chunk_rows rows (>= 2),
         or 0 for one decode step per prompt token."""
         check(lib().es_engine_set_prefill(self.h, int(chunk_rows)))
+
+    def xcd_kernels(self) -> bool:
+        """Whether decode steps use the XCD-cooperative kernels."""
+        r = lib().es_engine_xcd_kernels(self.h)
+        if r < 0:
+            raise EsError(-r, lib().es_last_error().decode())
+        return bool(r)
 
     def prompt_split(self):
         """(batched chunks, routed rows, decode rows) of the last reset request."""

@@ -387,6 +387,13 @@ int es_engine_generate(es_engine* e, const uint32_t* prompt, int len, int max_to
  * buffers (about 67 KB per row each) on first use. */
 int es_engine_set_prefill(es_engine* e, int chunk_rows);
 
+/* 1 when the engine's decode steps use the XCD-cooperative kernels (the
+ * layer's MLP in one launch whose blocks exchange activations within each
+ * XCD; chosen at es_engine_create after a placement probe), 0 when they use
+ * one launch per dependency; -ES_ERR_INVALID for a null engine. Both give the
+ * same bits. No reference counterpart. */
+int es_engine_xcd_kernels(const es_engine* e);
+
 /* How the last reset request consumed its prompt: batched chunks of
  * full-forward rows, rows of the routed last forward (0 or 2 .. 32), and
  * rows run on the decode kernels (0 or 1; every row with chunk_rows 0). No
