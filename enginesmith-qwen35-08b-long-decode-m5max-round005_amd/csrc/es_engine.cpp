@@ -157,6 +157,7 @@ int Engine::init(const void* blob, uint64_t bytes, std::string* err) {
   hmid_ = static_cast<uint16_t*>(alloc(1024 * 2));
   dpart_ = static_cast<float*>(alloc(8 * 1024 * sizeof(float)));
   xact_ = static_cast<uint16_t*>(alloc(8 * 512 * 2));
+  xgdn_ = static_cast<uint16_t*>(alloc(8 * 2 * 648 * 2));
   xflags_ = static_cast<uint32_t*>(alloc(8 * 32 * sizeof(uint32_t)));
   err_ = static_cast<uint32_t*>(alloc(256 * sizeof(uint32_t)));
   inv_freq_ = static_cast<float*>(alloc(32 * sizeof(float)));
@@ -166,7 +167,7 @@ int Engine::init(const void* blob, uint64_t bytes, std::string* err) {
   forced_ = static_cast<uint32_t*>(alloc((size_t)capacity_ * 4));
   for (void* p : {(void*)h_, (void*)z_, (void*)ab_, (void*)y_, (void*)q_, (void*)k_, (void*)v_,
                   (void*)act_, (void*)logits_, (void*)head_part_,
-                  attn_scratch_, (void*)proj_part_, (void*)hmid_, (void*)dpart_, (void*)xact_,
+                  attn_scratch_, (void*)proj_part_, (void*)hmid_, (void*)dpart_, (void*)xact_, (void*)xgdn_,
                   (void*)xflags_, (void*)err_, (void*)inv_freq_, (void*)st_,
                   (void*)prompt_,
                   (void*)out_, (void*)forced_}) {
@@ -295,7 +296,36 @@ hipError_t Engine::enqueue_layers(hipStream_t s, int splits) {
       // MLP down projection; its residual is the stream after the mixer (hmid_)
       return launch_qmv(L.down, act_, hmid_, h_, nullptr, s);
     };
-    if (!L.attention) {
+    if (!L.attention && fused_mlp_) {
+      // the whole GDN mixer up to its out_proj head partials in one launch
+      GdnXcdArgs g{};
+      if (l == 0) {
+        g.embed = embed_;
+      } else {
+        g.x = hmid_;
+        g.dpart = dpart_;
+      }
+      g.h_out = h_;
+      g.gain = L.input_norm;
+      g.qkv = L.qkv;
+      g.z = L.z;
+      g.a = L.a;
+      g.b = L.b;
+      g.out = L.out;
+      g.conv_w = L.conv_w;
+      g.norm_w = L.gdn_norm;
+      g.dt_bias = L.dt_bias;
+      g.a_log = L.a_log;
+      g.ring = L.ring;
+      g.state = L.state;
+      g.part = proj_part_;
+      g.xbuf = xgdn_;
+      g.flags = xflags_;
+      g.err = err_;
+      g.st = st_;
+      if ((e = launch_gdn_xcd(g, s)) != hipSuccess) return e;
+      if ((e = mlp(kGdnHeads)) != hipSuccess) return e;
+    } else if (!L.attention) {
       nm.count = 4;
       nm.m[0] = L.qkv; nm.y[0] = L.ring;
       nm.m[1] = L.z;   nm.y[1] = z_;

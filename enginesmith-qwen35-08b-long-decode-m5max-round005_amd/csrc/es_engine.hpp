@@ -146,11 +146,13 @@ class Engine {
   void* attn_scratch_ = nullptr;  // chain outputs, chain (max, sum)
   float* proj_part_ = nullptr;    // [16, 1024] head partials of out_proj / o_proj
   uint16_t* hmid_ = nullptr;      // [1024] residual after the attention / GDN mixer
-  // XCD-cooperative MLP (k_mlp_xcd), used when the start-up probe finds the
-  // 256 blocks of a launch on XCD b % 8
+  // XCD-cooperative kernels (k_gdn_xcd for GDN layers, k_mlp_xcd for every
+  // MLP), used when the start-up probe sees the blocks of a 256-block launch
+  // dealt to the 8 XCDs in turn
   bool fused_mlp_ = false;
   float* dpart_ = nullptr;        // [8, 1024] down-projection octet partials
   uint16_t* xact_ = nullptr;      // [8, 512] activation exchange
+  uint16_t* xgdn_ = nullptr;      // [8, 2, 648] GDN exchange (k_gdn_xcd)
   uint32_t* xflags_ = nullptr;    // [8, 32] barrier flags
   uint32_t* err_ = nullptr;       // device error word of the cooperative kernels
   int check_device_error(std::string* err);

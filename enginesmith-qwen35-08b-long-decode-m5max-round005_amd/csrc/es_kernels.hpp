@@ -155,6 +155,30 @@ struct MlpXcdArgs {
   uint32_t* err;            // error word: 2 = a barrier wait hit its limit
 };
 hipError_t launch_mlp_xcd(const MlpXcdArgs& a, int nparts, hipStream_t s);
+// A Gated DeltaNet layer up to its out_proj head partials in one 256-block
+// launch (k_norm_multi + k_gdn_recur_out, bit for bit): the input is the
+// embedding row of st->token (embed.w set) or x + the down partials dpart of
+// the previous layer's k_mlp_xcd; h_out (block 0) receives it.
+struct GdnXcdArgs {
+  const uint16_t* x;        // [1024] stream after the previous layer's mixer
+  const float* dpart;       // [8, 1024] the previous layer's down partials
+  Q4 embed;                 // layer 0: the token's embedding row is the input
+  uint16_t* h_out;          // [1024] the layer input
+  const uint16_t* gain;     // input norm [1024]
+  Q4 qkv, z, a, b, out;
+  const uint16_t* conv_w;   // [6144, 4]
+  const uint16_t* norm_w;   // [128]
+  const uint16_t* dt_bias;  // [16]
+  const float* a_log;       // [16]
+  uint16_t* ring;           // [4, 6144]
+  float* state;             // [16, 128, 128]
+  float* part;              // [16, 1024] out_proj head partials
+  uint16_t* xbuf;           // [8 XCDs][2 heads][648] exchange
+  uint32_t* flags;          // [8, 32] barrier flags (shared with k_mlp_xcd)
+  uint32_t* err;            // error word
+  const StepState* st;
+};
+hipError_t launch_gdn_xcd(const GdnXcdArgs& a, hipStream_t s);
 // out[b] = XCC_ID of block b of a 256-block launch.
 hipError_t launch_xcc_probe(uint32_t* out, hipStream_t s);
 

@@ -62,19 +62,23 @@ __device__ __forceinline__ uint32_t xcc_id() {
   return v & 15u;
 }
 
-// Barrier of the 32 blocks of one XCD: every block publishes `sense` in its
-// own flag once its stores are in the L2, then waits until all 32 flags carry
-// it. Flags alternate between launches, so they never need clearing. Called
-// by every thread of the block.
-__device__ __forceinline__ void xcd_barrier(uint32_t* flags, int rank, uint32_t sense, uint32_t* err) {
+// Barrier of the 32 blocks of one XCD. Each block's flag counts the barriers
+// it has passed: every block publishes `target` (its flag at launch start plus
+// the barrier's number in the launch) once its stores are in the L2, then
+// waits until every flag of the group has reached it (compared as a wrapping
+// difference). All blocks pass every barrier, so the flags are equal at each
+// launch start and never need clearing; counting, not alternating, lets a
+// block that has left one barrier publish the next without misleading a block
+// still waiting at the first. Called by every thread of the block.
+__device__ __forceinline__ void xcd_barrier(uint32_t* flags, int rank, uint32_t target, uint32_t* err) {
   wait_loads();  // this wave's stores (and loads) are complete
   __syncthreads();
   if (threadIdx.x < 64) {
     const int lane = threadIdx.x;
-    if (lane == 0) flags[rank] = sense;
+    if (lane == 0) flags[rank] = target;
     for (int n = 0;; ++n) {
-      const uint32_t f = lane < kGroupBlocks ? l2_load_b32(flags + lane) : sense;
-      if (__all(f == sense)) break;
+      const uint32_t f = lane < kGroupBlocks ? l2_load_b32(flags + lane) : target;
+      if (__all((int)(f - target) >= 0)) break;
       if (n >= kSpinLimit) {
         if (lane == 0) atomicOr(err, 2u);
         break;
@@ -114,7 +118,7 @@ __global__ __launch_bounds__(256) void k_mlp_xcd(MlpXcdArgs a) {
   float4 pv[NPART];
 #pragma unroll
   for (int k = 0; k < NPART; ++k) pv[k] = reinterpret_cast<const float4*>(a.part + k * kHidden)[t];
-  // this block's flag as it left it in the previous launch (on this XCD)
+  // this block's barrier count as it left it in the previous launch
   const uint32_t own = flags[rank];
   issue_fence();
   u32x4 cg[2], cu[2];
@@ -145,9 +149,9 @@ __global__ __launch_bounds__(256) void k_mlp_xcd(MlpXcdArgs a) {
   for (int p = 0; p < 2; ++p) {
     const int row = wide ? rank * 32 + p * 16 + (t >> 4) : rank * 32 + (t >> 3);
     drow[p] = row;
-    dc[p] = *reinterpret_cast<const u32x4*>(a.down.w + (size_t)row * 448 + dslice * 4);
-    ds[p] = a.down.s[(size_t)row * 56 + dslice / 2];
-    db[p] = a.down.b[(size_t)row * 56 + dslice / 2];
+    dc[p] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(a.down.w + (size_t)row * 448 + dslice * 4));
+    ds[p] = __builtin_nontemporal_load(a.down.s + (size_t)row * 56 + dslice / 2);
+    db[p] = __builtin_nontemporal_load(a.down.b + (size_t)row * 56 + dslice / 2);
   }
   issue_fence();
 
@@ -200,7 +204,7 @@ __global__ __launch_bounds__(256) void k_mlp_xcd(MlpXcdArgs a) {
   }
 
   // ---- exchange the XCD's activation elements
-  xcd_barrier(flags, rank, own ^ 1u, a.err);
+  xcd_barrier(flags, rank, own + 1u, a.err);
 
   // ---- phase 2: octet x of every down row of this block
   const int aoff = wide ? (L < 8 ? 32 * L : 256 + 32 * (L - 8)) : 32 * L;
@@ -214,6 +218,260 @@ __global__ __launch_bounds__(256) void k_mlp_xcd(MlpXcdArgs a) {
     v = tree4(v);
     v = v + dpp_half_mirror(v);         // the octet's tree over its 8 leaves
     if (L == 0) a.dpart[x * kHidden + drow[p]] = v;
+  }
+}
+
+// Two bf16 values read from the XCD's L2 (one statement with its wait).
+__device__ __forceinline__ uint2 l2_load_2xu16(const uint16_t* p0, const uint16_t* p1) {
+  uint32_t a, b;
+  asm volatile(
+      "global_load_ushort %0, %2, off sc1\n\t"
+      "global_load_ushort %1, %3, off sc1\n\t"
+      "s_waitcnt vmcnt(0)"
+      : "=&v"(a), "=&v"(b)
+      : "v"(p0), "v"(p1)
+      : "memory");
+  return make_uint2(a, b);
+}
+
+// ---- k_gdn_xcd: a Gated DeltaNet layer up to its out_proj head partials ----
+// It replaces the input-norm + projection launch and the recurrence launch.
+// XCD x holds heads x and x + 8, 16 blocks each (rank r: head x + 8 (r >> 4),
+// block j = r & 15 of the head). Phase 1: the layer input (embedding row, or
+// the stream after the previous layer's mixer plus its MLP's down partials),
+// RMSNorm, and the block's rows of the head: channels 8j .. 8j+7 of q, k, v
+// and z (block 0 of the head also a and b), one half-wave per row as
+// k_norm_multi; the q/k/v rows go to the ring and through the convolution with
+// the ring's three older taps and SiLU. Exchange. Phase 2: q and k L2-norms,
+// gates, and the delta rule for value rows 8j .. 8j+7 (16 lanes per row,
+// k_gdn_recur_out's order). Exchange. Phase 3: the head's gated RMSNorm and
+// out_proj rows 64j .. 64j+63 over the head's 128 columns: the head partials
+// k_gdn_recur_out writes, bit for bit.
+constexpr int kHx = 648;  // exchange elements per head: q k v z y (128 each), a, b, pad
+constexpr int kXq = 0, kXk = 128, kXv = 256, kXz = 384, kXy = 512, kXab = 640;
+
+template <bool EMBED>
+__global__ __launch_bounds__(256) void k_gdn_xcd(GdnXcdArgs a) {
+  __shared__ float hs[EMBED ? 1 : kNormLds];
+  __shared__ float norm_lds[kNormLds];
+  __shared__ float qk[256];
+  __shared__ float vv[8];
+  __shared__ float red[4];
+  __shared__ float gates[2];
+  __shared__ float yv[128];
+  __shared__ float xg[128 + 4];
+  __shared__ float ginv;
+  const int t = threadIdx.x, lane = t & 63, wave = t >> 6, half = lane >> 5, sl = lane & 31;
+  const int hw = wave * 2 + half;  // half-wave 0..7
+  const int x = (int)xcc_id() & 7, rank = blockIdx.x >> 3;
+  const int h = x + 8 * (rank >> 4), j = rank & 15;
+  uint32_t* flags = a.flags + x * kGroupBlocks;
+  uint16_t* xb = a.xbuf + (size_t)(x * 2 + (rank >> 4)) * kHx;
+
+  // ---- loads in the order they are needed: input, gain, position, sense;
+  // projection rows; conv taps; state rows; out_proj slice
+  const Raw64 graw = EMBED ? load_raw64(a.gain + sl * 32) : Raw64{};
+  uint2 x4 = EMBED ? uint2{0u, 0u} : reinterpret_cast<const uint2*>(a.x)[t];
+  const uint2 g4 = EMBED ? uint2{0u, 0u} : reinterpret_cast<const uint2*>(a.gain)[t];
+  float4 dp[EMBED ? 1 : 8];
+  if (!EMBED) {
+#pragma unroll
+    for (int k = 0; k < 8; ++k) dp[k] = reinterpret_cast<const float4*>(a.dpart + k * kHidden)[t];
+  }
+  int zero;
+  asm volatile("v_mov_b32 %0, 0" : "=v"(zero));
+  const int pos = (&a.st->pos)[zero];
+  const uint32_t own = flags[rank];
+  issue_fence();
+  // pass p: matrix p (q, k, v rows of in_proj_qkv, then z), channel 8j + hw
+  u32x4 c[5];
+  uint32_t sv[5], bv[5];
+#pragma unroll
+  for (int p = 0; p < 4; ++p) {
+    const Q4& m = p < 3 ? a.qkv : a.z;
+    const int row = (p < 3 ? p * 2048 : 0) + h * 128 + 8 * j + hw;
+    c[p] = *reinterpret_cast<const u32x4*>(m.w + (size_t)row * 128 + sl * 4);
+    sv[p] = m.s[(size_t)row * 16 + sl / 2];
+    bv[p] = m.b[(size_t)row * 16 + sl / 2];
+  }
+  // block 0 of the head: a (half-wave 0) and b (half-wave 1) of the head
+  const bool ab_pass = j == 0 && hw < 2;
+  {
+    const Q4& m = hw == 0 ? a.a : a.b;
+    const int row = ab_pass ? h : 0;
+    c[4] = *reinterpret_cast<const u32x4*>(m.w + (size_t)row * 128 + sl * 4);
+    sv[4] = m.s[(size_t)row * 16 + sl / 2];
+    bv[4] = m.b[(size_t)row * 16 + sl / 2];
+  }
+  // conv taps of the half-wave's q, k, v channels (ring slots of pos-3..pos-1)
+  uint32_t tap[3][4];
+  uint2 cw[3];
+#pragma unroll
+  for (int p = 0; p < 3; ++p) {
+    const int ch = p * 2048 + h * 128 + 8 * j + hw;
+#pragma unroll
+    for (int sl4 = 0; sl4 < 4; ++sl4) tap[p][sl4] = a.ring[(size_t)sl4 * kConv + ch];
+    cw[p] = *reinterpret_cast<const uint2*>(a.conv_w + (size_t)ch * 4);
+  }
+  // state: value rows 8j .. 8j+7 of the head, 16 lanes x 8 keys (t < 128)
+  const int srow = 8 * j + (t >> 4) % 8, sj = t & 15;
+  float S[8];
+  {
+    const float* sp = a.state + ((size_t)(h * 128 + srow)) * 128 + 8 * sj;
+    const float4 lo = reinterpret_cast<const float4*>(sp)[0];
+    const float4 hi = reinterpret_cast<const float4*>(sp)[1];
+    S[0] = lo.x; S[1] = lo.y; S[2] = lo.z; S[3] = lo.w;
+    S[4] = hi.x; S[5] = hi.y; S[6] = hi.z; S[7] = hi.w;
+  }
+  // out_proj: row 64j + t/4, K slice 4h + t%4
+  const int orow = 64 * j + (t >> 2), osl = 4 * h + (t & 3);
+  const u32x4 oc = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(a.out.w + (size_t)orow * 256 + osl * 4));
+  const uint32_t osv = __builtin_nontemporal_load(a.out.s + (size_t)orow * 32 + osl / 2);
+  const uint32_t obv = __builtin_nontemporal_load(a.out.b + (size_t)orow * 32 + osl / 2);
+  issue_fence();
+
+  // ---- phase 1: input, RMSNorm, projection rows, ring, convolution
+  float xv[32];
+  if (EMBED) {
+    const uint32_t tok = a.st->token;
+    embed_slice(a.embed, tok, sl, xv);
+    if (blockIdx.x == 0 && t < 32) store_bf16x32(a.h_out + sl * 32, xv);
+  } else {
+    const float hf[4] = {bf_lo(x4.x), bf_hi(x4.x), bf_lo(x4.y), bf_hi(x4.y)};
+    float hn[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      float cc[8];
+#pragma unroll
+      for (int k = 0; k < 8; ++k) cc[k] = e == 0 ? dp[k].x : e == 1 ? dp[k].y : e == 2 ? dp[k].z : dp[k].w;
+      hn[e] = bf2f(f2bf(hf[e] + rbf(((cc[0] + cc[1]) + (cc[2] + cc[3])) + ((cc[4] + cc[5]) + (cc[6] + cc[7])))));
+    }
+    x4 = make_uint2(pack_bf2(hn[0], hn[1]), pack_bf2(hn[2], hn[3]));
+    if (blockIdx.x == 0) reinterpret_cast<uint2*>(a.h_out)[t] = x4;
+    *reinterpret_cast<float4*>(hs + (t >> 3) * 36 + (t & 7) * 4) = make_float4(hn[0], hn[1], hn[2], hn[3]);
+    __syncthreads();
+    const float4* rp = reinterpret_cast<const float4*>(hs + sl * 36);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const float4 q = rp[i];
+      xv[4 * i] = q.x; xv[4 * i + 1] = q.y; xv[4 * i + 2] = q.z; xv[4 * i + 3] = q.w;
+    }
+  }
+  float xn[32];
+  if (EMBED) norm_slice_1024(xv, graw, xn);
+  else norm_block_1024(xv, x4, g4, norm_lds, xn);
+  float xr[32];
+  const float xs = prep_slice(xn, xr);
+  const int slot_new = pos & 3;
+#pragma unroll
+  for (int p = 0; p < 4; ++p) {
+    const uint32_t raw = f2bf(tree32(q4_slice(c[p], sv[p], bv[p], xr, xs)));
+    if (sl == 0) {
+      if (p < 3) {
+        const int ch = p * 2048 + h * 128 + 8 * j + hw;
+        a.ring[(size_t)slot_new * kConv + ch] = (uint16_t)raw;
+        // taps pos-3 .. pos: ring slots (pos+1+t) & 3 for t < 3, then the new row
+        uint32_t xt[4];
+#pragma unroll
+        for (int tt = 0; tt < 3; ++tt) {
+          const int sidx = (pos + 1 + tt) & 3;
+          xt[tt] = sidx == 0 ? tap[p][0] : sidx == 1 ? tap[p][1] : sidx == 2 ? tap[p][2] : tap[p][3];
+        }
+        xt[3] = raw;
+        const float act = conv4_silu(xt, cw[p]);
+        xb[(p == 0 ? kXq : p == 1 ? kXk : kXv) + 8 * j + hw] = (uint16_t)f2bf(act);
+      } else {
+        xb[kXz + 8 * j + hw] = (uint16_t)raw;
+      }
+    }
+  }
+  if (j == 0 && wave == 0) {  // wave-uniform: half-waves 0 and 1 form a and b
+    const uint32_t raw = f2bf(tree32(q4_slice(c[4], sv[4], bv[4], xr, xs)));
+    if (sl == 0) xb[kXab + half] = (uint16_t)raw;
+  }
+  xcd_barrier(flags, rank, own + 1u, a.err);
+
+  // ---- phase 2: q/k L2 norms (k_gdn_recur_out's order), gates, delta rule
+  {
+    const uint2 qkr = l2_load_2xu16(xb + (t < 128 ? kXq + t : kXk + (t - 128)), xb + kXv + 8 * j + (t & 7));
+    const float v = bf2f(qkr.x);
+    const float ss = tree64(v * v);
+    if (lane == 0) red[wave] = ss;
+    if (t < 8) vv[t] = bf2f(qkr.y);
+    if (t == 8) {
+      const uint2 ab = l2_load_2xu16(xb + kXab, xb + kXab + 1);
+      const float ax = rbf(bf2f(ab.x) + bf2f(a.dt_bias[h]));
+      gates[0] = es_exp(-es_exp(a.a_log[h]) * softplus_bf(ax));
+      gates[1] = sigmoid_bf(bf2f(ab.y));
+    }
+    __syncthreads();
+    const float tot = t < 128 ? red[0] + red[1] : red[2] + red[3];
+    const float inv = 1.0f / sqrtf(tot / 128.0f + 1.0e-6f / 128.0f);
+    const float scale = t < 128 ? 0.0078125f : rbf(0.08838834764831845f);
+    qk[t] = rbf(rbf(v * inv) * scale);
+    __syncthreads();
+  }
+  if (t < 128) {  // waves 0 and 1: value rows 8j + t/16
+    const float g = gates[0], beta = gates[1];
+    float kk[8], qq[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      kk[i] = qk[128 + 8 * sj + i];
+      qq[i] = qk[8 * sj + i];
+    }
+    float mem = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      S[i] = S[i] * g;
+      mem = fmaf(S[i], kk[i], mem);
+    }
+    mem = tree16(mem);
+    const float delta = (vv[t >> 4] - mem) * beta;
+    float out = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      S[i] = fmaf(kk[i], delta, S[i]);
+      out = fmaf(S[i], qq[i], out);
+    }
+    out = tree16(out);
+    float* sp = a.state + ((size_t)(h * 128 + srow)) * 128 + 8 * sj;
+    reinterpret_cast<float4*>(sp)[0] = make_float4(S[0], S[1], S[2], S[3]);
+    reinterpret_cast<float4*>(sp)[1] = make_float4(S[4], S[5], S[6], S[7]);
+    if (sj == 0) xb[kXy + srow] = (uint16_t)f2bf(out);
+  }
+  xcd_barrier(flags, rank, own + 2u, a.err);
+
+  // ---- phase 3: gated RMSNorm of the head, out_proj rows 64j .. 64j+63
+  if (t < 128) {
+    const uint2 yz = l2_load_2xu16(xb + kXy + t, xb + kXz + t);
+    yv[t] = bf2f(yz.x);
+    xg[t + (t >> 5)] = bf2f(yz.y);  // z, replaced by the gated value below
+  }
+  __syncthreads();
+  if (t < 16) {
+    float ss = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) ss = fmaf(yv[t * 8 + i], yv[t * 8 + i], ss);
+    ss = tree16(ss);
+    if (t == 0) ginv = 1.0f / sqrtf(ss / 128.0f + 1e-6f);
+  }
+  __syncthreads();
+  if (t < 128) {
+    const float norm = rbf(rbf(yv[t] * ginv) * bf2f(a.norm_w[t]));
+    const float gz = xg[t + (t >> 5)];
+    const float sy = 1.0f / (1.0f + es_exp(fabsf(gz)));
+    const float sig = gz < 0.0f ? sy : 1.0f - sy;
+    xg[t + (t >> 5)] = rbf((gz * sig) * norm);
+  }
+  __syncthreads();
+  {
+    float ov[32], oxr[32];
+    const int s4 = t & 3;
+#pragma unroll
+    for (int q = 0; q < 32; ++q) ov[q] = xg[s4 * 33 + q];
+    const float oxs = prep_slice(ov, oxr);
+    const float part = tree4(q4_slice(oc, osv, obv, oxr, oxs));
+    if (s4 == 0) a.part[(size_t)h * 1024 + orow] = part;
   }
 }
 
@@ -234,6 +492,21 @@ hipError_t launch_mlp_xcd(const MlpXcdArgs& a, int nparts, hipStream_t s) {
     hipLaunchKernelGGL(k_mlp_xcd<8>, dim3(256), dim3(256), 0, s, a);
   else
     return hipErrorInvalidValue;
+  return hipGetLastError();
+}
+
+hipError_t launch_gdn_xcd(const GdnXcdArgs& a, hipStream_t s) {
+  const bool embed = a.embed.w != nullptr;
+  if (!a.gain || !a.h_out || !a.st || !a.qkv.w || !a.z.w || !a.a.w || !a.b.w || !a.out.w || !a.conv_w ||
+      !a.norm_w || !a.dt_bias || !a.a_log || !a.ring || !a.state || !a.part || !a.xbuf || !a.flags || !a.err ||
+      a.qkv.n != kConv || a.qkv.k != kHidden || a.z.n != 2048 || a.z.k != kHidden || a.a.n != kGdnHeads ||
+      a.a.k != kHidden || a.b.n != kGdnHeads || a.b.k != kHidden || a.out.n != kHidden || a.out.k != 2048)
+    return hipErrorInvalidValue;
+  if (embed ? (a.embed.k != kHidden) : (!a.x || !a.dpart)) return hipErrorInvalidValue;
+  if (embed)
+    hipLaunchKernelGGL(k_gdn_xcd<true>, dim3(256), dim3(256), 0, s, a);
+  else
+    hipLaunchKernelGGL(k_gdn_xcd<false>, dim3(256), dim3(256), 0, s, a);
   return hipGetLastError();
 }
 
