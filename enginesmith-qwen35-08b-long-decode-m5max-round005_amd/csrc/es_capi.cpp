@@ -1,5 +1,5 @@
 // extern "C" entry points declared in include/es_decode.h.
-#include "../../include/es_decode.h"
+#include "es_decode.h"
 
 #include <hip/hip_runtime.h>
 

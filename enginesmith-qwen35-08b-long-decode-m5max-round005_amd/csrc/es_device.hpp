@@ -237,6 +237,12 @@ __device__ __forceinline__ float q4_slice(const u32x4 c, uint32_t scale, uint32_
   return fmaf(xs, bf2f(bias), bf2f(scale) * q4_dot32(c, xr));
 }
 
+// The same with the group's scale and bias packed in one word (scale in the
+// low half, bias in the high half): one load where q4_slice takes two.
+__device__ __forceinline__ float q4_slice_sb(const u32x4 c, uint32_t sb, const float* xr, float xs) {
+  return fmaf(xs, bf_hi(sb), bf_lo(sb) * q4_dot32(c, xr));
+}
+
 // Load a 32-element bf16 slice (64 B) as floats.
 __device__ __forceinline__ void load_bf16x32(const uint16_t* p, float* out) {
   const u32x4* q = reinterpret_cast<const u32x4*>(p);

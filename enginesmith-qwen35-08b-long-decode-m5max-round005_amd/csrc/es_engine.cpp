@@ -199,6 +199,34 @@ int Engine::init(const void* blob, uint64_t bytes, std::string* err) {
   ES_HIP(hipStreamSynchronize(stream_), "init sync");
   fused_mlp_ = xcc[0] < 8;
   for (int b = 0; b < 256; ++b) fused_mlp_ = fused_mlp_ && xcc[b] == (xcc[0] + (uint32_t)b) % 8;
+  if (fused_mlp_) {
+    // the XCD kernels read each Q4 group's scale and bias as one word
+    for (auto& L : layers_) {
+      const size_t ffn_groups = (size_t)3584 * 16, down_groups = (size_t)1024 * 56;
+      L.gu_sb = static_cast<uint2*>(alloc(ffn_groups * sizeof(uint2)));
+      L.down_sb = static_cast<uint32_t*>(alloc(down_groups * 4));
+      if (!L.gu_sb || !L.down_sb) {
+        if (err) *err = "device allocation of packed group words failed";
+        return 2;
+      }
+      ES_HIP(launch_pack_sb2(L.gate.s, L.gate.b, L.up.s, L.up.b, L.gu_sb, ffn_groups, stream_), "pack");
+      ES_HIP(launch_pack_sb(L.down.s, L.down.b, L.down_sb, down_groups, stream_), "pack");
+      if (L.attention) continue;
+      L.qkv_sb = static_cast<uint32_t*>(alloc((size_t)kConv * 16 * 4));
+      L.z_sb = static_cast<uint32_t*>(alloc((size_t)2048 * 16 * 4));
+      L.ab_sb = static_cast<uint32_t*>(alloc((size_t)2 * kGdnHeads * 16 * 4));
+      L.out_sb = static_cast<uint32_t*>(alloc((size_t)1024 * 32 * 4));
+      if (!L.qkv_sb || !L.z_sb || !L.ab_sb || !L.out_sb) {
+        if (err) *err = "device allocation of packed group words failed";
+        return 2;
+      }
+      ES_HIP(launch_pack_sb(L.qkv.s, L.qkv.b, L.qkv_sb, (size_t)kConv * 16, stream_), "pack");
+      ES_HIP(launch_pack_sb(L.z.s, L.z.b, L.z_sb, (size_t)2048 * 16, stream_), "pack");
+      ES_HIP(launch_pack_sb(L.a.s, L.a.b, L.ab_sb, (size_t)kGdnHeads * 16, stream_), "pack");
+      ES_HIP(launch_pack_sb(L.b.s, L.b.b, L.ab_sb + kGdnHeads * 16, (size_t)kGdnHeads * 16, stream_), "pack");
+      ES_HIP(launch_pack_sb(L.out.s, L.out.b, L.out_sb, (size_t)1024 * 32, stream_), "pack");
+    }
+  }
   ES_HIP(hipMemsetAsync(err_, 0, 256 * sizeof(uint32_t), stream_), "memset");
   ES_HIP(hipMemsetAsync(xflags_, 0, 8 * 32 * sizeof(uint32_t), stream_), "memset");
   ES_HIP(hipStreamSynchronize(stream_), "init sync");
@@ -281,6 +309,8 @@ hipError_t Engine::enqueue_layers(hipStream_t s, int splits) {
         m.gate = L.gate;
         m.up = L.up;
         m.down = L.down;
+        m.gu_sb = L.gu_sb;
+        m.down_sb = L.down_sb;
         m.h_old = h_;
         m.part = proj_part_;
         m.h_mid = hmid_;
@@ -312,6 +342,10 @@ hipError_t Engine::enqueue_layers(hipStream_t s, int splits) {
       g.a = L.a;
       g.b = L.b;
       g.out = L.out;
+      g.qkv_sb = L.qkv_sb;
+      g.z_sb = L.z_sb;
+      g.ab_sb = L.ab_sb;
+      g.out_sb = L.out_sb;
       g.conv_w = L.conv_w;
       g.norm_w = L.gdn_norm;
       g.dt_bias = L.dt_bias;

@@ -23,6 +23,14 @@ struct LayerDev {
   const uint16_t* input_norm;
   const uint16_t* post_norm;
   Q4 gate, up, down;
+  // packed scale|bias<<16 group words of the XCD kernels (launch_pack_sb):
+  // (gate, up) interleaved, down; GDN qkv, z, a then b, out
+  uint2* gu_sb;
+  uint32_t* down_sb;
+  uint32_t* qkv_sb;
+  uint32_t* z_sb;
+  uint32_t* ab_sb;
+  uint32_t* out_sb;
   // GDN
   Q4 qkv, z, a, b, out;
   const uint16_t* conv_w;

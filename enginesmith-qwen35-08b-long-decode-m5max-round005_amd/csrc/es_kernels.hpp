@@ -145,6 +145,8 @@ hipError_t launch_attn_merge_out(const AttnArgs& a, const Q4& o, float* part, hi
 // epilogue bit for bit.
 struct MlpXcdArgs {
   Q4 gate, up, down;
+  const uint2* gu_sb;       // [3584, 16] (gate, up) scale|bias<<16 words (launch_pack_sb2)
+  const uint32_t* down_sb;  // [1024, 56] scale|bias<<16 words (launch_pack_sb)
   const uint16_t* h_old;    // [1024] residual stream before the mixer
   const float* part;        // [nparts, 1024] mixer partials
   uint16_t* h_mid;          // [1024] written: stream after the mixer
@@ -166,6 +168,12 @@ struct GdnXcdArgs {
   uint16_t* h_out;          // [1024] the layer input
   const uint16_t* gain;     // input norm [1024]
   Q4 qkv, z, a, b, out;
+  // scale|bias<<16 words of the same matrices (launch_pack_sb): qkv [6144,16],
+  // z [2048,16], a then b [2,16,16], out [1024,32]
+  const uint32_t* qkv_sb;
+  const uint32_t* z_sb;
+  const uint32_t* ab_sb;
+  const uint32_t* out_sb;
   const uint16_t* conv_w;   // [6144, 4]
   const uint16_t* norm_w;   // [128]
   const uint16_t* dt_bias;  // [16]
@@ -179,6 +187,12 @@ struct GdnXcdArgs {
   const StepState* st;
 };
 hipError_t launch_gdn_xcd(const GdnXcdArgs& a, hipStream_t s);
+// Packed group words for the XCD kernels: out[i] = s[i] | b[i] << 16 (the
+// bf16 scale and bias of one Q4 group), n groups; pack_sb2 interleaves two
+// matrices of the same shape: out[i] = (s0|b0<<16, s1|b1<<16).
+hipError_t launch_pack_sb(const uint16_t* s, const uint16_t* b, uint32_t* out, size_t n, hipStream_t st);
+hipError_t launch_pack_sb2(const uint16_t* s0, const uint16_t* b0, const uint16_t* s1, const uint16_t* b1,
+                           uint2* out, size_t n, hipStream_t st);
 // out[b] = XCC_ID of block b of a 256-block launch.
 hipError_t launch_xcc_probe(uint32_t* out, hipStream_t s);
 

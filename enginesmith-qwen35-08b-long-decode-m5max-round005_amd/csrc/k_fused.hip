@@ -110,6 +110,9 @@ __global__ __launch_bounds__(256) void k_mlp_xcd(MlpXcdArgs a) {
   const int x = (int)xcc_id() & 7, rank = blockIdx.x >> 3;
   const int nact = x < 6 ? 16 : 8;  // activation elements of this block
   uint32_t* flags = a.flags + x * kGroupBlocks;
+  // every pointer argument in scalar registers at once (one wait)
+  asm volatile("" :: "s"(a.gate.w), "s"(a.up.w), "s"(a.gu_sb), "s"(a.down.w), "s"(a.down_sb), "s"(a.h_old),
+               "s"(a.part), "s"(a.h_mid), "s"(a.gain), "s"(a.dpart), "s"(a.xact), "s"(a.flags), "s"(a.err));
 
   // ---- loads: residual, gain and mixer partials; the sense of this launch;
   // gate/up weights; the down weights of phase 2
@@ -122,7 +125,7 @@ __global__ __launch_bounds__(256) void k_mlp_xcd(MlpXcdArgs a) {
   const uint32_t own = flags[rank];
   issue_fence();
   u32x4 cg[2], cu[2];
-  uint32_t sg[2], bg[2], su[2], bu[2];
+  uint32_t gsb[2], usb[2];
   int er[2];
 #pragma unroll
   for (int p = 0; p < 2; ++p) {
@@ -131,10 +134,9 @@ __global__ __launch_bounds__(256) void k_mlp_xcd(MlpXcdArgs a) {
     er[p] = j < nact ? e : -1;
     cg[p] = *reinterpret_cast<const u32x4*>(a.gate.w + (size_t)e * 128 + sl * 4);
     cu[p] = *reinterpret_cast<const u32x4*>(a.up.w + (size_t)e * 128 + sl * 4);
-    sg[p] = a.gate.s[(size_t)e * 16 + sl / 2];
-    bg[p] = a.gate.b[(size_t)e * 16 + sl / 2];
-    su[p] = a.up.s[(size_t)e * 16 + sl / 2];
-    bu[p] = a.up.b[(size_t)e * 16 + sl / 2];
+    const uint2 gu = a.gu_sb[(size_t)e * 16 + sl / 2];
+    gsb[p] = gu.x;
+    usb[p] = gu.y;
   }
   // phase 2: down rows 32 rank .. +31; x < 6: 16 lanes per row (lane L holds
   // slice 8x+L, or 8x+64+L-8 for L >= 8), two passes of 16 rows; x >= 6: 8
@@ -143,15 +145,14 @@ __global__ __launch_bounds__(256) void k_mlp_xcd(MlpXcdArgs a) {
   const int L = wide ? (t & 15) : (t & 7);
   const int dslice = wide ? (L < 8 ? 8 * x + L : 8 * x + 64 + (L - 8)) : 8 * x + L;
   u32x4 dc[2];
-  uint32_t ds[2], db[2];
+  uint32_t dsb[2];
   int drow[2];
 #pragma unroll
   for (int p = 0; p < 2; ++p) {
     const int row = wide ? rank * 32 + p * 16 + (t >> 4) : rank * 32 + (t >> 3);
     drow[p] = row;
     dc[p] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(a.down.w + (size_t)row * 448 + dslice * 4));
-    ds[p] = __builtin_nontemporal_load(a.down.s + (size_t)row * 56 + dslice / 2);
-    db[p] = __builtin_nontemporal_load(a.down.b + (size_t)row * 56 + dslice / 2);
+    dsb[p] = __builtin_nontemporal_load(a.down_sb + (size_t)row * 56 + dslice / 2);
   }
   issue_fence();
 
@@ -194,8 +195,8 @@ __global__ __launch_bounds__(256) void k_mlp_xcd(MlpXcdArgs a) {
   uint16_t* xact = a.xact + x * 512;
 #pragma unroll
   for (int p = 0; p < 2; ++p) {
-    const float g = tree32(q4_slice(cg[p], sg[p], bg[p], xr, xs));
-    const float u = tree32(q4_slice(cu[p], su[p], bu[p], xr, xs));
+    const float g = tree32(q4_slice_sb(cg[p], gsb[p], xr, xs));
+    const float u = tree32(q4_slice_sb(cu[p], usb[p], xr, xs));
     if (sl == 0 && er[p] >= 0) {
       const float gb = rbf(g), ub = rbf(u);
       const float silu = rbf(gb * sigmoid_bf(gb));
@@ -213,7 +214,7 @@ __global__ __launch_bounds__(256) void k_mlp_xcd(MlpXcdArgs a) {
 #pragma unroll
   for (int p = 0; p < 2; ++p) {
     if (!wide && p == 1) break;
-    float v = q4_slice(dc[p], ds[p], db[p], xr, xs);
+    float v = q4_slice_sb(dc[p], dsb[p], xr, xs);
     if (wide) v = v + dpp_row_ror8(v);  // leaf: slices 8x+L and 8x+64+L
     v = tree4(v);
     v = v + dpp_half_mirror(v);         // the octet's tree over its 8 leaves
@@ -232,6 +233,22 @@ __device__ __forceinline__ uint2 l2_load_2xu16(const uint16_t* p0, const uint16_
       : "v"(p0), "v"(p1)
       : "memory");
   return make_uint2(a, b);
+}
+
+// Value of lane K of each row of 16 lanes, in every lane of the row (DPP
+// row_newbcast).
+template <int K>
+__device__ __forceinline__ uint32_t row_bcast(uint32_t v) {
+  return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x150 + K, 0xf, 0xf, false);
+}
+// Taps (slots 0..3) and conv weights of pass P from the lanes that loaded them.
+template <int P>
+__device__ __forceinline__ void row_gather(uint32_t tapv, uint2 cwv, uint32_t (&tap)[3][4], uint2 (&cw)[3]) {
+  tap[P][0] = row_bcast<4 * P>(tapv);
+  tap[P][1] = row_bcast<4 * P + 1>(tapv);
+  tap[P][2] = row_bcast<4 * P + 2>(tapv);
+  tap[P][3] = row_bcast<4 * P + 3>(tapv);
+  cw[P] = make_uint2(row_bcast<12 + P>(cwv.x), row_bcast<12 + P>(cwv.y));
 }
 
 // ---- k_gdn_xcd: a Gated DeltaNet layer up to its out_proj head partials ----
@@ -267,6 +284,13 @@ __global__ __launch_bounds__(256) void k_gdn_xcd(GdnXcdArgs a) {
   const int h = x + 8 * (rank >> 4), j = rank & 15;
   uint32_t* flags = a.flags + x * kGroupBlocks;
   uint16_t* xb = a.xbuf + (size_t)(x * 2 + (rank >> 4)) * kHx;
+  // every pointer argument in scalar registers at once: one wait for the
+  // argument fetch instead of one per batch between the vector loads
+  asm volatile("" :: "s"(a.x), "s"(a.dpart), "s"(a.h_out), "s"(a.gain), "s"(a.qkv.w), "s"(a.qkv_sb),
+               "s"(a.z.w), "s"(a.z_sb), "s"(a.a.w), "s"(a.b.w), "s"(a.ab_sb), "s"(a.out.w), "s"(a.out_sb),
+               "s"(a.conv_w), "s"(a.norm_w));
+  asm volatile("" :: "s"(a.dt_bias), "s"(a.a_log), "s"(a.ring), "s"(a.state), "s"(a.part), "s"(a.st),
+               "s"(a.embed.w), "s"(a.embed.s), "s"(a.embed.b), "s"(a.flags), "s"(a.xbuf), "s"(a.err));
 
   // ---- loads in the order they are needed: input, gain, position, sense;
   // projection rows; conv taps; state rows; out_proj slice
@@ -285,38 +309,35 @@ __global__ __launch_bounds__(256) void k_gdn_xcd(GdnXcdArgs a) {
   issue_fence();
   // pass p: matrix p (q, k, v rows of in_proj_qkv, then z), channel 8j + hw
   u32x4 c[5];
-  uint32_t sv[5], bv[5];
+  uint32_t sbw[5];
 #pragma unroll
   for (int p = 0; p < 4; ++p) {
-    const Q4& m = p < 3 ? a.qkv : a.z;
     const int row = (p < 3 ? p * 2048 : 0) + h * 128 + 8 * j + hw;
-    c[p] = *reinterpret_cast<const u32x4*>(m.w + (size_t)row * 128 + sl * 4);
-    sv[p] = m.s[(size_t)row * 16 + sl / 2];
-    bv[p] = m.b[(size_t)row * 16 + sl / 2];
+    c[p] = *reinterpret_cast<const u32x4*>((p < 3 ? a.qkv.w : a.z.w) + (size_t)row * 128 + sl * 4);
+    sbw[p] = (p < 3 ? a.qkv_sb : a.z_sb)[(size_t)row * 16 + sl / 2];
   }
-  // block 0 of the head: a (half-wave 0) and b (half-wave 1) of the head
+  // block 0 of the head: a (half-wave 0) and b (half-wave 1) of the head.
+  // The half-waves of a wave differ, so the pointers are chosen per lane from
+  // values already in scalar registers (choosing between the two argument
+  // structs per lane would read them with vector loads, and waiting for those
+  // would also wait for the input loads issued before them).
   const bool ab_pass = j == 0 && hw < 2;
   {
-    const Q4& m = hw == 0 ? a.a : a.b;
+    const bool is_a = hw == 0;
     const int row = ab_pass ? h : 0;
-    c[4] = *reinterpret_cast<const u32x4*>(m.w + (size_t)row * 128 + sl * 4);
-    sv[4] = m.s[(size_t)row * 16 + sl / 2];
-    bv[4] = m.b[(size_t)row * 16 + sl / 2];
+    c[4] = *reinterpret_cast<const u32x4*>((is_a ? a.a.w : a.b.w) + (size_t)row * 128 + sl * 4);
+    sbw[4] = a.ab_sb[(size_t)((is_a ? 0 : kGdnHeads) + row) * 16 + sl / 2];
   }
-  // conv taps of the half-wave's q, k, v channels (ring slots of pos-3..pos-1)
-  uint32_t tap[3][4];
-  uint2 cw[3];
-#pragma unroll
-  for (int p = 0; p < 3; ++p) {
-    const int ch = p * 2048 + h * 128 + 8 * j + hw;
-#pragma unroll
-    for (int sl4 = 0; sl4 < 4; ++sl4) tap[p][sl4] = a.ring[(size_t)sl4 * kConv + ch];
-    cw[p] = *reinterpret_cast<const uint2*>(a.conv_w + (size_t)ch * 4);
-  }
+  // conv taps of the half-wave's q, k, v channels (ring slots of pos-3..pos)
+  // and their conv weights, one load each across the half-wave: lane l < 12
+  // holds slot l & 3 of pass l >> 2, lane 12 + p the weights of pass p
+  const int tl = sl < 12 ? sl : 0, cl = sl >= 12 && sl < 15 ? sl - 12 : 0;
+  const uint32_t tapv = a.ring[(size_t)(tl & 3) * kConv + (tl >> 2) * 2048 + h * 128 + 8 * j + hw];
+  const uint2 cwv = *reinterpret_cast<const uint2*>(a.conv_w + (size_t)(cl * 2048 + h * 128 + 8 * j + hw) * 4);
   // state: value rows 8j .. 8j+7 of the head, 16 lanes x 8 keys (t < 128)
   const int srow = 8 * j + (t >> 4) % 8, sj = t & 15;
-  float S[8];
-  {
+  float S[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
+  if (t < 128) {
     const float* sp = a.state + ((size_t)(h * 128 + srow)) * 128 + 8 * sj;
     const float4 lo = reinterpret_cast<const float4*>(sp)[0];
     const float4 hi = reinterpret_cast<const float4*>(sp)[1];
@@ -326,8 +347,7 @@ __global__ __launch_bounds__(256) void k_gdn_xcd(GdnXcdArgs a) {
   // out_proj: row 64j + t/4, K slice 4h + t%4
   const int orow = 64 * j + (t >> 2), osl = 4 * h + (t & 3);
   const u32x4 oc = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(a.out.w + (size_t)orow * 256 + osl * 4));
-  const uint32_t osv = __builtin_nontemporal_load(a.out.s + (size_t)orow * 32 + osl / 2);
-  const uint32_t obv = __builtin_nontemporal_load(a.out.b + (size_t)orow * 32 + osl / 2);
+  const uint32_t osb = __builtin_nontemporal_load(a.out_sb + (size_t)orow * 32 + osl / 2);
   issue_fence();
 
   // ---- phase 1: input, RMSNorm, projection rows, ring, convolution
@@ -363,9 +383,16 @@ __global__ __launch_bounds__(256) void k_gdn_xcd(GdnXcdArgs a) {
   float xr[32];
   const float xs = prep_slice(xn, xr);
   const int slot_new = pos & 3;
+  // lane 0 of each half-wave takes the taps and weights of its row of 16
+  // lanes (lanes 0-15 and 32-47) by DPP row broadcast
+  uint32_t tap[3][4];
+  uint2 cw[3];
+  row_gather<0>(tapv, cwv, tap, cw);
+  row_gather<1>(tapv, cwv, tap, cw);
+  row_gather<2>(tapv, cwv, tap, cw);
 #pragma unroll
   for (int p = 0; p < 4; ++p) {
-    const uint32_t raw = f2bf(tree32(q4_slice(c[p], sv[p], bv[p], xr, xs)));
+    const uint32_t raw = f2bf(tree32(q4_slice_sb(c[p], sbw[p], xr, xs)));
     if (sl == 0) {
       if (p < 3) {
         const int ch = p * 2048 + h * 128 + 8 * j + hw;
@@ -386,7 +413,7 @@ __global__ __launch_bounds__(256) void k_gdn_xcd(GdnXcdArgs a) {
     }
   }
   if (j == 0 && wave == 0) {  // wave-uniform: half-waves 0 and 1 form a and b
-    const uint32_t raw = f2bf(tree32(q4_slice(c[4], sv[4], bv[4], xr, xs)));
+    const uint32_t raw = f2bf(tree32(q4_slice_sb(c[4], sbw[4], xr, xs)));
     if (sl == 0) xb[kXab + half] = (uint16_t)raw;
   }
   xcd_barrier(flags, rank, own + 1u, a.err);
@@ -470,9 +497,20 @@ __global__ __launch_bounds__(256) void k_gdn_xcd(GdnXcdArgs a) {
 #pragma unroll
     for (int q = 0; q < 32; ++q) ov[q] = xg[s4 * 33 + q];
     const float oxs = prep_slice(ov, oxr);
-    const float part = tree4(q4_slice(oc, osv, obv, oxr, oxs));
+    const float part = tree4(q4_slice_sb(oc, osb, oxr, oxs));
     if (s4 == 0) a.part[(size_t)h * 1024 + orow] = part;
   }
+}
+
+__global__ __launch_bounds__(256) void k_pack_sb(const uint16_t* s, const uint16_t* b, uint32_t* out, size_t n) {
+  const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+  if (i < n) out[i] = (uint32_t)s[i] | (uint32_t)b[i] << 16;
+}
+
+__global__ __launch_bounds__(256) void k_pack_sb2(const uint16_t* s0, const uint16_t* b0, const uint16_t* s1,
+                                                  const uint16_t* b1, uint2* out, size_t n) {
+  const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+  if (i < n) out[i] = make_uint2((uint32_t)s0[i] | (uint32_t)b0[i] << 16, (uint32_t)s1[i] | (uint32_t)b1[i] << 16);
 }
 
 __global__ __launch_bounds__(256) void k_xcc_probe(uint32_t* out) {
@@ -484,7 +522,7 @@ __global__ __launch_bounds__(256) void k_xcc_probe(uint32_t* out) {
 hipError_t launch_mlp_xcd(const MlpXcdArgs& a, int nparts, hipStream_t s) {
   if (!a.gate.w || !a.up.w || !a.down.w || a.gate.k != kHidden || a.up.k != kHidden || a.gate.n != kFfn ||
       a.up.n != kFfn || a.down.n != kHidden || a.down.k != kFfn || !a.h_old || !a.part || !a.h_mid ||
-      a.h_mid == a.h_old || !a.gain || !a.dpart || !a.xact || !a.flags || !a.err)
+      a.h_mid == a.h_old || !a.gain || !a.dpart || !a.xact || !a.flags || !a.err || !a.gu_sb || !a.down_sb)
     return hipErrorInvalidValue;
   if (nparts == 16)
     hipLaunchKernelGGL(k_mlp_xcd<16>, dim3(256), dim3(256), 0, s, a);
@@ -499,6 +537,7 @@ hipError_t launch_gdn_xcd(const GdnXcdArgs& a, hipStream_t s) {
   const bool embed = a.embed.w != nullptr;
   if (!a.gain || !a.h_out || !a.st || !a.qkv.w || !a.z.w || !a.a.w || !a.b.w || !a.out.w || !a.conv_w ||
       !a.norm_w || !a.dt_bias || !a.a_log || !a.ring || !a.state || !a.part || !a.xbuf || !a.flags || !a.err ||
+      !a.qkv_sb || !a.z_sb || !a.ab_sb || !a.out_sb ||
       a.qkv.n != kConv || a.qkv.k != kHidden || a.z.n != 2048 || a.z.k != kHidden || a.a.n != kGdnHeads ||
       a.a.k != kHidden || a.b.n != kGdnHeads || a.b.k != kHidden || a.out.n != kHidden || a.out.k != 2048)
     return hipErrorInvalidValue;
@@ -507,6 +546,19 @@ hipError_t launch_gdn_xcd(const GdnXcdArgs& a, hipStream_t s) {
     hipLaunchKernelGGL(k_gdn_xcd<true>, dim3(256), dim3(256), 0, s, a);
   else
     hipLaunchKernelGGL(k_gdn_xcd<false>, dim3(256), dim3(256), 0, s, a);
+  return hipGetLastError();
+}
+
+hipError_t launch_pack_sb(const uint16_t* s, const uint16_t* b, uint32_t* out, size_t n, hipStream_t st) {
+  if (!s || !b || !out || n == 0 || n > ((size_t)1 << 32)) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(k_pack_sb, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, s, b, out, n);
+  return hipGetLastError();
+}
+
+hipError_t launch_pack_sb2(const uint16_t* s0, const uint16_t* b0, const uint16_t* s1, const uint16_t* b1,
+                           uint2* out, size_t n, hipStream_t st) {
+  if (!s0 || !b0 || !s1 || !b1 || !out || n == 0 || n > ((size_t)1 << 32)) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(k_pack_sb2, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, s0, b0, s1, b1, out, n);
   return hipGetLastError();
 }
 
