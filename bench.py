@@ -34,6 +34,7 @@ KV_BYTES_PER_POS = 6 * 2 * 2 * 256 * 2               # 6 layers x {K,V} x 2 head
 FUSED_BYTES_PER_POS = 2 * 2 * 256 * 2
 FUSED_FIXED_BYTES = 8 * 512 * 2 + 2 * 2 * 256 * 2 + 2 * 2 * 256 * 2 + 8 * 64 * (256 + 2) * 4
 PROFILES = os.path.join(ROOT, "profiles")
+GEN_STEPS = 256  # generate() wall time per context
 
 
 def committed_traffic(kernel, ctx):
@@ -81,27 +82,76 @@ def oracle_from_gpu_state(eng, blob, position, extra):
     return m
 
 
-def cpu_baseline(orc, first, stream, ctx):
-    """Oracle decode steps on the host cores from the GPU's post-prefill state
-    (bounded sample), replaying the GPU's greedy stream teacher-forced: the
-    timed CPU baseline and the token agreement of the same steps."""
+def bf16_random(r, n, scale=1.0):
+    """n bf16 values of N(0, scale) (upper halves of the float32 bits)."""
+    return (r.normal(0.0, scale, n).astype(np.float32).view(np.uint32) >> 16).astype(np.uint16)
+
+
+def median_time(fn, reps):
+    ts = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        fn()
+        ts.append(time.perf_counter() - t0)
+    return float(np.median(ts))
+
+
+def cpu_isolated(views, contexts, reps=3):
+    """Oracle timings of the path's pieces on the host cores (median of reps,
+    the oracle's current thread count): the Q4 matvec at the model's four
+    shapes, one GDN step of all 18 layers (conv, gates and delta rule over 16
+    heads), and the decode attention of the 6 GQA layers at each context over
+    synthetic K/V rows (one layer timed, times 6)."""
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import oracle as O
-    cores = os.cpu_count() or 1
-    threads = min(cores, 16)
+    r = np.random.default_rng(7)
+    qmv = {}
+    for name, n, k in (("layers.0.mlp.gate_proj", 3584, 1024), ("layers.0.mlp.down_proj", 1024, 3584),
+                       ("layers.0.linear_attn.in_proj_qkv", 6144, 1024), ("embed_tokens", VOCAB, 1024)):
+        codes = views[name + ".weight"].reshape(n, k // 8)
+        sc = views[name + ".scales"].reshape(n, k // 64)
+        bi = views[name + ".biases"].reshape(n, k // 64)
+        x = bf16_random(r, k)
+        dt = median_time(lambda: O.q4_matvec(codes, sc, bi, x), reps)
+        nbytes = codes.nbytes + sc.nbytes + bi.nbytes + 2 * (k + n)
+        qmv[f"{k}->{n}"] = dict(us=round(dt * 1e6, 1), GBs=round(nbytes / dt / 1e9, 2))
+    gdn_layers = [l for l in range(N_LAYERS) if l % 4 != 3]
+    raw, a, b = bf16_random(r, 6144, 0.5), bf16_random(r, 16), bf16_random(r, 16)
+    hist = {l: np.zeros((3, 6144), dtype=np.uint16) for l in gdn_layers}
+    state = {l: np.zeros((16, 128, 128), dtype=np.float32) for l in gdn_layers}
+
+    def gdn_step():
+        for l in gdn_layers:
+            g = f"layers.{l}.linear_attn"
+            conv, gate, beta = O.gdn_conv_prepare(raw, hist[l], views[g + ".conv1d.weight"], a, b,
+                                                  views[g + ".A_log"], views[g + ".dt_bias"])
+            O.gdn_recur(conv, gate, beta, state[l])
+
+    gdn_s = median_time(gdn_step, reps)
+    cap = max(contexts) + 1
+    kc = bf16_random(r, 2 * cap * 256, 0.5).reshape(2, cap, 256)
+    vc = bf16_random(r, 2 * cap * 256, 0.5).reshape(2, cap, 256)
+    query, q_proj = bf16_random(r, 2048, 0.1), bf16_random(r, 4096)
+    gqa = {}
+    for ctx in contexts:
+        dt = median_time(lambda: O.attn_decode_gated(query, kc, vc, ctx, cap, q_proj), reps)
+        gqa[str(ctx)] = dict(us_6_layers=round(6 * dt * 1e6, 1), GBs=round(ctx * 2048 / dt / 1e9, 2))
+    return dict(q4_matvec=qmv, gdn_18_layers_us=round(gdn_s * 1e6, 1), gqa_decode=gqa)
+
+
+def cpu_decode_sample(orc, first, stream, threads):
+    """Oracle decode steps from the GPU's post-prefill state on `threads`
+    host threads, replaying the GPU's greedy stream teacher-forced: seconds
+    per step and the number of disagreeing steps."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle as O
     O.set_threads(threads)
     inp, mism = first, 0
     t0 = time.perf_counter()
     for t in stream:
         mism += orc.step(inp) != t
         inp = t
-    dt = time.perf_counter() - t0
-    steps = len(stream)
-    return (dict(value=steps / dt, unit="tok/s", cores=threads, kind="port",
-                 sample=f"{steps} oracle decode steps of the 24-layer model at {ctx} context from the GPU's "
-                        f"post-prefill state, {threads} OpenMP threads on {cores} host cores"),
-            dict(context=ctx, steps=steps, mismatches=mism,
-                 judged="teacher-forced against the oracle from the GPU's post-prefill state"))
+    return (time.perf_counter() - t0) / max(len(stream), 1), mism
 
 
 def main():
@@ -130,10 +180,13 @@ def main():
     t0 = time.perf_counter()
     blob = E.random_weights(N_LAYERS, VOCAB, seed, threads=min(os.cpu_count() or 8, 16))
     gen_s = time.perf_counter() - t0
-    cap = max(contexts) + args.steps + args.warmup + 16
+    cap = max(contexts) + args.steps + args.warmup + 16 + GEN_STEPS + args.cpu_steps + 1
     eng = E.Engine(blob, N_LAYERS, VOCAB, capacity=cap)
     w = weight_bytes()
-    per_ctx = {}
+    per_ctx, cpu_ctx, agreement = {}, {}, []
+    host_cores = os.cpu_count() or 1
+    threads = min(host_cores, 16)
+    single = None
     r = np.random.default_rng(seed)
     # allocate the prefill buffers and capture the graphs outside the clocks
     eng.generate(r.integers(0, VOCAB, 600).tolist(), 1, reset=True)
@@ -144,19 +197,36 @@ def main():
         t0 = time.perf_counter()
         first = eng.generate(prompt, 1, reset=True)[0]
         ttft_ms = (time.perf_counter() - t0) * 1e3
-        if ctx == max(contexts) and not args.no_cpu:
-            # oracle sample: state handed over after the prompt, then a few
-            # greedy GPU tokens that the oracle replays (timed after the GPU runs)
-            orc = oracle_from_gpu_state(eng, blob, eng.position, args.cpu_steps + 4)
-            cpu_sample = (orc, first, eng.generate([], args.cpu_steps, reset=False), ctx)
+        if not args.no_cpu:
+            # oracle sample: the state handed over after the prompt, then a few
+            # greedy GPU tokens that the oracle replays teacher-forced on the
+            # host cores (the GPU is idle meanwhile); at the headline context
+            # one more step on a single thread
+            head = ctx == max(contexts)
+            n_cpu = args.cpu_steps if head else max(1, args.cpu_steps // 2)
+            orc = oracle_from_gpu_state(eng, blob, eng.position, n_cpu + 4)
+            stream = eng.generate([], n_cpu + (1 if head else 0), reset=False)
+            sec, mism = cpu_decode_sample(orc, first, stream[:n_cpu], threads)
+            cpu_ctx[ctx] = round(1.0 / sec, 3)
+            if head:
+                sec1, mism1 = cpu_decode_sample(orc, stream[n_cpu - 1], stream[n_cpu:], 1)
+                single = dict(tok_s=round(1.0 / sec1, 4), steps=1, context=ctx)
+                mism += mism1
+            agreement.append(dict(context=ctx, steps=len(stream), mismatches=int(mism)))
+            del orc
         ms = eng.time_decode(args.steps, args.warmup)
+        # the serving path: generate() with its host synchronisation every 16 steps
+        t0 = time.perf_counter()
+        eng.generate([], GEN_STEPS, reset=False)
+        gen_ms = (time.perf_counter() - t0) * 1e3
         tps = args.steps / (ms / 1e3)
         b = bytes_per_token(ctx, w)
         per_ctx[ctx] = dict(tok_s=round(tps, 1), ms_per_step=round(ms / args.steps, 4),
                             bytes_per_token=b, achieved_GBs=round(b * tps / 1e9, 1),
                             roofline_frac=round(b * tps / HBM_PEAK, 4),
                             prompt_tokens=start, ttft_ms=round(ttft_ms, 1),
-                            prefill_tok_s=round((start - 1) / (ttft_ms / 1e3), 1))
+                            prefill_tok_s=round((start - 1) / (ttft_ms / 1e3), 1),
+                            generate_256=dict(wall_ms=round(gen_ms, 1), tok_s=round(GEN_STEPS / (gen_ms / 1e3), 1)))
         print(f"# ctx {ctx}: TTFT {ttft_ms:.0f} ms for {start} prompt tokens; {tps:.1f} tok/s, "
               f"{ms / args.steps * 1e3:.1f} us/step, "
               f"{b * tps / 1e9:.0f} GB/s ({b * tps / HBM_PEAK * 100:.1f}% of 8 TB/s)", file=sys.stderr, flush=True)
@@ -177,9 +247,18 @@ def main():
     read_ms = E.time_read(copy_bytes, reps=10)
     read_gbs = copy_bytes / (read_ms / 1e3) / 1e9
 
-    cpu, agreement = None, None
+    cpu = None
     if not args.no_cpu:
-        cpu, agreement = cpu_baseline(*cpu_sample)
+        sys.path.insert(0, os.path.join(ROOT, "oracle"))
+        import oracle as O
+        O.set_threads(threads)
+        iso = cpu_isolated(E.tensor_views(blob, N_LAYERS, VOCAB), contexts)
+        cpu = dict(value=cpu_ctx[head_ctx], unit="tok/s", cores=threads, kind="port",
+                   sample=f"oracle decode steps of the 24-layer model from the GPU's post-prefill state "
+                          f"({args.cpu_steps} at {head_ctx}, {max(1, args.cpu_steps // 2)} at each other "
+                          f"context), {threads} OpenMP threads; isolated pieces median of 3",
+                   threads=threads, host_cores=host_cores, per_context={str(k): v for k, v in cpu_ctx.items()},
+                   single_thread=single, isolated=iso)
 
     main_ctx = per_ctx[head_ctx]
     line = {
@@ -202,7 +281,9 @@ def main():
             "per_context": {str(k): v for k, v in per_ctx.items()},
             "step_roofline_frac_8TBs": main_ctx["roofline_frac"],
             "ttft_ms": {str(k): v["ttft_ms"] for k, v in per_ctx.items()},
-            "token_agreement": agreement,
+            "token_agreement": dict(contexts=agreement,
+                                    judged="greedy GPU tokens replayed teacher-forced by the oracle "
+                                           "from the GPU's post-prefill state") if agreement else None,
             "weight_gen_s": round(gen_s, 1),
             "head_kernel_us": round(head_ms * 1e3, 2),
         },
@@ -215,6 +296,8 @@ def main():
             "unit": "GB/s",
             "frac": round(chain_bytes / (chain_ms / 1e3) / HBM_PEAK, 4),
             "traffic": committed_traffic("k_attn_fused", head_ctx),
+            "traffic_source": f"profiles/k_attn_fused_ctx{head_ctx}_counters.txt: rocprofv3 FETCH_SIZE + "
+                              f"WRITE_SIZE per launch from a committed run, not measured in this one",
             "algorithmic_bytes": chain_bytes,
             "launch_us": round(chain_ms * 1e3, 2),
             "attention_layer_us": {k: round(v * 1e3, 2) for k, v in parts.items()},

@@ -457,17 +457,28 @@ int Engine::upload_state(int pos, int step, uint32_t token, std::string* err) {
   return 0;
 }
 
-int Engine::launch_steps(int kind, int first_pos, int n, std::string* err) {
+// Graph chunks of a run of n steps from first_pos: up to kGraphSteps steps
+// each, every chunk on one attention route (the route changes once, at 1024
+// attended positions), a remainder as one graph of its own length.
+std::vector<std::pair<int, int>> Engine::step_plan(int first_pos, int n) const {
+  std::vector<std::pair<int, int>> plan;  // (splits, steps)
   int done = 0;
   while (done < n) {
     const int pos = first_pos + done;
     const int splits = splits_for(pos + 1);
-    int steps = 1;
-    if (n - done >= kGraphSteps && splits_for(pos + kGraphSteps) == splits) steps = kGraphSteps;
+    int steps = std::min(kGraphSteps, n - done);
+    while (steps > 1 && splits_for(pos + steps) != splits) --steps;
+    plan.emplace_back(splits, steps);
+    done += steps;
+  }
+  return plan;
+}
+
+int Engine::launch_steps(int kind, int first_pos, int n, std::string* err) {
+  for (const auto& [splits, steps] : step_plan(first_pos, n)) {
     hipGraphExec_t ex = graph(kind, splits, steps, err);
     if (!ex) return 2;
     ES_HIP(hipGraphLaunch(ex, stream_), "hipGraphLaunch");
-    done += steps;
   }
   return 0;
 }
@@ -916,10 +927,9 @@ int Engine::time_decode(int steps, int warmup, double* ms_total, std::string* er
     return 1;
   }
   if (int rc = upload_state(position_, 0, pending_, err)) return rc;
-  // capture the graphs before the clock starts (the warmup uses the same ones)
-  if (!graph(kKindDecode, splits_for(position_ + 1), 1, err)) return 2;
-  if (steps >= kGraphSteps && !graph(kKindDecode, splits_for(position_ + 1), kGraphSteps, err))
-    return 2;
+  // capture every graph of the timed run before the clock starts
+  for (const auto& [splits, n] : step_plan(position_ + warmup, steps))
+    if (!graph(kKindDecode, splits, n, err)) return 2;
   if (int rc = launch_steps(kKindDecode, position_, warmup, err)) return rc;
   ES_HIP(hipStreamSynchronize(stream_), "warmup sync");
   hipEvent_t e0, e1;

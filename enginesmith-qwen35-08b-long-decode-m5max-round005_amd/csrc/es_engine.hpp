@@ -11,6 +11,7 @@
 #include <atomic>
 #include <cstdint>
 #include <string>
+#include <utility>
 #include <vector>
 
 #include "es_kernels.hpp"
@@ -110,6 +111,7 @@ class Engine {
   hipGraphExec_t graph(int kind, int splits, int steps, std::string* err);
   // Enqueue `n` steps of one kind from absolute position first_pos: whole
   // kGraphSteps-step graphs, then single-step graphs for the rest.
+  std::vector<std::pair<int, int>> step_plan(int first_pos, int n) const;
   int launch_steps(int kind, int first_pos, int n, std::string* err);
   static constexpr int kGraphSteps = 16;
   int run_steps(int kind, int first_pos, int count, const uint32_t* forced_dev,
