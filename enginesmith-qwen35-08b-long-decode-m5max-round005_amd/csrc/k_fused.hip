@@ -193,15 +193,18 @@ __global__ __launch_bounds__(256) void k_mlp_xcd(MlpXcdArgs a) {
   float xr[32];
   float xs = prep_slice(xn, xr);
   uint16_t* xact = a.xact + x * 512;
+  float gv[2], uv[2];
 #pragma unroll
   for (int p = 0; p < 2; ++p) {
-    const float g = tree32(q4_slice_sb(cg[p], gsb[p], xr, xs));
-    const float u = tree32(q4_slice_sb(cu[p], usb[p], xr, xs));
-    if (sl == 0 && er[p] >= 0) {
-      const float gb = rbf(g), ub = rbf(u);
-      const float silu = rbf(gb * sigmoid_bf(gb));
-      xact[rank * nact + wave * 4 + 2 * p + half] = (uint16_t)f2bf(silu * ub);
-    }
+    gv[p] = tree32(q4_slice_sb(cg[p], gsb[p], xr, xs));
+    uv[p] = tree32(q4_slice_sb(cu[p], usb[p], xr, xs));
+  }
+  // lane p < 2 of each half-wave forms element p's SwiGLU (every lane holds
+  // both sums)
+  if (sl < 2 && (sl == 0 ? er[0] : er[1]) >= 0) {
+    const float gb = rbf(sl == 0 ? gv[0] : gv[1]), ub = rbf(sl == 0 ? uv[0] : uv[1]);
+    const float silu = rbf(gb * sigmoid_bf(gb));
+    xact[rank * nact + wave * 4 + 2 * sl + half] = (uint16_t)f2bf(silu * ub);
   }
 
   // ---- exchange the XCD's activation elements
@@ -233,22 +236,6 @@ __device__ __forceinline__ uint2 l2_load_2xu16(const uint16_t* p0, const uint16_
       : "v"(p0), "v"(p1)
       : "memory");
   return make_uint2(a, b);
-}
-
-// Value of lane K of each row of 16 lanes, in every lane of the row (DPP
-// row_newbcast).
-template <int K>
-__device__ __forceinline__ uint32_t row_bcast(uint32_t v) {
-  return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x150 + K, 0xf, 0xf, false);
-}
-// Taps (slots 0..3) and conv weights of pass P from the lanes that loaded them.
-template <int P>
-__device__ __forceinline__ void row_gather(uint32_t tapv, uint2 cwv, uint32_t (&tap)[3][4], uint2 (&cw)[3]) {
-  tap[P][0] = row_bcast<4 * P>(tapv);
-  tap[P][1] = row_bcast<4 * P + 1>(tapv);
-  tap[P][2] = row_bcast<4 * P + 2>(tapv);
-  tap[P][3] = row_bcast<4 * P + 3>(tapv);
-  cw[P] = make_uint2(row_bcast<12 + P>(cwv.x), row_bcast<12 + P>(cwv.y));
 }
 
 // ---- k_gdn_xcd: a Gated DeltaNet layer up to its out_proj head partials ----
@@ -328,8 +315,8 @@ __global__ __launch_bounds__(256) void k_gdn_xcd(GdnXcdArgs a) {
     c[4] = *reinterpret_cast<const u32x4*>((is_a ? a.a.w : a.b.w) + (size_t)row * 128 + sl * 4);
     sbw[4] = a.ab_sb[(size_t)((is_a ? 0 : kGdnHeads) + row) * 16 + sl / 2];
   }
-  // conv taps of the half-wave's q, k, v channels (ring slots of pos-3..pos)
-  // and their conv weights, one load each across the half-wave: lane l < 12
+  // conv taps of the half-wave's q, k, v channels (ring slots 0..3) and
+  // their conv weights, one load each across the half-wave: lane l < 12
   // holds slot l & 3 of pass l >> 2, lane 12 + p the weights of pass p
   const int tl = sl < 12 ? sl : 0, cl = sl >= 12 && sl < 15 ? sl - 12 : 0;
   const uint32_t tapv = a.ring[(size_t)(tl & 3) * kConv + (tl >> 2) * 2048 + h * 128 + 8 * j + hw];
@@ -383,30 +370,27 @@ __global__ __launch_bounds__(256) void k_gdn_xcd(GdnXcdArgs a) {
   float xr[32];
   const float xs = prep_slice(xn, xr);
   const int slot_new = pos & 3;
-  // lane 0 of each half-wave takes the taps and weights of its row of 16
-  // lanes (lanes 0-15 and 32-47) by DPP row broadcast
-  uint32_t tap[3][4];
-  uint2 cw[3];
-  row_gather<0>(tapv, cwv, tap, cw);
-  row_gather<1>(tapv, cwv, tap, cw);
-  row_gather<2>(tapv, cwv, tap, cw);
-#pragma unroll
-  for (int p = 0; p < 4; ++p) {
-    const uint32_t raw = f2bf(tree32(q4_slice_sb(c[p], sbw[p], xr, xs)));
-    if (sl == 0) {
-      if (p < 3) {
-        const int ch = p * 2048 + h * 128 + 8 * j + hw;
-        a.ring[(size_t)slot_new * kConv + ch] = (uint16_t)raw;
-        // taps pos-3 .. pos: ring slots (pos+1+t) & 3 for t < 3, then the new row
-        uint32_t xt[4];
-#pragma unroll
-        for (int tt = 0; tt < 3; ++tt) {
-          const int sidx = (pos + 1 + tt) & 3;
-          xt[tt] = sidx == 0 ? tap[p][0] : sidx == 1 ? tap[p][1] : sidx == 2 ? tap[p][2] : tap[p][3];
-        }
-        xt[3] = raw;
-        const float act = conv4_silu(xt, cw[p]);
-        xb[(p == 0 ? kXq : p == 1 ? kXk : kXv) + 8 * j + hw] = (uint16_t)f2bf(act);
+  // every lane of a half-wave holds the four projected values (tree32). Lane
+  // p < 3 of the half-wave writes pass p's ring row and convolves it over
+  // the taps of pos-3 .. pos-1 (ring slots (pos+1+t) & 3, fetched from the
+  // lanes that loaded them) and the new row; lane 3 stores z
+  const uint32_t raw_q = f2bf(tree32(q4_slice_sb(c[0], sbw[0], xr, xs)));
+  const uint32_t raw_k = f2bf(tree32(q4_slice_sb(c[1], sbw[1], xr, xs)));
+  const uint32_t raw_v = f2bf(tree32(q4_slice_sb(c[2], sbw[2], xr, xs)));
+  const uint32_t raw_z = f2bf(tree32(q4_slice_sb(c[3], sbw[3], xr, xs)));
+  {
+    const int src = (lane & 32) + 4 * (sl < 3 ? sl : 0);
+    const uint32_t x0 = (uint32_t)__shfl((int)tapv, src + ((pos + 1) & 3));
+    const uint32_t x1 = (uint32_t)__shfl((int)tapv, src + ((pos + 2) & 3));
+    const uint32_t x2 = (uint32_t)__shfl((int)tapv, src + ((pos + 3) & 3));
+    const int wsrc = (lane & 32) + 12 + (sl < 3 ? sl : 0);
+    const uint2 w = make_uint2((uint32_t)__shfl((int)cwv.x, wsrc), (uint32_t)__shfl((int)cwv.y, wsrc));
+    if (sl < 4) {
+      const uint32_t raw = sl == 0 ? raw_q : sl == 1 ? raw_k : sl == 2 ? raw_v : raw_z;
+      if (sl < 3) {
+        a.ring[(size_t)slot_new * kConv + sl * 2048 + h * 128 + 8 * j + hw] = (uint16_t)raw;
+        const uint32_t xt[4] = {x0, x1, x2, raw};
+        xb[sl * 128 + 8 * j + hw] = (uint16_t)f2bf(conv4_silu(xt, w));  // q, k, v of the exchange
       } else {
         xb[kXz + 8 * j + hw] = (uint16_t)raw;
       }
@@ -425,11 +409,14 @@ __global__ __launch_bounds__(256) void k_gdn_xcd(GdnXcdArgs a) {
     const float ss = tree64(v * v);
     if (lane == 0) red[wave] = ss;
     if (t < 8) vv[t] = bf2f(qkr.y);
-    if (t == 8) {
+    if (t == 8 || t == 9) {  // lane 8: the decay g, lane 9: beta
       const uint2 ab = l2_load_2xu16(xb + kXab, xb + kXab + 1);
-      const float ax = rbf(bf2f(ab.x) + bf2f(a.dt_bias[h]));
-      gates[0] = es_exp(-es_exp(a.a_log[h]) * softplus_bf(ax));
-      gates[1] = sigmoid_bf(bf2f(ab.y));
+      if (t == 8) {
+        const float ax = rbf(bf2f(ab.x) + bf2f(a.dt_bias[h]));
+        gates[0] = es_exp(-es_exp(a.a_log[h]) * softplus_bf(ax));
+      } else {
+        gates[1] = sigmoid_bf(bf2f(ab.y));
+      }
     }
     __syncthreads();
     const float tot = t < 128 ? red[0] + red[1] : red[2] + red[3];
