@@ -167,6 +167,11 @@ __device__ __forceinline__ float tree4(float v) {
   v = v + dpp_xor2(v);
   return v;
 }
+// Sum of each group of 8 lanes, (quad 0) + (quad 1), in all its lanes.
+__device__ __forceinline__ float tree8(float v) {
+  v = tree4(v);
+  return v + dpp_half_mirror(v);
+}
 __device__ __forceinline__ float tree16(float v) {
   v = tree4(v);
   v = v + dpp_half_mirror(v);

@@ -202,20 +202,20 @@ int Engine::init(const void* blob, uint64_t bytes, std::string* err) {
   if (fused_mlp_) {
     // the XCD kernels read each Q4 group's scale and bias as one word
     for (auto& L : layers_) {
-      const size_t ffn_groups = (size_t)3584 * 16, down_groups = (size_t)1024 * 56;
+      const size_t ffn_groups = (size_t)3584 * 16;
       L.gu_sb = static_cast<uint2*>(alloc(ffn_groups * sizeof(uint2)));
-      L.down_sb = static_cast<uint32_t*>(alloc(down_groups * 4));
+      L.down_sb = static_cast<uint32_t*>(alloc((size_t)8 * 1024 * 8 * 4));
       if (!L.gu_sb || !L.down_sb) {
         if (err) *err = "device allocation of packed group words failed";
         return 2;
       }
       ES_HIP(launch_pack_sb2(L.gate.s, L.gate.b, L.up.s, L.up.b, L.gu_sb, ffn_groups, stream_), "pack");
-      ES_HIP(launch_pack_sb(L.down.s, L.down.b, L.down_sb, down_groups, stream_), "pack");
+      ES_HIP(launch_pack_down_octets(L.down.s, L.down.b, L.down_sb, stream_), "pack");
       if (L.attention) continue;
       L.qkv_sb = static_cast<uint32_t*>(alloc((size_t)kConv * 16 * 4));
       L.z_sb = static_cast<uint32_t*>(alloc((size_t)2048 * 16 * 4));
       L.ab_sb = static_cast<uint32_t*>(alloc((size_t)2 * kGdnHeads * 16 * 4));
-      L.out_sb = static_cast<uint32_t*>(alloc((size_t)1024 * 32 * 4));
+      L.out_sb = static_cast<uint32_t*>(alloc((size_t)8 * 1024 * 4 * 4));
       if (!L.qkv_sb || !L.z_sb || !L.ab_sb || !L.out_sb) {
         if (err) *err = "device allocation of packed group words failed";
         return 2;
@@ -224,7 +224,7 @@ int Engine::init(const void* blob, uint64_t bytes, std::string* err) {
       ES_HIP(launch_pack_sb(L.z.s, L.z.b, L.z_sb, (size_t)2048 * 16, stream_), "pack");
       ES_HIP(launch_pack_sb(L.a.s, L.a.b, L.ab_sb, (size_t)kGdnHeads * 16, stream_), "pack");
       ES_HIP(launch_pack_sb(L.b.s, L.b.b, L.ab_sb + kGdnHeads * 16, (size_t)kGdnHeads * 16, stream_), "pack");
-      ES_HIP(launch_pack_sb(L.out.s, L.out.b, L.out_sb, (size_t)1024 * 32, stream_), "pack");
+      ES_HIP(launch_pack_out_pairs(L.out.s, L.out.b, L.out_sb, stream_), "pack");
     }
   }
   ES_HIP(hipMemsetAsync(err_, 0, 256 * sizeof(uint32_t), stream_), "memset");
@@ -358,7 +358,7 @@ hipError_t Engine::enqueue_layers(hipStream_t s, int splits) {
       g.err = err_;
       g.st = st_;
       if ((e = launch_gdn_xcd(g, s)) != hipSuccess) return e;
-      if ((e = mlp(kGdnHeads)) != hipSuccess) return e;
+      if ((e = mlp(8)) != hipSuccess) return e;  // the eight head-pair partials
     } else if (!L.attention) {
       nm.count = 4;
       nm.m[0] = L.qkv; nm.y[0] = L.ring;

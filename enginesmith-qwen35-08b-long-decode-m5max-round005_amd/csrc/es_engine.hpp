@@ -24,8 +24,8 @@ struct LayerDev {
   const uint16_t* input_norm;
   const uint16_t* post_norm;
   Q4 gate, up, down;
-  // packed scale|bias<<16 group words of the XCD kernels (launch_pack_sb):
-  // (gate, up) interleaved, down; GDN qkv, z, a then b, out
+  // packed scale|bias<<16 group words of the XCD kernels: (gate, up)
+  // interleaved, down by XCD octet; GDN qkv, z, a then b, out by head pair
   uint2* gu_sb;
   uint32_t* down_sb;
   uint32_t* qkv_sb;

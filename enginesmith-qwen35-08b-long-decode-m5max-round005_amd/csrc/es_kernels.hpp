@@ -138,7 +138,8 @@ hipError_t launch_attn_merge_out(const AttnArgs& a, const Q4& o, float* part, hi
 // ---- XCD-cooperative decode kernels, k_fused.hip ----
 // The MLP of a layer in one 256-block launch (blocks of one XCD exchange
 // activations through its L2): h_mid = bf16(h_old + bf16(pairwise sum of the
-// nparts mixer partials)) (16: GDN out_proj heads, 8: o_proj heads), post
+// 8 mixer partials)) (k_gdn_xcd's head pairs, or k_attn_merge_out's o_proj
+// heads; nparts must be 8), post
 // RMSNorm, gate/up, SwiGLU, then dpart[x][r] = octet x's share of the down
 // row r's sum (x = 0..7). The consumer adds them: h = bf16(h_mid +
 // bf16(pairwise sum over x of dpart[x][r])), the down projection's residual
@@ -146,7 +147,7 @@ hipError_t launch_attn_merge_out(const AttnArgs& a, const Q4& o, float* part, hi
 struct MlpXcdArgs {
   Q4 gate, up, down;
   const uint2* gu_sb;       // [3584, 16] (gate, up) scale|bias<<16 words (launch_pack_sb2)
-  const uint32_t* down_sb;  // [1024, 56] scale|bias<<16 words (launch_pack_sb)
+  const uint32_t* down_sb;  // [8 octets, 1024, 8] scale|bias<<16 words (launch_pack_down_octets)
   const uint16_t* h_old;    // [1024] residual stream before the mixer
   const float* part;        // [nparts, 1024] mixer partials
   uint16_t* h_mid;          // [1024] written: stream after the mixer
@@ -169,7 +170,8 @@ struct GdnXcdArgs {
   const uint16_t* gain;     // input norm [1024]
   Q4 qkv, z, a, b, out;
   // scale|bias<<16 words of the same matrices (launch_pack_sb): qkv [6144,16],
-  // z [2048,16], a then b [2,16,16], out [1024,32]
+  // z [2048,16], a then b [2,16,16]; out per XCD [8, 1024, 4] (the groups of
+  // the XCD's head pair, launch_pack_out_pairs)
   const uint32_t* qkv_sb;
   const uint32_t* z_sb;
   const uint32_t* ab_sb;
@@ -180,7 +182,7 @@ struct GdnXcdArgs {
   const float* a_log;       // [16]
   uint16_t* ring;           // [4, 6144]
   float* state;             // [16, 128, 128]
-  float* part;              // [16, 1024] out_proj head partials
+  float* part;              // [8, 1024] out_proj partials of the head pairs (2x, 2x+1)
   uint16_t* xbuf;           // [8 XCDs][2 heads][648] exchange
   uint32_t* flags;          // [8, 32] barrier flags (shared with k_mlp_xcd)
   uint32_t* err;            // error word
@@ -193,6 +195,13 @@ hipError_t launch_gdn_xcd(const GdnXcdArgs& a, hipStream_t s);
 hipError_t launch_pack_sb(const uint16_t* s, const uint16_t* b, uint32_t* out, size_t n, hipStream_t st);
 hipError_t launch_pack_sb2(const uint16_t* s0, const uint16_t* b0, const uint16_t* s1, const uint16_t* b1,
                            uint2* out, size_t n, hipStream_t st);
+// The down projection's words by XCD octet: out[x][r][w] = the word of group
+// 4x + w (w < 4) and, for x < 6, of group 32 + 4x + w - 4 (w >= 4) of row r
+// (K = 3584: 56 groups per row), so each XCD reads one contiguous block.
+hipError_t launch_pack_down_octets(const uint16_t* s, const uint16_t* b, uint32_t* out, hipStream_t st);
+// out_proj's words by head pair: out[x][r][w] = the word of group 4x + w of
+// row r (K = 2048: 32 groups per row; heads 2x, 2x+1 span groups 4x .. 4x+3).
+hipError_t launch_pack_out_pairs(const uint16_t* s, const uint16_t* b, uint32_t* out, hipStream_t st);
 // out[b] = XCC_ID of block b of a 256-block launch.
 hipError_t launch_xcc_probe(uint32_t* out, hipStream_t s);
 

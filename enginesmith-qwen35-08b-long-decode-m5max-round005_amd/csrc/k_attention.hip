@@ -35,11 +35,6 @@ namespace {
 
 constexpr float kFiniteMin = -3.40282346638528859812e38f;
 
-__device__ __forceinline__ float tree8(float v) {
-  v = tree4(v);
-  return v + dpp_half_mirror(v);
-}
-
 // fma chain over the 8 bf16 dims of one 16-byte K chunk.
 __device__ __forceinline__ float chunk_dot(const float* q, const u32x4& k) {
   float s = 0.0f;

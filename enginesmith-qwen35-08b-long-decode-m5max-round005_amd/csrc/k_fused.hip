@@ -144,6 +144,7 @@ __global__ __launch_bounds__(256) void k_mlp_xcd(MlpXcdArgs a) {
   const int wide = x < 6;
   const int L = wide ? (t & 15) : (t & 7);
   const int dslice = wide ? (L < 8 ? 8 * x + L : 8 * x + 64 + (L - 8)) : 8 * x + L;
+  const int dword = L < 8 ? L / 2 : 4 + (L - 8) / 2;  // its group's word in the octet's row
   u32x4 dc[2];
   uint32_t dsb[2];
   int drow[2];
@@ -152,7 +153,7 @@ __global__ __launch_bounds__(256) void k_mlp_xcd(MlpXcdArgs a) {
     const int row = wide ? rank * 32 + p * 16 + (t >> 4) : rank * 32 + (t >> 3);
     drow[p] = row;
     dc[p] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(a.down.w + (size_t)row * 448 + dslice * 4));
-    dsb[p] = __builtin_nontemporal_load(a.down_sb + (size_t)row * 56 + dslice / 2);
+    dsb[p] = __builtin_nontemporal_load(a.down_sb + ((size_t)x * 1024 + row) * 8 + dword);
   }
   issue_fence();
 
@@ -238,19 +239,23 @@ __device__ __forceinline__ uint2 l2_load_2xu16(const uint16_t* p0, const uint16_
   return make_uint2(a, b);
 }
 
-// ---- k_gdn_xcd: a Gated DeltaNet layer up to its out_proj head partials ----
+// ---- k_gdn_xcd: a Gated DeltaNet layer up to its out_proj partials ----
 // It replaces the input-norm + projection launch and the recurrence launch.
-// XCD x holds heads x and x + 8, 16 blocks each (rank r: head x + 8 (r >> 4),
-// block j = r & 15 of the head). Phase 1: the layer input (embedding row, or
-// the stream after the previous layer's mixer plus its MLP's down partials),
-// RMSNorm, and the block's rows of the head: channels 8j .. 8j+7 of q, k, v
-// and z (block 0 of the head also a and b), one half-wave per row as
-// k_norm_multi; the q/k/v rows go to the ring and through the convolution with
-// the ring's three older taps and SiLU. Exchange. Phase 2: q and k L2-norms,
-// gates, and the delta rule for value rows 8j .. 8j+7 (16 lanes per row,
-// k_gdn_recur_out's order). Exchange. Phase 3: the head's gated RMSNorm and
-// out_proj rows 64j .. 64j+63 over the head's 128 columns: the head partials
-// k_gdn_recur_out writes, bit for bit.
+// XCD x holds the head pair 2x, 2x + 1, 16 blocks each (rank r: head
+// 2x + (r >> 4), block j = r & 15 of the head). Phase 1: the layer input
+// (embedding row, or the stream after the previous layer's mixer plus its
+// MLP's down partials), RMSNorm, and the block's rows of the head: channels
+// 8j .. 8j+7 of q, k, v and z (block 0 of the head also a and b), one
+// half-wave per row as k_norm_multi; the q/k/v rows go to the ring and
+// through the convolution with the ring's three older taps and SiLU.
+// Exchange. Phase 2: q and k L2-norms, gates, and the delta rule for value
+// rows 8j .. 8j+7 (16 lanes per row, k_gdn_recur_out's order). Exchange.
+// Phase 3: both heads' gated RMSNorm and out_proj rows 32r .. 32r+31 over the
+// pair's 256 columns: per row tree8 of its eight 32-column slice partials,
+// which is the head partial of 2x (tree4 of its four slices) plus that of
+// 2x + 1 -- the first level of the pairwise sum over the 16 head partials
+// that k_gdn_recur_out writes, so the next launch's pairwise sum of the eight
+// pair partials is bit for bit the same.
 constexpr int kHx = 648;  // exchange elements per head: q k v z y (128 each), a, b, pad
 constexpr int kXq = 0, kXk = 128, kXv = 256, kXz = 384, kXy = 512, kXab = 640;
 
@@ -262,13 +267,13 @@ __global__ __launch_bounds__(256) void k_gdn_xcd(GdnXcdArgs a) {
   __shared__ float vv[8];
   __shared__ float red[4];
   __shared__ float gates[2];
-  __shared__ float yv[128];
-  __shared__ float xg[128 + 4];
-  __shared__ float ginv;
+  __shared__ float yv[256];       // phase 3: y of the head pair
+  __shared__ float xg[256 + 8];   // z, then the gated value; slice s at xg[33 s ..]
+  __shared__ float ginv[2];
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6, half = lane >> 5, sl = lane & 31;
   const int hw = wave * 2 + half;  // half-wave 0..7
   const int x = (int)xcc_id() & 7, rank = blockIdx.x >> 3;
-  const int h = x + 8 * (rank >> 4), j = rank & 15;
+  const int h = 2 * x + (rank >> 4), j = rank & 15;
   uint32_t* flags = a.flags + x * kGroupBlocks;
   uint16_t* xb = a.xbuf + (size_t)(x * 2 + (rank >> 4)) * kHx;
   // every pointer argument in scalar registers at once: one wait for the
@@ -331,10 +336,12 @@ __global__ __launch_bounds__(256) void k_gdn_xcd(GdnXcdArgs a) {
     S[0] = lo.x; S[1] = lo.y; S[2] = lo.z; S[3] = lo.w;
     S[4] = hi.x; S[5] = hi.y; S[6] = hi.z; S[7] = hi.w;
   }
-  // out_proj: row 64j + t/4, K slice 4h + t%4
-  const int orow = 64 * j + (t >> 2), osl = 4 * h + (t & 3);
-  const u32x4 oc = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(a.out.w + (size_t)orow * 256 + osl * 4));
-  const uint32_t osb = __builtin_nontemporal_load(a.out_sb + (size_t)orow * 32 + osl / 2);
+  // out_proj: row 32 rank + t/8, K slice 8x + t%8 (the pair's eight slices,
+  // 128 contiguous bytes of the row)
+  const int orow = 32 * rank + (t >> 3), os8 = t & 7;
+  const u32x4 oc = __builtin_nontemporal_load(
+      reinterpret_cast<const u32x4*>(a.out.w + (size_t)orow * 256 + (8 * x + os8) * 4));
+  const uint32_t osb = __builtin_nontemporal_load(a.out_sb + ((size_t)x * 1024 + orow) * 4 + os8 / 2);
   issue_fence();
 
   // ---- phase 1: input, RMSNorm, projection rows, ring, convolution
@@ -455,23 +462,26 @@ __global__ __launch_bounds__(256) void k_gdn_xcd(GdnXcdArgs a) {
   }
   xcd_barrier(flags, rank, own + 2u, a.err);
 
-  // ---- phase 3: gated RMSNorm of the head, out_proj rows 64j .. 64j+63
-  if (t < 128) {
-    const uint2 yz = l2_load_2xu16(xb + kXy + t, xb + kXz + t);
+  // ---- phase 3: gated RMSNorm of both heads of the pair (threads 128 hl ..
+  // 128 hl + 127: head 2x + hl), out_proj rows 32 rank .. +31
+  const int hl = t >> 7, dl = t & 127;
+  {
+    const uint16_t* xh = a.xbuf + (size_t)(x * 2 + hl) * kHx;
+    const uint2 yz = l2_load_2xu16(xh + kXy + dl, xh + kXz + dl);
     yv[t] = bf2f(yz.x);
     xg[t + (t >> 5)] = bf2f(yz.y);  // z, replaced by the gated value below
   }
   __syncthreads();
-  if (t < 16) {
+  if (dl < 16) {  // lanes 0-15 of waves 0 and 2
     float ss = 0.0f;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) ss = fmaf(yv[t * 8 + i], yv[t * 8 + i], ss);
+    for (int i = 0; i < 8; ++i) ss = fmaf(yv[128 * hl + dl * 8 + i], yv[128 * hl + dl * 8 + i], ss);
     ss = tree16(ss);
-    if (t == 0) ginv = 1.0f / sqrtf(ss / 128.0f + 1e-6f);
+    if (dl == 0) ginv[hl] = 1.0f / sqrtf(ss / 128.0f + 1e-6f);
   }
   __syncthreads();
-  if (t < 128) {
-    const float norm = rbf(rbf(yv[t] * ginv) * bf2f(a.norm_w[t]));
+  {
+    const float norm = rbf(rbf(yv[t] * ginv[hl]) * bf2f(a.norm_w[dl]));
     const float gz = xg[t + (t >> 5)];
     const float sy = 1.0f / (1.0f + es_exp(fabsf(gz)));
     const float sig = gz < 0.0f ? sy : 1.0f - sy;
@@ -480,12 +490,11 @@ __global__ __launch_bounds__(256) void k_gdn_xcd(GdnXcdArgs a) {
   __syncthreads();
   {
     float ov[32], oxr[32];
-    const int s4 = t & 3;
 #pragma unroll
-    for (int q = 0; q < 32; ++q) ov[q] = xg[s4 * 33 + q];
+    for (int q = 0; q < 32; ++q) ov[q] = xg[os8 * 33 + q];
     const float oxs = prep_slice(ov, oxr);
-    const float part = tree4(q4_slice_sb(oc, osb, oxr, oxs));
-    if (s4 == 0) a.part[(size_t)h * 1024 + orow] = part;
+    const float part = tree8(q4_slice_sb(oc, osb, oxr, oxs));
+    if (os8 == 0) a.part[(size_t)x * 1024 + orow] = part;
   }
 }
 
@@ -500,6 +509,24 @@ __global__ __launch_bounds__(256) void k_pack_sb2(const uint16_t* s0, const uint
   if (i < n) out[i] = make_uint2((uint32_t)s0[i] | (uint32_t)b0[i] << 16, (uint32_t)s1[i] | (uint32_t)b1[i] << 16);
 }
 
+// out[x][r][w] for w < 8: groups 4x + w (w < 4), 32 + 4x + w - 4 (w >= 4, x < 6).
+__global__ __launch_bounds__(256) void k_pack_down_octets(const uint16_t* s, const uint16_t* b, uint32_t* out) {
+  const int i = blockIdx.x * 256 + threadIdx.x;  // < 8 * 1024 * 8
+  const int x = i >> 13, r = (i >> 3) & 1023, w = i & 7;
+  const int g = w < 4 ? 4 * x + w : 32 + 4 * x + (w - 4);
+  const bool used = w < 4 || x < 6;
+  const size_t src = (size_t)r * 56 + (used ? g : 0);
+  out[i] = used ? ((uint32_t)s[src] | (uint32_t)b[src] << 16) : 0u;
+}
+
+// out[x][r][w] = group 4x + w of row r (32 groups per row).
+__global__ __launch_bounds__(256) void k_pack_out_pairs(const uint16_t* s, const uint16_t* b, uint32_t* out) {
+  const int i = blockIdx.x * 256 + threadIdx.x;  // < 8 * 1024 * 4
+  const int x = i >> 12, r = (i >> 2) & 1023, w = i & 3;
+  const size_t src = (size_t)r * 32 + 4 * x + w;
+  out[i] = (uint32_t)s[src] | (uint32_t)b[src] << 16;
+}
+
 __global__ __launch_bounds__(256) void k_xcc_probe(uint32_t* out) {
   if (threadIdx.x == 0) out[blockIdx.x] = xcc_id();
 }
@@ -511,12 +538,8 @@ hipError_t launch_mlp_xcd(const MlpXcdArgs& a, int nparts, hipStream_t s) {
       a.up.n != kFfn || a.down.n != kHidden || a.down.k != kFfn || !a.h_old || !a.part || !a.h_mid ||
       a.h_mid == a.h_old || !a.gain || !a.dpart || !a.xact || !a.flags || !a.err || !a.gu_sb || !a.down_sb)
     return hipErrorInvalidValue;
-  if (nparts == 16)
-    hipLaunchKernelGGL(k_mlp_xcd<16>, dim3(256), dim3(256), 0, s, a);
-  else if (nparts == 8)
-    hipLaunchKernelGGL(k_mlp_xcd<8>, dim3(256), dim3(256), 0, s, a);
-  else
-    return hipErrorInvalidValue;
+  if (nparts != 8) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(k_mlp_xcd<8>, dim3(256), dim3(256), 0, s, a);
   return hipGetLastError();
 }
 
@@ -546,6 +569,18 @@ hipError_t launch_pack_sb2(const uint16_t* s0, const uint16_t* b0, const uint16_
                            uint2* out, size_t n, hipStream_t st) {
   if (!s0 || !b0 || !s1 || !b1 || !out || n == 0 || n > ((size_t)1 << 32)) return hipErrorInvalidValue;
   hipLaunchKernelGGL(k_pack_sb2, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, s0, b0, s1, b1, out, n);
+  return hipGetLastError();
+}
+
+hipError_t launch_pack_down_octets(const uint16_t* s, const uint16_t* b, uint32_t* out, hipStream_t st) {
+  if (!s || !b || !out) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(k_pack_down_octets, dim3(8 * 1024 * 8 / 256), dim3(256), 0, st, s, b, out);
+  return hipGetLastError();
+}
+
+hipError_t launch_pack_out_pairs(const uint16_t* s, const uint16_t* b, uint32_t* out, hipStream_t st) {
+  if (!s || !b || !out) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(k_pack_out_pairs, dim3(8 * 1024 * 4 / 256), dim3(256), 0, st, s, b, out);
   return hipGetLastError();
 }
 
