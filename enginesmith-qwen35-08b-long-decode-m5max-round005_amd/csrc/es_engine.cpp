@@ -199,6 +199,15 @@ int Engine::init(const void* blob, uint64_t bytes, std::string* err) {
   ES_HIP(hipStreamSynchronize(stream_), "init sync");
   fused_mlp_ = xcc[0] < 8;
   for (int b = 0; b < 256; ++b) fused_mlp_ = fused_mlp_ && xcc[b] == (xcc[0] + (uint32_t)b) % 8;
+  for (auto& L : layers_) {
+    if (!L.attention) continue;
+    L.o_sb = static_cast<uint32_t*>(alloc((size_t)8 * 1024 * 4 * 4));
+    if (!L.o_sb) {
+      if (err) *err = "device allocation of packed group words failed";
+      return 2;
+    }
+    ES_HIP(launch_pack_out_pairs(L.o.s, L.o.b, L.o_sb, stream_), "pack");
+  }
   if (fused_mlp_) {
     // the XCD kernels read each Q4 group's scale and bias as one word
     for (auto& L : layers_) {
@@ -391,7 +400,7 @@ hipError_t Engine::enqueue_layers(hipStream_t s, int splits) {
       if ((e = launch_norm_multi(nm, s)) != hipSuccess) return e;
       const AttnArgs a = attn_args(L, splits);
       if ((e = launch_attn_fused(a, s)) != hipSuccess) return e;
-      if ((e = launch_attn_merge_out(a, L.o, proj_part_, s)) != hipSuccess) return e;
+      if ((e = launch_attn_merge_out(a, L.o, L.o_sb, proj_part_, s)) != hipSuccess) return e;
       if ((e = mlp(kQHeads)) != hipSuccess) return e;
     }
   }

@@ -32,6 +32,7 @@ struct LayerDev {
   uint32_t* z_sb;
   uint32_t* ab_sb;
   uint32_t* out_sb;
+  uint32_t* o_sb;  // attention o_proj by head (launch_pack_out_pairs), every engine mode
   // GDN
   Q4 qkv, z, a, b, out;
   const uint16_t* conv_w;

@@ -132,8 +132,10 @@ hipError_t launch_attn_fused(const AttnArgs& a, hipStream_t s);
 hipError_t launch_attn_merge(const AttnArgs& a, hipStream_t s);
 // Engine path: merge + gate, then o_proj partials per head (part[h][r] = the
 // head's 256 columns of row r, its eight slice partials combined pairwise);
-// the next launch adds the 8 partials pairwise.
-hipError_t launch_attn_merge_out(const AttnArgs& a, const Q4& o, float* part, hipStream_t s);
+// the next launch adds the 8 partials pairwise. o_sb: o_proj's group words by
+// head ([8, 1024, 4], launch_pack_out_pairs: head h spans groups 4h .. 4h+3).
+hipError_t launch_attn_merge_out(const AttnArgs& a, const Q4& o, const uint32_t* o_sb, float* part,
+                                 hipStream_t s);
 
 // ---- XCD-cooperative decode kernels, k_fused.hip ----
 // The MLP of a layer in one 256-block launch (blocks of one XCD exchange

@@ -540,7 +540,7 @@ __global__ __launch_bounds__(64) void k_attn_merge(AttnArgs a) {
 // tree8. The 64-slice tree of a K=2048 row pairs adjacent slices first, so the
 // row's full sum is the pairwise tree8 of the 8 head partials, formed by the
 // next launch, bit for bit.
-__global__ __launch_bounds__(256) void k_attn_merge_out(AttnArgs a, Q4 o, float* part) {
+__global__ __launch_bounds__(256) void k_attn_merge_out(AttnArgs a, Q4 o, const uint32_t* o_sb, float* part) {
   __shared__ float fac[kAttnMaxChains];
   __shared__ float total;
   __shared__ float gx[256 + 8];  // gated output, slice s at gx[33 s ..]
@@ -558,13 +558,13 @@ __global__ __launch_bounds__(256) void k_attn_merge_out(AttnArgs a, Q4 o, float*
   const uint32_t gate_raw = a.q_proj[h * 512 + 256 + t];
   issue_fence();
   u32x4 oc[4];
-  uint32_t osv[4], obv[4];
+  uint32_t osb[4];
 #pragma unroll
   for (int p = 0; p < 4; ++p) {
     const size_t row = (size_t)rg * 128 + 32 * p + (t >> 3);
     oc[p] = *reinterpret_cast<const u32x4*>(o.w + row * 256 + gs * 4);
-    osv[p] = o.s[row * 32 + gs / 2];
-    obv[p] = o.b[row * 32 + gs / 2];
+    // the head's four group words of the row, contiguous (launch_pack_out_pairs)
+    osb[p] = o_sb[((size_t)h * 1024 + row) * 4 + sl / 2];
   }
   issue_fence();
   if (wave == 0) merge_factors(mlv, lane, two_pass, fac, &total);
@@ -578,7 +578,7 @@ __global__ __launch_bounds__(256) void k_attn_merge_out(AttnArgs a, Q4 o, float*
 #pragma unroll
   for (int p = 0; p < 4; ++p) {
     const int row = rg * 128 + 32 * p + (t >> 3);
-    const float pp = tree8(q4_slice(oc[p], osv[p], obv[p], xr, xs));
+    const float pp = tree8(q4_slice_sb(oc[p], osb[p], xr, xs));
     if (sl == 0) part[(size_t)h * 1024 + row] = pp;
   }
 }
@@ -608,10 +608,10 @@ hipError_t launch_attn_fused(const AttnArgs& a, hipStream_t s) {
   return hipGetLastError();
 }
 
-hipError_t launch_attn_merge_out(const AttnArgs& a, const Q4& o, float* part, hipStream_t s) {
-  if (!attn_ok(a) || !o.w || !o.s || !o.b || o.n != kHidden || o.k != 2048 || !part)
-    return hipErrorInvalidValue;
-  hipLaunchKernelGGL(k_attn_merge_out, dim3(kQHeads, 8), dim3(256), 0, s, a, o, part);
+hipError_t launch_attn_merge_out(const AttnArgs& a, const Q4& o, const uint32_t* o_sb, float* part,
+                                 hipStream_t s) {
+  if (!attn_ok(a) || !o.w || !o_sb || o.n != kHidden || o.k != 2048 || !part) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(k_attn_merge_out, dim3(kQHeads, 8), dim3(256), 0, s, a, o, o_sb, part);
   return hipGetLastError();
 }
 
