@@ -326,6 +326,14 @@ __global__ __launch_bounds__(256) void k_gdn_xcd(GdnXcdArgs a) {
   const int tl = sl < 12 ? sl : 0, cl = sl >= 12 && sl < 15 ? sl - 12 : 0;
   const uint32_t tapv = a.ring[(size_t)(tl & 3) * kConv + (tl >> 2) * 2048 + h * 128 + 8 * j + hw];
   const uint2 cwv = *reinterpret_cast<const uint2*>(a.conv_w + (size_t)(cl * 2048 + h * 128 + 8 * j + hw) * 4);
+  // per-head constants of phase 2 (lane 8: dt_bias and A_log of the head)
+  // and the gated norm's weight of phase 3, loaded now: issued after the
+  // exchange loads they would add memory round trips to both phases
+  // (unconditional, converted at use: a load under a branch is waited for
+  // inside it, and that wait would cover every load issued before it)
+  const uint32_t dtb_raw = a.dt_bias[h];
+  const float alog = a.a_log[h];
+  const uint32_t gnw_raw = a.norm_w[t & 127];
   // state: value rows 8j .. 8j+7 of the head, 16 lanes x 8 keys (t < 128)
   const int srow = 8 * j + (t >> 4) % 8, sj = t & 15;
   float S[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
@@ -419,8 +427,8 @@ __global__ __launch_bounds__(256) void k_gdn_xcd(GdnXcdArgs a) {
     if (t == 8 || t == 9) {  // lane 8: the decay g, lane 9: beta
       const uint2 ab = l2_load_2xu16(xb + kXab, xb + kXab + 1);
       if (t == 8) {
-        const float ax = rbf(bf2f(ab.x) + bf2f(a.dt_bias[h]));
-        gates[0] = es_exp(-es_exp(a.a_log[h]) * softplus_bf(ax));
+        const float ax = rbf(bf2f(ab.x) + bf2f(dtb_raw));
+        gates[0] = es_exp(-es_exp(alog) * softplus_bf(ax));
       } else {
         gates[1] = sigmoid_bf(bf2f(ab.y));
       }
@@ -481,7 +489,7 @@ __global__ __launch_bounds__(256) void k_gdn_xcd(GdnXcdArgs a) {
   }
   __syncthreads();
   {
-    const float norm = rbf(rbf(yv[t] * ginv[hl]) * bf2f(a.norm_w[dl]));
+    const float norm = rbf(rbf(yv[t] * ginv[hl]) * bf2f(gnw_raw));
     const float gz = xg[t + (t >> 5)];
     const float sy = 1.0f / (1.0f + es_exp(fabsf(gz)));
     const float sig = gz < 0.0f ? sy : 1.0f - sy;
