@@ -174,14 +174,39 @@ __global__ __launch_bounds__(256) void k_head_tail(HeadArgs a, int nb) {
   __shared__ unsigned int wmin[4];
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
   const int vocab = a.embed.n;
+  // Thread t's block partials (blocks t, t + 256, ...) are read once into
+  // registers when there are at most kTailRegs of them (the model's
+  // vocabulary needs 4), instead of once per pass; the step state too.
+  constexpr int kTailRegs = 4;
+  const bool in_regs = nb <= 256 * kTailRegs;
+  float2 pm[kTailRegs];
+#pragma unroll
+  for (int i = 0; i < kTailRegs; ++i) {
+    const int b = t + 256 * i;
+    pm[i] = in_regs && b < nb ? reinterpret_cast<const float2*>(a.part)[b] : make_float2(0.0f, 0.0f);
+  }
+  const int st_step = a.st && t == 0 ? a.st->step : 0;
+  const int st_pos = a.st && t == 0 ? a.st->pos : 0;
   float gm = -3.402823466e38f;
-  for (int b = t; b < nb; b += 256) gm = fmaxf(gm, a.part[2 * b]);
+  if (in_regs) {
+#pragma unroll
+    for (int i = 0; i < kTailRegs; ++i)
+      if (t + 256 * i < nb) gm = fmaxf(gm, pm[i].x);
+  } else {
+    for (int b = t; b < nb; b += 256) gm = fmaxf(gm, a.part[2 * b]);
+  }
   gm = wave_max(gm);
   if (lane == 0) wred[wave] = gm;
   __syncthreads();
   gm = fmaxf(fmaxf(wred[0], wred[1]), fmaxf(wred[2], wred[3]));
   float gs = 0.0f;
-  for (int b = t; b < nb; b += 256) gs = gs + a.part[2 * b + 1] * es_exp(a.part[2 * b] - gm);
+  if (in_regs) {
+#pragma unroll
+    for (int i = 0; i < kTailRegs; ++i)
+      if (t + 256 * i < nb) gs = gs + pm[i].y * es_exp(pm[i].x - gm);
+  } else {
+    for (int b = t; b < nb; b += 256) gs = gs + a.part[2 * b + 1] * es_exp(a.part[2 * b] - gm);
+  }
   gs = tree64(gs);
   if (lane == 0) wred2[wave] = gs;
   __syncthreads();
@@ -189,8 +214,16 @@ __global__ __launch_bounds__(256) void k_head_tail(HeadArgs a, int nb) {
   const float lse = rbf(es_log(gs) + gm);
   const float target = rbf(gm - lse);
   unsigned int first = 0xffffffffu;
-  for (int b = t; b < nb; b += 256)
-    if (rbf(a.part[2 * b] - lse) == target && (unsigned int)b < first) first = (unsigned int)b;
+  if (in_regs) {
+#pragma unroll
+    for (int i = 0; i < kTailRegs; ++i) {
+      const int b = t + 256 * i;
+      if (b < nb && rbf(pm[i].x - lse) == target && (unsigned int)b < first) first = (unsigned int)b;
+    }
+  } else {
+    for (int b = t; b < nb; b += 256)
+      if (rbf(a.part[2 * b] - lse) == target && (unsigned int)b < first) first = (unsigned int)b;
+  }
   first = wave_umin(first);
   if (lane == 0) wmin[wave] = first;
   __syncthreads();
@@ -212,11 +245,10 @@ __global__ __launch_bounds__(256) void k_head_tail(HeadArgs a, int nb) {
     if (a.token_out) *a.token_out = tok;
     if (a.lse_out) *a.lse_out = lse;
     if (a.st) {
-      const int step = a.st->step;
-      if (a.out_tokens) a.out_tokens[step] = tok;
+      if (a.out_tokens) a.out_tokens[st_step] = tok;
       a.st->token = tok;
-      a.st->step = step + 1;
-      a.st->pos = a.st->pos + 1;
+      a.st->step = st_step + 1;
+      a.st->pos = st_pos + 1;
     }
   }
 }
