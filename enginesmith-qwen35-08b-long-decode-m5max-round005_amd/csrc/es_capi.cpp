@@ -554,6 +554,12 @@ int es_engine_xcd_kernels(const es_engine* e) {
   return e->impl->fused_mlp() ? 1 : 0;
 }
 
+int es_engine_set_xcd_kernels(es_engine* e, int on) {
+  if (!e || !e->impl) return fail(ES_ERR_INVALID, "null engine");
+  std::string err;
+  return engine_rc(e->impl->set_xcd_kernels(on != 0, &err), err);
+}
+
 int es_engine_prompt_split(const es_engine* e, int* chunks, int* routed_rows, int* decode_rows) {
   if (!e || !e->impl || !chunks || !routed_rows || !decode_rows)
     return fail(ES_ERR_INVALID, "es_engine_prompt_split: null argument");

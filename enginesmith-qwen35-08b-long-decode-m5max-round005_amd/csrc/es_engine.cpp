@@ -197,8 +197,9 @@ int Engine::init(const void* blob, uint64_t bytes, std::string* err) {
   uint32_t xcc[256];
   ES_HIP(hipMemcpyAsync(xcc, err_, sizeof(xcc), hipMemcpyDeviceToHost, stream_), "placement probe");
   ES_HIP(hipStreamSynchronize(stream_), "init sync");
-  fused_mlp_ = xcc[0] < 8;
-  for (int b = 0; b < 256; ++b) fused_mlp_ = fused_mlp_ && xcc[b] == (xcc[0] + (uint32_t)b) % 8;
+  xcd_ok_ = xcc[0] < 8;
+  for (int b = 0; b < 256; ++b) xcd_ok_ = xcd_ok_ && xcc[b] == (xcc[0] + (uint32_t)b) % 8;
+  fused_mlp_ = xcd_ok_;
   for (auto& L : layers_) {
     if (!L.attention) continue;
     L.o_sb = static_cast<uint32_t*>(alloc((size_t)8 * 1024 * 4 * 4));
@@ -602,6 +603,24 @@ int Engine::set_prefill(int chunk_rows, std::string* err) {
     return 1;
   }
   prefill_rows_ = chunk_rows;
+  return 0;
+}
+
+int Engine::set_xcd_kernels(bool on, std::string* err) {
+  if (on && !xcd_ok_) {
+    if (err) *err = "XCD-cooperative kernels unavailable: workgroups are not dealt to the XCDs in turn";
+    return 1;
+  }
+  if (on == fused_mlp_) return 0;
+  // the cached graphs hold the other kernels; every step starts from the
+  // embedding, so the switch needs no state conversion
+  ES_HIP(hipStreamSynchronize(stream_), "sync");
+  for (auto& g : graphs_) {
+    (void)hipGraphExecDestroy(g.exec);
+    (void)hipGraphDestroy(g.g);
+  }
+  graphs_.clear();
+  fused_mlp_ = on;
   return 0;
 }
 

@@ -98,6 +98,9 @@ class Engine {
   int time_head(int reps, double* ms_avg, std::string* err);
 
   bool fused_mlp() const { return fused_mlp_; }
+  // Decode steps on the XCD-cooperative kernels (on, when the start-up probe
+  // allowed them) or on one launch per dependency; both give the same bits.
+  int set_xcd_kernels(bool on, std::string* err);
   int n_layers() const { return shape_.n_layers; }
   int vocab() const { return shape_.vocab; }
   int capacity() const { return capacity_; }
@@ -161,6 +164,7 @@ class Engine {
   // MLP), used when the start-up probe sees the blocks of a 256-block launch
   // dealt to the 8 XCDs in turn
   bool fused_mlp_ = false;
+  bool xcd_ok_ = false;           // the probe's verdict (packed words exist)
   float* dpart_ = nullptr;        // [8, 1024] down-projection octet partials
   uint16_t* xact_ = nullptr;      // [8, 512] activation exchange
   uint16_t* xgdn_ = nullptr;      // [8, 2, 648] GDN exchange (k_gdn_xcd)

@@ -104,6 +104,7 @@ _SIGNATURES = {
     "es_engine_set_prefill": (c_int, [c_void_p, c_int]),
     "es_engine_prompt_split": (c_int, [c_void_p, POINTER(c_int), POINTER(c_int), POINTER(c_int)]),
     "es_engine_xcd_kernels": (c_int, [c_void_p]),
+    "es_engine_set_xcd_kernels": (c_int, [c_void_p, c_int]),
     "es_engine_cancel": (None, [c_void_p]),
     "es_engine_clear_cancel": (None, [c_void_p]),
     "es_engine_position": (c_int, [c_void_p]),
@@ -336,6 +337,11 @@ class Engine:
         if r < 0:
             raise EsError(-r, lib().es_last_error().decode())
         return bool(r)
+
+    def set_xcd_kernels(self, on: bool) -> None:
+        """Decode steps on the XCD-cooperative kernels (True) or on one launch
+        per dependency (False); both give the same bits."""
+        check(lib().es_engine_set_xcd_kernels(self.h, 1 if on else 0))
 
     def prompt_split(self):
         """(batched chunks, routed rows, decode rows) of the last reset request."""

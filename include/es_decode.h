@@ -393,6 +393,12 @@ int es_engine_set_prefill(es_engine* e, int chunk_rows);
  * one launch per dependency; -ES_ERR_INVALID for a null engine. Both give the
  * same bits. No reference counterpart. */
 int es_engine_xcd_kernels(const es_engine* e);
+/* Selects the decode kernels: on=1 the XCD-cooperative ones (ES_ERR_INVALID
+ * when the placement probe ruled them out), on=0 one launch per dependency.
+ * Call between requests; the engine's cached decode graphs are rebuilt. No
+ * reference counterpart: lets tests hold the two kernel sets to the same
+ * bits. */
+int es_engine_set_xcd_kernels(es_engine* e, int on);
 
 /* How the last reset request consumed its prompt: batched chunks of
  * full-forward rows, rows of the routed last forward (0 or 2 .. 32), and

@@ -116,6 +116,42 @@ def test_graph_batches_equal_one_step_launches(small):
     assert np.array_equal(eng.read_kv(3, 0, end - 40, 40), kv_a)
 
 
+def test_xcd_kernels_equal_per_dependency_launches(small):
+    """The XCD-cooperative decode kernels (k_gdn_xcd: a GDN layer up to its
+    out_proj partials in one launch; k_mlp_xcd: a layer's MLP in one launch)
+    leave the same tokens, logits, GDN rings and states and KV rows as one
+    launch per dependency, on both attention routes (40 and 1,100 cached
+    positions: 32 and 64 chains)."""
+    eng, _, _ = small
+    assert eng.xcd_kernels(), "the start-up probe ruled out the XCD kernels on this GPU"
+    r = rng(47)
+    for n in (40, 1100):
+        prompt = r.integers(0, SMALL["vocab"], n).tolist()
+        extra = r.integers(0, SMALL["vocab"], 7).tolist()
+        runs = []
+        try:
+            for on in (True, False):
+                eng.set_xcd_kernels(on)
+                assert eng.xcd_kernels() == on
+                gen = eng.generate(prompt, 21, reset=True)  # one batch of 16 + 5
+                am, lg = eng.forced_decode([gen[-1]] + extra, want_logits=True)
+                end = eng.position
+                gdn = [eng.read_gdn(layer) for layer in range(3)]
+                kv = [eng.read_kv(3, which, 0, end) for which in (0, 1)]
+                runs.append((gen, am, lg, gdn, kv))
+        finally:
+            eng.set_xcd_kernels(True)
+        (ga, ama, lga, gdna, kva), (gb, amb, lgb, gdnb, kvb) = runs
+        assert ga == gb, n
+        assert np.array_equal(ama, amb), n
+        assert np.array_equal(lga, lgb), n
+        for (ra, sa), (rb, sb) in zip(gdna, gdnb):
+            assert np.array_equal(ra, rb), n
+            assert np.array_equal(sa.view(np.uint32), sb.view(np.uint32)), n
+        for a, b in zip(kva, kvb):
+            assert np.array_equal(a, b), n
+
+
 def test_reset_isolation(small):
     eng, _, _ = small
     r = rng(44)
