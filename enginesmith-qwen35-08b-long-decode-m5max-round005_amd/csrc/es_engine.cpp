@@ -156,8 +156,8 @@ int Engine::init(const void* blob, uint64_t bytes, std::string* err) {
   proj_part_ = static_cast<float*>(alloc((size_t)kGdnHeads * kHidden * sizeof(float)));
   hmid_ = static_cast<uint16_t*>(alloc(1024 * 2));
   dpart_ = static_cast<float*>(alloc(8 * 1024 * sizeof(float)));
-  xact_ = static_cast<uint16_t*>(alloc(8 * 512 * 2));
-  xgdn_ = static_cast<uint16_t*>(alloc(8 * 2 * 648 * 2));
+  xact_ = static_cast<uint32_t*>(alloc(8 * 512 * 4));
+  xgdn_ = static_cast<uint32_t*>(alloc(8 * 2 * 648 * 4));
   xflags_ = static_cast<uint32_t*>(alloc(8 * 32 * sizeof(uint32_t)));
   err_ = static_cast<uint32_t*>(alloc(256 * sizeof(uint32_t)));
   inv_freq_ = static_cast<float*>(alloc(32 * sizeof(float)));
@@ -239,11 +239,14 @@ int Engine::init(const void* blob, uint64_t bytes, std::string* err) {
   }
   ES_HIP(hipMemsetAsync(err_, 0, 256 * sizeof(uint32_t), stream_), "memset");
   ES_HIP(hipMemsetAsync(xflags_, 0, 8 * 32 * sizeof(uint32_t), stream_), "memset");
+  // tag 0 on every exchange word: the first tag a launch waits for is 1
+  ES_HIP(hipMemsetAsync(xact_, 0, 8 * 512 * 4, stream_), "memset");
+  ES_HIP(hipMemsetAsync(xgdn_, 0, 8 * 2 * 648 * 4, stream_), "memset");
   ES_HIP(hipStreamSynchronize(stream_), "init sync");
   return 0;
 }
 
-// The cooperative kernels report an exhausted barrier wait in err_; the
+// The cooperative kernels report an exhausted exchange wait in err_; the
 // step's results are then not to be trusted.
 int Engine::check_device_error(std::string* err) {
   if (!fused_mlp_) return 0;
@@ -253,7 +256,7 @@ int Engine::check_device_error(std::string* err) {
   if (e == 0) return 0;
   ES_HIP(hipMemsetAsync(err_, 0, sizeof(uint32_t), stream_), "error word");
   ES_HIP(hipStreamSynchronize(stream_), "error word");
-  if (err) *err = "decode kernels: an XCD group barrier timed out";
+  if (err) *err = "decode kernels: an XCD exchange wait timed out";
   return 2;
 }
 

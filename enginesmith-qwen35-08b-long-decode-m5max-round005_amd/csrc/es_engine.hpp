@@ -166,9 +166,9 @@ class Engine {
   bool fused_mlp_ = false;
   bool xcd_ok_ = false;           // the probe's verdict (packed words exist)
   float* dpart_ = nullptr;        // [8, 1024] down-projection octet partials
-  uint16_t* xact_ = nullptr;      // [8, 512] activation exchange
-  uint16_t* xgdn_ = nullptr;      // [8, 2, 648] GDN exchange (k_gdn_xcd)
-  uint32_t* xflags_ = nullptr;    // [8, 32] barrier flags
+  uint32_t* xact_ = nullptr;      // [8, 512] activation exchange words (value | tag << 16)
+  uint32_t* xgdn_ = nullptr;      // [8, 2, 648] GDN exchange words (k_gdn_xcd)
+  uint32_t* xflags_ = nullptr;    // [8, 32] per-block exchange counts
   uint32_t* err_ = nullptr;       // device error word of the cooperative kernels
   int check_device_error(std::string* err);
   float* inv_freq_ = nullptr;

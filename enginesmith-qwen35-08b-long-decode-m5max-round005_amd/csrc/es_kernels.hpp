@@ -155,9 +155,9 @@ struct MlpXcdArgs {
   uint16_t* h_mid;          // [1024] written: stream after the mixer
   const uint16_t* gain;     // post-attention norm [1024]
   float* dpart;             // [8, 1024] down partials
-  uint16_t* xact;           // [8, 512] activation exchange
-  uint32_t* flags;          // [8, 32] barrier flags (zero at start-up)
-  uint32_t* err;            // error word: 2 = a barrier wait hit its limit
+  uint32_t* xact;           // [8, 512] activation exchange words: bf16 | tag << 16 (zeroed at start-up)
+  uint32_t* flags;          // [8, 32] per-block exchange counts (zero at start-up)
+  uint32_t* err;            // error word: 2 = an exchange wait hit its limit
 };
 hipError_t launch_mlp_xcd(const MlpXcdArgs& a, int nparts, hipStream_t s);
 // A Gated DeltaNet layer up to its out_proj head partials in one 256-block
@@ -185,8 +185,8 @@ struct GdnXcdArgs {
   uint16_t* ring;           // [4, 6144]
   float* state;             // [16, 128, 128]
   float* part;              // [8, 1024] out_proj partials of the head pairs (2x, 2x+1)
-  uint16_t* xbuf;           // [8 XCDs][2 heads][648] exchange
-  uint32_t* flags;          // [8, 32] barrier flags (shared with k_mlp_xcd)
+  uint32_t* xbuf;           // [8 XCDs][2 heads][648] exchange words: bf16 | tag << 16 (zeroed at start-up)
+  uint32_t* flags;          // [8, 32] per-block exchange counts (shared with k_mlp_xcd)
   uint32_t* err;            // error word
   const StepState* st;
 };

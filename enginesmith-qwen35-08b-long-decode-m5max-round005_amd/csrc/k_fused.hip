@@ -5,8 +5,8 @@
 // 256-block launch and the blocks of one XCD have distinct b >> 3. A block
 // takes its XCD from the XCC_ID hardware register and its rank within the XCD
 // from b >> 3. The 32 blocks of an XCD share its L2 and exchange data through
-// it at the cost of one store and one load round trip, where any exchange
-// between XCDs costs a kernel boundary. The engine uses these kernels only
+// it (tagged words, below) at the cost of one store and one load, where any
+// exchange between XCDs costs a kernel boundary. The engine uses these kernels only
 // after a start-up probe has seen that dealing. Waits are bounded: a wait that
 // exceeds its spin limit (as it would if two blocks of one XCD shared a rank)
 // sets an error word, which the engine checks after each batch of steps, and
@@ -30,60 +30,57 @@ namespace {
 constexpr int kGroupBlocks = 32;          // blocks per XCD in a 256-block launch
 constexpr int kSpinLimit = 1 << 22;       // polls before a wait gives up
 
-// Loads that miss the vector L1 and read the XCD's L2, where the stores of the
-// group's other blocks land (the L1 writes through).
-__device__ __forceinline__ uint32_t l2_load_b32(const void* p) {
-  uint32_t v;
-  asm volatile("global_load_dword %0, %1, off sc1\n\ts_waitcnt vmcnt(0)" : "=v"(v) : "v"(p) : "memory");
-  return v;
-}
-// 64 contiguous bytes (four 16-byte loads) the same way. The loads and their
-// wait are one statement: the hardware does not hold a read of a register a
-// load has not filled yet, so no instruction may touch the outputs before the
-// wait.
-__device__ __forceinline__ Raw64 l2_load_64B(const void* p) {
-  Raw64 r;
-  asm volatile(
-      "global_load_dwordx4 %0, %4, off sc1\n\t"
-      "global_load_dwordx4 %1, %4, off offset:16 sc1\n\t"
-      "global_load_dwordx4 %2, %4, off offset:32 sc1\n\t"
-      "global_load_dwordx4 %3, %4, off offset:48 sc1\n\t"
-      "s_waitcnt vmcnt(0)"
-      : "=&v"(r.q[0]), "=&v"(r.q[1]), "=&v"(r.q[2]), "=&v"(r.q[3])
-      : "v"(p)
-      : "memory");
-  return r;
-}
-__device__ __forceinline__ void wait_loads() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
-
 __device__ __forceinline__ uint32_t xcc_id() {
   uint32_t v;
   asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(v));
   return v & 15u;
 }
 
-// Barrier of the 32 blocks of one XCD. Each block's flag counts the barriers
-// it has passed: every block publishes `target` (its flag at launch start plus
-// the barrier's number in the launch) once its stores are in the L2, then
-// waits until every flag of the group has reached it (compared as a wrapping
-// difference). All blocks pass every barrier, so the flags are equal at each
-// launch start and never need clearing; counting, not alternating, lets a
-// block that has left one barrier publish the next without misleading a block
-// still waiting at the first. Called by every thread of the block.
-__device__ __forceinline__ void xcd_barrier(uint32_t* flags, int rank, uint32_t target, uint32_t* err) {
-  wait_loads();  // this wave's stores (and loads) are complete
-  __syncthreads();
+// Exchanges within an XCD are tagged words: each published word holds a bf16
+// value in its low half and the exchange's tag in its high half, written whole
+// by one aligned 32-bit store (the L1 writes through to the XCD's L2), so a
+// word that carries the tag holds this exchange's value, and a reader polls
+// the data itself with loads that miss the L1 (sc1). That is one memory round
+// trip after the last write, where a barrier on flags takes four (the
+// writer's store acknowledgement, its flag store, the flag poll, the data
+// load). The tag is the low 16 bits of the block's exchange count: flags[rank]
+// holds the count as the block left its previous launch, and every block of an
+// XCD makes the same exchanges, so the counts agree at each launch start; a
+// launch with E exchanges uses count + 1 .. count + E and stores count + E.
+// Consecutive writes of a word are at most a few exchanges apart, so they
+// carry different tags (the words and counts start at 0, the first tag is 1).
+//
+// xcd_gather: wave 0 reads the `count` words (8 per lane) until every one
+// carries `tag`, and writes their values to lds (slice k of 32 at lds[36k ..]);
+// the block then syncs.
+__device__ __forceinline__ void xcd_gather(const uint32_t* words, int count, uint32_t tag, float* lds,
+                                           uint32_t* err) {
   if (threadIdx.x < 64) {
     const int lane = threadIdx.x;
-    if (lane == 0) flags[rank] = target;
+    const bool live = lane * 8 < count;
+    const uint32_t* p = words + (live ? lane * 8 : 0);
+    u32x4 w0, w1;
     for (int n = 0;; ++n) {
-      const uint32_t f = lane < kGroupBlocks ? l2_load_b32(flags + lane) : target;
-      if (__all((int)(f - target) >= 0)) break;
+      asm volatile(
+          "global_load_dwordx4 %0, %2, off sc1\n\t"
+          "global_load_dwordx4 %1, %2, off offset:16 sc1\n\t"
+          "s_waitcnt vmcnt(0)"
+          : "=&v"(w0), "=&v"(w1)
+          : "v"(p)
+          : "memory");
+      bool ok = true;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) ok = ok && (w0[i] >> 16) == tag && (w1[i] >> 16) == tag;
+      if (__all(ok || !live)) break;
       if (n >= kSpinLimit) {
         if (lane == 0) atomicOr(err, 2u);
         break;
       }
-      __builtin_amdgcn_s_sleep(1);
+    }
+    if (live) {
+      float4* d = reinterpret_cast<float4*>(lds + (lane >> 2) * 36 + (lane & 3) * 8);
+      d[0] = make_float4(bf_lo(w0[0]), bf_lo(w0[1]), bf_lo(w0[2]), bf_lo(w0[3]));
+      d[1] = make_float4(bf_lo(w1[0]), bf_lo(w1[1]), bf_lo(w1[2]), bf_lo(w1[3]));
     }
   }
   __syncthreads();
@@ -114,14 +111,14 @@ __global__ __launch_bounds__(256) void k_mlp_xcd(MlpXcdArgs a) {
   asm volatile("" :: "s"(a.gate.w), "s"(a.up.w), "s"(a.gu_sb), "s"(a.down.w), "s"(a.down_sb), "s"(a.h_old),
                "s"(a.part), "s"(a.h_mid), "s"(a.gain), "s"(a.dpart), "s"(a.xact), "s"(a.flags), "s"(a.err));
 
-  // ---- loads: residual, gain and mixer partials; the sense of this launch;
+  // ---- loads: residual, gain and mixer partials; the exchange count;
   // gate/up weights; the down weights of phase 2
   const uint2 ho = reinterpret_cast<const uint2*>(a.h_old)[t];
   const uint2 g4 = reinterpret_cast<const uint2*>(a.gain)[t];
   float4 pv[NPART];
 #pragma unroll
   for (int k = 0; k < NPART; ++k) pv[k] = reinterpret_cast<const float4*>(a.part + k * kHidden)[t];
-  // this block's barrier count as it left it in the previous launch
+  // this block's exchange count as it left the previous launch
   const uint32_t own = flags[rank];
   issue_fence();
   u32x4 cg[2], cu[2];
@@ -193,7 +190,8 @@ __global__ __launch_bounds__(256) void k_mlp_xcd(MlpXcdArgs a) {
   norm_block_1024(xv, x4, g4, norm_lds, xn);
   float xr[32];
   float xs = prep_slice(xn, xr);
-  uint16_t* xact = a.xact + x * 512;
+  uint32_t* xact = a.xact + x * 512;
+  const uint32_t tag = (own + 1u) & 0xffffu;
   float gv[2], uv[2];
 #pragma unroll
   for (int p = 0; p < 2; ++p) {
@@ -205,15 +203,24 @@ __global__ __launch_bounds__(256) void k_mlp_xcd(MlpXcdArgs a) {
   if (sl < 2 && (sl == 0 ? er[0] : er[1]) >= 0) {
     const float gb = rbf(sl == 0 ? gv[0] : gv[1]), ub = rbf(sl == 0 ? uv[0] : uv[1]);
     const float silu = rbf(gb * sigmoid_bf(gb));
-    xact[rank * nact + wave * 4 + 2 * sl + half] = (uint16_t)f2bf(silu * ub);
+    xact[rank * nact + wave * 4 + 2 * sl + half] = f2bf(silu * ub) | tag << 16;
   }
 
-  // ---- exchange the XCD's activation elements
-  xcd_barrier(flags, rank, own + 1u, a.err);
+  // ---- exchange the XCD's activation elements (hs is free again: the
+  // norm's barrier followed its last read)
+  if (t == 0) flags[rank] = own + 1u;
+  xcd_gather(xact, wide ? 512 : 256, tag, hs, a.err);
 
   // ---- phase 2: octet x of every down row of this block
-  const int aoff = wide ? (L < 8 ? 32 * L : 256 + 32 * (L - 8)) : 32 * L;
-  unpack_bf16x32(l2_load_64B(xact + aoff), xv);
+  // lane L's slice: elements 32L .. 32L+31 of the exchange
+  {
+    const float4* rp = reinterpret_cast<const float4*>(hs + L * 36);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const float4 q = rp[i];
+      xv[4 * i] = q.x; xv[4 * i + 1] = q.y; xv[4 * i + 2] = q.z; xv[4 * i + 3] = q.w;
+    }
+  }
   xs = prep_slice(xv, xr);
 #pragma unroll
   for (int p = 0; p < 2; ++p) {
@@ -226,17 +233,27 @@ __global__ __launch_bounds__(256) void k_mlp_xcd(MlpXcdArgs a) {
   }
 }
 
-// Two bf16 values read from the XCD's L2 (one statement with its wait).
-__device__ __forceinline__ uint2 l2_load_2xu16(const uint16_t* p0, const uint16_t* p1) {
+// Two tagged exchange words (xcd_gather's format) read by each lane from the
+// XCD's L2 until the first carries tag0 and the second tag1; returns their
+// bf16 values.
+__device__ __forceinline__ uint2 xcd_poll2(const uint32_t* p0, uint32_t tag0, const uint32_t* p1, uint32_t tag1,
+                                           uint32_t* err) {
   uint32_t a, b;
-  asm volatile(
-      "global_load_ushort %0, %2, off sc1\n\t"
-      "global_load_ushort %1, %3, off sc1\n\t"
-      "s_waitcnt vmcnt(0)"
-      : "=&v"(a), "=&v"(b)
-      : "v"(p0), "v"(p1)
-      : "memory");
-  return make_uint2(a, b);
+  for (int n = 0;; ++n) {
+    asm volatile(
+        "global_load_dword %0, %2, off sc1\n\t"
+        "global_load_dword %1, %3, off sc1\n\t"
+        "s_waitcnt vmcnt(0)"
+        : "=&v"(a), "=&v"(b)
+        : "v"(p0), "v"(p1)
+        : "memory");
+    if (__all((a >> 16) == tag0 && (b >> 16) == tag1)) break;
+    if (n >= kSpinLimit) {
+      atomicOr(err, 2u);
+      break;
+    }
+  }
+  return make_uint2(a & 0xffffu, b & 0xffffu);
 }
 
 // ---- k_gdn_xcd: a Gated DeltaNet layer up to its out_proj partials ----
@@ -275,7 +292,7 @@ __global__ __launch_bounds__(256) void k_gdn_xcd(GdnXcdArgs a) {
   const int x = (int)xcc_id() & 7, rank = blockIdx.x >> 3;
   const int h = 2 * x + (rank >> 4), j = rank & 15;
   uint32_t* flags = a.flags + x * kGroupBlocks;
-  uint16_t* xb = a.xbuf + (size_t)(x * 2 + (rank >> 4)) * kHx;
+  uint32_t* xb = a.xbuf + (size_t)(x * 2 + (rank >> 4)) * kHx;
   // every pointer argument in scalar registers at once: one wait for the
   // argument fetch instead of one per batch between the vector loads
   asm volatile("" :: "s"(a.x), "s"(a.dpart), "s"(a.h_out), "s"(a.gain), "s"(a.qkv.w), "s"(a.qkv_sb),
@@ -351,6 +368,8 @@ __global__ __launch_bounds__(256) void k_gdn_xcd(GdnXcdArgs a) {
       reinterpret_cast<const u32x4*>(a.out.w + (size_t)orow * 256 + (8 * x + os8) * 4));
   const uint32_t osb = __builtin_nontemporal_load(a.out_sb + ((size_t)x * 1024 + orow) * 4 + os8 / 2);
   issue_fence();
+  // tags of this launch's two exchanges (q, k, v, z, a, b; then y)
+  const uint32_t tag1 = (own + 1u) & 0xffffu, tag2 = (own + 2u) & 0xffffu;
 
   // ---- phase 1: input, RMSNorm, projection rows, ring, convolution
   float xv[32];
@@ -405,27 +424,27 @@ __global__ __launch_bounds__(256) void k_gdn_xcd(GdnXcdArgs a) {
       if (sl < 3) {
         a.ring[(size_t)slot_new * kConv + sl * 2048 + h * 128 + 8 * j + hw] = (uint16_t)raw;
         const uint32_t xt[4] = {x0, x1, x2, raw};
-        xb[sl * 128 + 8 * j + hw] = (uint16_t)f2bf(conv4_silu(xt, w));  // q, k, v of the exchange
+        xb[sl * 128 + 8 * j + hw] = f2bf(conv4_silu(xt, w)) | tag1 << 16;  // q, k, v of the exchange
       } else {
-        xb[kXz + 8 * j + hw] = (uint16_t)raw;
+        xb[kXz + 8 * j + hw] = raw | tag1 << 16;
       }
     }
   }
   if (j == 0 && wave == 0) {  // wave-uniform: half-waves 0 and 1 form a and b
     const uint32_t raw = f2bf(tree32(q4_slice_sb(c[4], sbw[4], xr, xs)));
-    if (sl == 0) xb[kXab + half] = (uint16_t)raw;
+    if (sl == 0) xb[kXab + half] = raw | tag1 << 16;
   }
-  xcd_barrier(flags, rank, own + 1u, a.err);
+  if (t == 0) flags[rank] = own + 2u;  // this launch's two exchanges
 
   // ---- phase 2: q/k L2 norms (k_gdn_recur_out's order), gates, delta rule
   {
-    const uint2 qkr = l2_load_2xu16(xb + (t < 128 ? kXq + t : kXk + (t - 128)), xb + kXv + 8 * j + (t & 7));
+    const uint2 qkr = xcd_poll2(xb + (t < 128 ? kXq + t : kXk + (t - 128)), tag1, xb + kXv + 8 * j + (t & 7), tag1, a.err);
     const float v = bf2f(qkr.x);
     const float ss = tree64(v * v);
     if (lane == 0) red[wave] = ss;
     if (t < 8) vv[t] = bf2f(qkr.y);
     if (t == 8 || t == 9) {  // lane 8: the decay g, lane 9: beta
-      const uint2 ab = l2_load_2xu16(xb + kXab, xb + kXab + 1);
+      const uint2 ab = xcd_poll2(xb + kXab, tag1, xb + kXab + 1, tag1, a.err);
       if (t == 8) {
         const float ax = rbf(bf2f(ab.x) + bf2f(dtb_raw));
         gates[0] = es_exp(-es_exp(alog) * softplus_bf(ax));
@@ -466,16 +485,15 @@ __global__ __launch_bounds__(256) void k_gdn_xcd(GdnXcdArgs a) {
     float* sp = a.state + ((size_t)(h * 128 + srow)) * 128 + 8 * sj;
     reinterpret_cast<float4*>(sp)[0] = make_float4(S[0], S[1], S[2], S[3]);
     reinterpret_cast<float4*>(sp)[1] = make_float4(S[4], S[5], S[6], S[7]);
-    if (sj == 0) xb[kXy + srow] = (uint16_t)f2bf(out);
+    if (sj == 0) xb[kXy + srow] = f2bf(out) | tag2 << 16;
   }
-  xcd_barrier(flags, rank, own + 2u, a.err);
 
   // ---- phase 3: gated RMSNorm of both heads of the pair (threads 128 hl ..
   // 128 hl + 127: head 2x + hl), out_proj rows 32 rank .. +31
   const int hl = t >> 7, dl = t & 127;
   {
-    const uint16_t* xh = a.xbuf + (size_t)(x * 2 + hl) * kHx;
-    const uint2 yz = l2_load_2xu16(xh + kXy + dl, xh + kXz + dl);
+    const uint32_t* xh = a.xbuf + (size_t)(x * 2 + hl) * kHx;
+    const uint2 yz = xcd_poll2(xh + kXy + dl, tag2, xh + kXz + dl, tag1, a.err);
     yv[t] = bf2f(yz.x);
     xg[t + (t >> 5)] = bf2f(yz.y);  // z, replaced by the gated value below
   }
