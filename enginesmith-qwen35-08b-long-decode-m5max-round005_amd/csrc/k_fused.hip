@@ -339,9 +339,13 @@ __global__ __launch_bounds__(256) void k_gdn_xcd(GdnXcdArgs a) {
   }
   // conv taps of the half-wave's q, k, v channels (ring slots 0..3) and
   // their conv weights, one load each across the half-wave: lane l < 12
-  // holds slot l & 3 of pass l >> 2, lane 12 + p the weights of pass p
+  // holds slot l & 3 of pass l >> 2, lane 12 + p the weights of pass p. The
+  // tap is read as the aligned word of channels hw & ~1, hw | 1 (both this
+  // block's; element offsets are even up to hw) and its half chosen after the
+  // norm: a 16-bit load needs a zero extension the compiler places early.
   const int tl = sl < 12 ? sl : 0, cl = sl >= 12 && sl < 15 ? sl - 12 : 0;
-  const uint32_t tapv = a.ring[(size_t)(tl & 3) * kConv + (tl >> 2) * 2048 + h * 128 + 8 * j + hw];
+  uint32_t tapw = reinterpret_cast<const uint32_t*>(
+      a.ring)[((size_t)(tl & 3) * kConv + (tl >> 2) * 2048 + h * 128 + 8 * j + hw) >> 1];
   const uint2 cwv = *reinterpret_cast<const uint2*>(a.conv_w + (size_t)(cl * 2048 + h * 128 + 8 * j + hw) * 4);
   // per-head constants of phase 2 (lane 8: dt_bias and A_log of the head)
   // and the gated norm's weight of phase 3, loaded now: issued after the
@@ -401,6 +405,12 @@ __global__ __launch_bounds__(256) void k_gdn_xcd(GdnXcdArgs a) {
   float xn[32];
   if (EMBED) norm_slice_1024(xv, graw, xn);
   else norm_block_1024(xv, x4, g4, norm_lds, xn);
+  // Keeps work on values loaded late (the conv taps, issued after every
+  // projection row) out of the norm: using one there makes the norm wait for
+  // all the loads issued before it.
+  issue_fence();
+  asm volatile("" : "+v"(tapw));
+  const uint32_t tapv = (hw & 1) ? tapw >> 16 : tapw & 0xffffu;
   float xr[32];
   const float xs = prep_slice(xn, xr);
   const int slot_new = pos & 3;
