@@ -256,6 +256,28 @@ __device__ __forceinline__ uint2 xcd_poll2(const uint32_t* p0, uint32_t tag0, co
   return make_uint2(a & 0xffffu, b & 0xffffu);
 }
 
+// The same for three words with one tag.
+__device__ __forceinline__ uint3 xcd_poll3(const uint32_t* p0, const uint32_t* p1, const uint32_t* p2, uint32_t tag,
+                                           uint32_t* err) {
+  uint32_t a, b, c;
+  for (int n = 0;; ++n) {
+    asm volatile(
+        "global_load_dword %0, %3, off sc1\n\t"
+        "global_load_dword %1, %4, off sc1\n\t"
+        "global_load_dword %2, %5, off sc1\n\t"
+        "s_waitcnt vmcnt(0)"
+        : "=&v"(a), "=&v"(b), "=&v"(c)
+        : "v"(p0), "v"(p1), "v"(p2)
+        : "memory");
+    if (__all((a >> 16) == tag && (b >> 16) == tag && (c >> 16) == tag)) break;
+    if (n >= kSpinLimit) {
+      atomicOr(err, 2u);
+      break;
+    }
+  }
+  return make_uint3(a & 0xffffu, b & 0xffffu, c & 0xffffu);
+}
+
 // ---- k_gdn_xcd: a Gated DeltaNet layer up to its out_proj partials ----
 // It replaces the input-norm + projection launch and the recurrence launch.
 // XCD x holds the head pair 2x, 2x + 1, 16 blocks each (rank r: head
@@ -448,19 +470,20 @@ __global__ __launch_bounds__(256) void k_gdn_xcd(GdnXcdArgs a) {
 
   // ---- phase 2: q/k L2 norms (k_gdn_recur_out's order), gates, delta rule
   {
-    const uint2 qkr = xcd_poll2(xb + (t < 128 ? kXq + t : kXk + (t - 128)), tag1, xb + kXv + 8 * j + (t & 7), tag1, a.err);
+    // lanes 8 and 9 also read a and b (the same exchange), the others their
+    // q/k word twice
+    const uint32_t* qk_word = xb + (t < 128 ? kXq + t : kXk + (t - 128));
+    const uint3 qkr = xcd_poll3(qk_word, xb + kXv + 8 * j + (t & 7), t == 8 || t == 9 ? xb + kXab + (t - 8) : qk_word,
+                                tag1, a.err);
     const float v = bf2f(qkr.x);
     const float ss = tree64(v * v);
     if (lane == 0) red[wave] = ss;
     if (t < 8) vv[t] = bf2f(qkr.y);
-    if (t == 8 || t == 9) {  // lane 8: the decay g, lane 9: beta
-      const uint2 ab = xcd_poll2(xb + kXab, tag1, xb + kXab + 1, tag1, a.err);
-      if (t == 8) {
-        const float ax = rbf(bf2f(ab.x) + bf2f(dtb_raw));
-        gates[0] = es_exp(-es_exp(alog) * softplus_bf(ax));
-      } else {
-        gates[1] = sigmoid_bf(bf2f(ab.y));
-      }
+    if (t == 8) {  // the decay g
+      const float ax = rbf(bf2f(qkr.z) + bf2f(dtb_raw));
+      gates[0] = es_exp(-es_exp(alog) * softplus_bf(ax));
+    } else if (t == 9) {  // beta
+      gates[1] = sigmoid_bf(bf2f(qkr.z));
     }
     __syncthreads();
     const float tot = t < 128 ? red[0] + red[1] : red[2] + red[3];
