@@ -534,12 +534,15 @@ __global__ __launch_bounds__(64) void k_attn_merge(AttnArgs a) {
   a.gated[h * 256 + d] = (uint16_t)merge_dim(gate_raw, two_pass, fac, total, v);
 }
 
-// Engine path: merge + gate of head h (every one of the 8 blocks of the head
-// forms all 256 dims) and the head's share of o_proj for output rows
-// 128*rg .. +127: per row the eight 32-column slice partials combined by
+// Engine path: merge + gate of head h (every one of the 32 blocks of the head
+// forms all 256 dims; more blocks with fewer rows each finish sooner than 8
+// blocks of 128 rows) and the head's share of o_proj for output rows
+// 32*rg .. +31: per row the eight 32-column slice partials combined by
 // tree8. The 64-slice tree of a K=2048 row pairs adjacent slices first, so the
 // row's full sum is the pairwise tree8 of the 8 head partials, formed by the
 // next launch, bit for bit.
+constexpr int kMergeRows = 32;  // o_proj rows per block: 8 lanes per row
+
 __global__ __launch_bounds__(256) void k_attn_merge_out(AttnArgs a, Q4 o, const uint32_t* o_sb, float* part) {
   __shared__ float fac[kAttnMaxChains];
   __shared__ float total;
@@ -557,15 +560,10 @@ __global__ __launch_bounds__(256) void k_attn_merge_out(AttnArgs a, Q4 o, const 
   load_chain_outputs(a, h, t, two_pass, v);
   const uint32_t gate_raw = a.q_proj[h * 512 + 256 + t];
   issue_fence();
-  u32x4 oc[4];
-  uint32_t osb[4];
-#pragma unroll
-  for (int p = 0; p < 4; ++p) {
-    const size_t row = (size_t)rg * 128 + 32 * p + (t >> 3);
-    oc[p] = *reinterpret_cast<const u32x4*>(o.w + row * 256 + gs * 4);
-    // the head's four group words of the row, contiguous (launch_pack_out_pairs)
-    osb[p] = o_sb[((size_t)h * 1024 + row) * 4 + sl / 2];
-  }
+  const size_t row = (size_t)kMergeRows * rg + (t >> 3);
+  const u32x4 oc = *reinterpret_cast<const u32x4*>(o.w + row * 256 + gs * 4);
+  // the head's four group words of the row, contiguous (launch_pack_out_pairs)
+  const uint32_t osb = o_sb[((size_t)h * 1024 + row) * 4 + sl / 2];
   issue_fence();
   if (wave == 0) merge_factors(mlv, lane, two_pass, fac, &total);
   __syncthreads();
@@ -575,12 +573,8 @@ __global__ __launch_bounds__(256) void k_attn_merge_out(AttnArgs a, Q4 o, const 
 #pragma unroll
   for (int q = 0; q < 32; ++q) xv[q] = gx[sl * 33 + q];
   const float xs = prep_slice(xv, xr);
-#pragma unroll
-  for (int p = 0; p < 4; ++p) {
-    const int row = rg * 128 + 32 * p + (t >> 3);
-    const float pp = tree8(q4_slice_sb(oc[p], osb[p], xr, xs));
-    if (sl == 0) part[(size_t)h * 1024 + row] = pp;
-  }
+  const float pp = tree8(q4_slice_sb(oc, osb, xr, xs));
+  if (sl == 0) part[(size_t)h * 1024 + row] = pp;
 }
 
 bool attn_ok(const AttnArgs& a) {
@@ -611,7 +605,7 @@ hipError_t launch_attn_fused(const AttnArgs& a, hipStream_t s) {
 hipError_t launch_attn_merge_out(const AttnArgs& a, const Q4& o, const uint32_t* o_sb, float* part,
                                  hipStream_t s) {
   if (!attn_ok(a) || !o.w || !o_sb || o.n != kHidden || o.k != 2048 || !part) return hipErrorInvalidValue;
-  hipLaunchKernelGGL(k_attn_merge_out, dim3(kQHeads, 8), dim3(256), 0, s, a, o, o_sb, part);
+  hipLaunchKernelGGL(k_attn_merge_out, dim3(kQHeads, kHidden / kMergeRows), dim3(256), 0, s, a, o, o_sb, part);
   return hipGetLastError();
 }
 
