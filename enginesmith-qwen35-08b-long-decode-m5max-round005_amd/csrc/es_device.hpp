@@ -25,6 +25,7 @@ constexpr int kQProj = 4096;      // 8 x (256 query + 256 gate)
 constexpr int kKvProj = 512;      // 2 x 256
 
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));  // for the nontemporal builtins
 typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
 
 // ---- bf16 ----

@@ -377,15 +377,16 @@ __global__ __launch_bounds__(256) void k_gdn_xcd(GdnXcdArgs a) {
   const uint32_t dtb_raw = a.dt_bias[h];
   const float alog = a.a_log[h];
   const uint32_t gnw_raw = a.norm_w[t & 127];
-  // state: value rows 8j .. 8j+7 of the head, 16 lanes x 8 keys (t < 128)
+  // state: value rows 8j .. 8j+7 of the head, 16 lanes x 8 keys (t < 128).
+  // Read and written non-temporally (1 MB per layer, touched once a step).
   const int srow = 8 * j + (t >> 4) % 8, sj = t & 15;
   float S[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
   if (t < 128) {
-    const float* sp = a.state + ((size_t)(h * 128 + srow)) * 128 + 8 * sj;
-    const float4 lo = reinterpret_cast<const float4*>(sp)[0];
-    const float4 hi = reinterpret_cast<const float4*>(sp)[1];
-    S[0] = lo.x; S[1] = lo.y; S[2] = lo.z; S[3] = lo.w;
-    S[4] = hi.x; S[5] = hi.y; S[6] = hi.z; S[7] = hi.w;
+    const f32x4* sp = reinterpret_cast<const f32x4*>(a.state + ((size_t)(h * 128 + srow)) * 128 + 8 * sj);
+    const f32x4 lo = __builtin_nontemporal_load(sp);
+    const f32x4 hi = __builtin_nontemporal_load(sp + 1);
+    S[0] = lo[0]; S[1] = lo[1]; S[2] = lo[2]; S[3] = lo[3];
+    S[4] = hi[0]; S[5] = hi[1]; S[6] = hi[2]; S[7] = hi[3];
   }
   // out_proj: row 32 rank + t/8, K slice 8x + t%8 (the pair's eight slices,
   // 128 contiguous bytes of the row)
@@ -515,9 +516,9 @@ __global__ __launch_bounds__(256) void k_gdn_xcd(GdnXcdArgs a) {
       out = fmaf(S[i], qq[i], out);
     }
     out = tree16(out);
-    float* sp = a.state + ((size_t)(h * 128 + srow)) * 128 + 8 * sj;
-    reinterpret_cast<float4*>(sp)[0] = make_float4(S[0], S[1], S[2], S[3]);
-    reinterpret_cast<float4*>(sp)[1] = make_float4(S[4], S[5], S[6], S[7]);
+    f32x4* sp = reinterpret_cast<f32x4*>(a.state + ((size_t)(h * 128 + srow)) * 128 + 8 * sj);
+    __builtin_nontemporal_store(f32x4{S[0], S[1], S[2], S[3]}, sp);
+    __builtin_nontemporal_store(f32x4{S[4], S[5], S[6], S[7]}, sp + 1);
     if (sj == 0) xb[kXy + srow] = f2bf(out) | tag2 << 16;
   }
 
