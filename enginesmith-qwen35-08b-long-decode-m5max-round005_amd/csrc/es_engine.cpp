@@ -703,10 +703,18 @@ int Engine::prefill_rows(int pos0, int m, int slot, bool wait_prev, bool routed,
       ES_HIP(hipStreamWaitEvent(s, state_done_[(slot + kPrefillStreams - 1) % kPrefillStreams][l], 0),
              "prefill wait");
     if (!L.attention) {
-      ES_HIP(linear_rows(L.qkv, b.u, m, routed, nullptr, b.raw, s), "prefill qkv");
-      ES_HIP(linear_rows(L.z, b.u, m, routed, nullptr, b.z, s), "prefill z");
-      ES_HIP(linear_rows(L.a, b.u, m, routed, nullptr, b.a, s), "prefill a");
-      ES_HIP(linear_rows(L.b, b.u, m, routed, nullptr, b.b, s), "prefill b");
+      if (routed) {
+        ES_HIP(linear_rows(L.qkv, b.u, m, routed, nullptr, b.raw, s), "prefill qkv");
+        ES_HIP(linear_rows(L.z, b.u, m, routed, nullptr, b.z, s), "prefill z");
+        ES_HIP(linear_rows(L.a, b.u, m, routed, nullptr, b.a, s), "prefill a");
+        ES_HIP(linear_rows(L.b, b.u, m, routed, nullptr, b.b, s), "prefill b");
+      } else {
+        // the four input linears share their input: one GEMM over the
+        // stacked rows, each segment to its own output (the same bits)
+        const Q4 w[4] = {L.qkv, L.z, L.a, L.b};
+        uint16_t* const y[4] = {b.raw, b.z, b.a, b.b};
+        ES_HIP(launch_q4_gemm_stacked(w, y, 4, b.u, m, s), "prefill qkv|z|a|b");
+      }
       GdnPrepRowsArgs g{b.raw, L.ring, L.conv_w, b.a, b.b, L.a_log, L.dt_bias, pos0, m,
                         b.q, b.k, b.v, b.g, b.beta};
       ES_HIP(launch_gdn_prep_rows(g, s), "prefill gdn prepare");
@@ -715,9 +723,15 @@ int Engine::prefill_rows(int pos0, int m, int slot, bool wait_prev, bool routed,
       ES_HIP(launch_gdn_norm_gate_rows(b.y, b.z, L.gdn_norm, m, b.gated, s), "prefill gdn norm gate");
       ES_HIP(linear_rows(L.out, b.gated, m, routed, b.h, b.h, s), "prefill out_proj");
     } else {
-      ES_HIP(linear_rows(L.q, b.u, m, routed, nullptr, b.qp, s), "prefill q");
-      ES_HIP(linear_rows(L.k, b.u, m, routed, nullptr, b.kp, s), "prefill k");
-      ES_HIP(linear_rows(L.v, b.u, m, routed, nullptr, b.vp, s), "prefill v");
+      if (routed) {
+        ES_HIP(linear_rows(L.q, b.u, m, routed, nullptr, b.qp, s), "prefill q");
+        ES_HIP(linear_rows(L.k, b.u, m, routed, nullptr, b.kp, s), "prefill k");
+        ES_HIP(linear_rows(L.v, b.u, m, routed, nullptr, b.vp, s), "prefill v");
+      } else {
+        const Q4 w[3] = {L.q, L.k, L.v};
+        uint16_t* const y[3] = {b.qp, b.kp, b.vp};
+        ES_HIP(launch_q4_gemm_stacked(w, y, 3, b.u, m, s), "prefill q|k|v");
+      }
       AttnPrepRowsArgs a{b.qp, b.kp, b.vp, L.q_norm, L.k_norm, inv_freq_, pos0, m,
                          b.query, L.kcache, L.vcache, capacity_};
       ES_HIP(launch_attn_prep_rows(a, s), "prefill attention prepare");

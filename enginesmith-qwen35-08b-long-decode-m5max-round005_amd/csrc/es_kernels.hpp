@@ -217,6 +217,18 @@ hipError_t launch_q4_gemm(const Q4& w, const uint16_t* x, int m, const uint16_t*
 // row-batched linears followed by swiglu_bf16): act [m, gate.n].
 hipError_t launch_q4_gemm_swiglu(const Q4& gate, const Q4& up, const uint16_t* x, int m, uint16_t* act,
                                  hipStream_t s);
+// Linears sharing one input, stacked along N (q|k|v, qkv|z|a|b): segment s
+// is Y_s[m, w[s].n] = bf16(X . W_s^T), bit for bit the separate linears.
+struct WideGemmArgs {
+  Q4 w[4];
+  uint16_t* y[4];
+  int nstart[5];  // first column of each segment; nstart[nseg] = total N
+  int nseg;
+  const uint16_t* x;
+  int m;
+};
+hipError_t launch_q4_gemm_stacked(const Q4* w, uint16_t* const* y, int nseg, const uint16_t* x, int m,
+                                  hipStream_t s);
 // Row forms of the decode operators (m rows = consecutive positions
 // pos0 .. pos0+m-1), each with the decode kernels' arithmetic per row.
 hipError_t launch_embed_rows(const Q4& e, const uint32_t* tokens, int m, uint16_t* h, hipStream_t s);

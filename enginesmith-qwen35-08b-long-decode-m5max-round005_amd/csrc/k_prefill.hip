@@ -21,6 +21,13 @@ namespace {
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef __attribute__((address_space(3))) void* lds_ptr_t;
+
+// Wait until at most N vector-memory operations of this wave are pending.
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
 
 constexpr int kGemmBM = 128, kGemmBN = 128, kGemmBK = 64, kGemmLds = 72;
 
@@ -157,6 +164,249 @@ __global__ __launch_bounds__(256) void k_q4_gemm(Q4 w, Q4 w2, const uint16_t* __
         y[o] = (uint16_t)f2bf(v);
       }
     }
+}
+
+// ---- wide GEMM: 256 x 256 block tiles for the linears with N >= 2048 ----
+//
+// k_q4_gemm_wide computes the same products as k_q4_gemm, bit for bit: the
+// same bf16 operands (weights dequantised as bf16(fma(scale, q, bias))) and,
+// for every output element, the same sequence of 32x32x16 MFMAs over K in
+// increasing order. Only the tiling differs. A block of 256 threads owns a
+// 256 x 256 output tile; each wave a 128 x 128 quarter (16 MFMA accumulators
+// in the accumulation registers), so every 16-byte fragment read from LDS
+// feeds four MFMAs instead of two. X reaches LDS by DMA (global_load_lds, no
+// registers); each thread dequantises one weight row per 64-column step.
+// LDS rows are 128 bytes with no padding; the 16-byte chunk c of row r sits
+// at slot c ^ ((r >> 1) & 7), so the 16 rows that one 16-lane group of a
+// fragment read touches cover all 64 banks once. The X DMA applies the same
+// permutation on the source side (lane l of an instruction fetches the chunk
+// that belongs in its slot).
+// Output columns may span up to four weight matrices stacked along N
+// (q|k|v, qkv|z|a|b), each written to its own [m][n_s] output.
+// A block holds a whole CU (128 KB of LDS, all registers), so beside the
+// other prefill stream's recurrence or attention it gets fewer CUs than the
+// 128 x 128 kernel, whose blocks share CUs: in the two-stream prefill it pays
+// for the stacked input linears (one launch for four) but not for gate/up,
+// which keeps k_q4_gemm.
+constexpr int kWideM = 256, kWideN = 256, kWideK = 64;
+
+__device__ __forceinline__ int wide_slot(int r, int c) { return ((c ^ ((r >> 1) & 7)) << 3) + (r << 6); }
+
+// Fragment reads as inline assembly: the compiler treats an LDS read after a
+// DMA into LDS as dependent on it and would wait for every DMA in flight
+// (including the next stage's) before the first read of a step. Four reads
+// of one operand: rows r, r+32, r+64, r+96 share the slot, 4096 bytes apart.
+__device__ __forceinline__ void wide_read4(uint32_t addr, u32x4& f0, u32x4& f1, u32x4& f2, u32x4& f3) {
+  asm volatile(
+      "ds_read_b128 %0, %4\n\t"
+      "ds_read_b128 %1, %4 offset:4096\n\t"
+      "ds_read_b128 %2, %4 offset:8192\n\t"
+      "ds_read_b128 %3, %4 offset:12288"
+      : "=&v"(f0), "=&v"(f1), "=&v"(f2), "=&v"(f3)
+      : "v"(addr));
+}
+__device__ __forceinline__ void wide_wait8(u32x4 (&a)[4], u32x4 (&b)[4]) {
+  asm volatile("s_waitcnt lgkmcnt(0)"
+               : "+v"(a[0]), "+v"(a[1]), "+v"(a[2]), "+v"(a[3]), "+v"(b[0]), "+v"(b[1]), "+v"(b[2]), "+v"(b[3]));
+}
+
+// One 64-column step of the MFMA loop over the staged tiles at LDS byte
+// addresses xt (X) and wt (W): the fragments of slice kk + 1 are read while
+// the 16 MFMAs of slice kk run.
+__device__ __forceinline__ void wide_step(uint32_t xt, uint32_t wt, int xrow, int wrow, f32x16 (&acc)[4][4],
+                                          int fh) {
+  // byte address of slot c of rows xrow (+32i) and wrow (+32j)
+  auto xaddr = [&](int c) { return xt + (uint32_t)(wide_slot(xrow, c) * 2); };
+  auto waddr = [&](int c) { return wt + (uint32_t)(wide_slot(wrow, c) * 2); };
+  u32x4 fa[2][4], fb[2][4];
+  wide_read4(xaddr(fh), fa[0][0], fa[0][1], fa[0][2], fa[0][3]);
+  wide_read4(waddr(fh), fb[0][0], fb[0][1], fb[0][2], fb[0][3]);
+  wide_wait8(fa[0], fb[0]);
+#pragma unroll
+  for (int kk = 0; kk < 4; ++kk) {
+    const int cur = kk & 1;
+    if (kk + 1 < 4) {
+      const int c = 2 * (kk + 1) + fh;
+      wide_read4(xaddr(c), fa[cur ^ 1][0], fa[cur ^ 1][1], fa[cur ^ 1][2], fa[cur ^ 1][3]);
+      wide_read4(waddr(c), fb[cur ^ 1][0], fb[cur ^ 1][1], fb[cur ^ 1][2], fb[cur ^ 1][3]);
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, fa[cur][i]),
+                                                            __builtin_bit_cast(bf16x8, fb[cur][j]), acc[i][j], 0,
+                                                            0, 0);
+    if (kk + 1 < 4) wide_wait8(fa[cur ^ 1], fb[cur ^ 1]);
+  }
+}
+
+// Barrier for the staged tiles: the caller has waited for its own X DMA
+// (vmcnt); lgkmcnt(0) covers the dequantised weights written by ds_write.
+// Unlike __syncthreads it does not wait for the weight loads still in flight.
+__device__ __forceinline__ void wide_barrier() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
+// The two stages are four separate LDS arrays (not one indexed array), so the
+// compiler can see that the DMA into one stage does not write the other and
+// does not wait for it before reading fragments.
+__shared__ __attribute__((aligned(16))) uint16_t g_wide_x0[kWideM * kWideK];
+__shared__ __attribute__((aligned(16))) uint16_t g_wide_x1[kWideM * kWideK];
+__shared__ __attribute__((aligned(16))) uint16_t g_wide_w0[kWideN * kWideK];
+__shared__ __attribute__((aligned(16))) uint16_t g_wide_w1[kWideN * kWideK];
+
+__global__ __launch_bounds__(256, 1) void k_q4_gemm_wide(WideGemmArgs a) {
+  const int t = threadIdx.x, lane = t & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
+  const int K = a.w[0].k, m = a.m;
+  const int m0 = blockIdx.y * kWideM;
+  const int nk = K / kWideK;
+
+  // this thread's weight row: segment, row within it, validity
+  const int n_row = blockIdx.x * kWideN + t;
+  int seg = 0;
+#pragma unroll
+  for (int sg = 1; sg < 4; ++sg)
+    if (sg < a.nseg && n_row >= a.nstart[sg]) seg = sg;
+  const int wrow = n_row - a.nstart[seg];
+  const bool wok = n_row < a.nstart[a.nseg];
+  const uint32_t* wcodes = seg == 0 ? a.w[0].w : seg == 1 ? a.w[1].w : seg == 2 ? a.w[2].w : a.w[3].w;
+  const uint16_t* wsc = seg == 0 ? a.w[0].s : seg == 1 ? a.w[1].s : seg == 2 ? a.w[2].s : a.w[3].s;
+  const uint16_t* wbi = seg == 0 ? a.w[0].b : seg == 1 ? a.w[1].b : seg == 2 ? a.w[2].b : a.w[3].b;
+  const int r_ok = wok ? wrow : 0;
+  const u32x4* cptr = reinterpret_cast<const u32x4*>(wcodes + (size_t)r_ok * (K >> 3));
+  const uint16_t* sptr = wsc + (size_t)r_ok * (K >> 6);
+  const uint16_t* bptr = wbi + (size_t)r_ok * (K >> 6);
+
+  // X DMA: instruction i of this wave fills LDS rows 8(8w+i) .. +7, lane l
+  // the slot l & 7 of row l >> 3
+  const int xr_lane = lane >> 3, xslot = lane & 7;
+  auto issue_x = [&](int kb, uint16_t* xt) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int r = (wave * 8 + i) * 8 + xr_lane;
+      const int c = xslot ^ ((r >> 1) & 7);
+      const int gr = min(m0 + r, m - 1);
+      const uint16_t* g = a.x + (size_t)gr * K + kb * kWideK + c * 8;
+      __builtin_amdgcn_global_load_lds(g, (lds_ptr_t)&xt[(wave * 8 + i) * 512], 16, 0, 0);
+    }
+  };
+  // Weight loads and the dequantised stores are inline assembly as well, so
+  // the compiler inserts no waits of its own in the loop; each wait below is
+  // counted by hand (the order of the vector-memory operations of a step:
+  // the previous step's 4 weight loads, 8 X DMA, this step's 4 weight loads).
+  struct WRegs {
+    u32x4 c0, c1;
+    uint32_t s, b;
+  };
+  auto load_w = [&](int kb, WRegs& r) {
+    const u32x4* cp = cptr + kb * 2;
+    const uint16_t* sp = sptr + kb;
+    const uint16_t* bp = bptr + kb;
+    asm volatile(
+        "global_load_dwordx4 %0, %4, off\n\t"
+        "global_load_dwordx4 %1, %4, off offset:16\n\t"
+        "global_load_ushort %2, %5, off\n\t"
+        "global_load_ushort %3, %6, off"
+        : "=&v"(r.c0), "=&v"(r.c1), "=&v"(r.s), "=&v"(r.b)
+        : "v"(cp), "v"(sp), "v"(bp));
+  };
+  // dequantise 64 weights (bf16(fma(scale, q, bias)); rows past N are 0);
+  // the caller has waited for the set's loads
+  auto store_w = [&](uint32_t wt, const WRegs& r) {
+    const float sc = wok ? bf2f(r.s) : 0.0f, bi = wok ? bf2f(r.b) : 0.0f;
+#pragma unroll
+    for (int c = 0; c < 8; ++c) {
+      const uint32_t word = c < 4 ? r.c0[c] : r.c1[c - 4];
+      float v[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) v[j] = fmaf(sc, (float)((word >> (4 * j)) & 15u), bi);
+      const u32x4 o{pack2(v[0], v[1]), pack2(v[2], v[3]), pack2(v[4], v[5]), pack2(v[6], v[7])};
+      asm volatile("ds_write_b128 %0, %1" ::"v"(wt + (uint32_t)(wide_slot(t, c) * 2)), "v"(o));
+    }
+  };
+  // waits for a weight set with N vector-memory operations issued after it
+  auto wait_set12 = [](WRegs& r) { asm volatile("s_waitcnt vmcnt(12)" : "+v"(r.c0), "+v"(r.c1), "+v"(r.s), "+v"(r.b)); };
+  auto wait_set4 = [](WRegs& r) { asm volatile("s_waitcnt vmcnt(4)" : "+v"(r.c0), "+v"(r.c1), "+v"(r.s), "+v"(r.b)); };
+
+  const int wm = (wave >> 1) * 128, wn = (wave & 1) * 128;
+  const int fr = lane & 31, fh = lane >> 5;
+  f32x16 acc[4][4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+
+  // Weights are loaded two steps ahead (register sets wa, wb) and dequantised
+  // into the stage being filled while the MFMAs of the other stage run; the
+  // end-of-step wait covers the X DMA but not the four weight loads issued
+  // after it.
+  auto lds_addr = [](const uint16_t* p) {
+    return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) uint16_t*)p;
+  };
+  const uint32_t lx0 = lds_addr(g_wide_x0), lx1 = lds_addr(g_wide_x1);
+  const uint32_t lw0 = lds_addr(g_wide_w0), lw1 = lds_addr(g_wide_w1);
+  // Weights are loaded two steps ahead (register set wa for even steps, wb
+  // for odd) and dequantised into the stage being filled after the MFMAs of
+  // the other stage are issued. Every step issues the same operations, so the
+  // loop has no branch between a load and its wait: the X DMA of step s + 1
+  // (8 operations) and the weight loads of step s + 2 (4), with the step
+  // clamped to the last one (those loads fill the stage nobody reads again).
+  // At the start of step s only the loads of weight set s + 1 are in flight;
+  // it waits for them with 12 operations issued after them, and for its DMA
+  // with 4.
+  WRegs wa, wb;
+  issue_x(0, g_wide_x0);
+  load_w(0, wa);
+  load_w(1, wb);
+  wait_set4(wa);
+  store_w(lw0, wa);
+  wide_barrier();
+  auto run_step = [&](int st, uint32_t lx, uint32_t lw, uint16_t* x_next, uint32_t lw_next, WRegs& w_next,
+                      WRegs& w_after) {
+    issue_x(min(st + 1, nk - 1), x_next);
+    load_w(min(st + 2, nk - 1), w_after);
+    issue_fence();
+    wide_step(lx, lw, wm + fr, wn + fr, acc, fh);
+    wait_set12(w_next);
+    store_w(lw_next, w_next);
+    wait_vmcnt<4>();
+    wide_barrier();
+  };
+  for (int kb = 0; kb < nk; kb += 2) {  // K is a multiple of 128: nk even
+    run_step(kb, lx0, lw0, g_wide_x1, lw1, wb, wa);
+    run_step(kb + 1, lx1, lw1, g_wide_x0, lw0, wa, wb);
+  }
+  // The last step's weight loads (into wb) are still in flight: wait with
+  // both sets as operands, so the compiler keeps their registers until the
+  // data has landed instead of giving them to the epilogue.
+  asm volatile("s_waitcnt vmcnt(0)"
+               : "+v"(wa.c0), "+v"(wa.c1), "+v"(wa.s), "+v"(wa.b), "+v"(wb.c0), "+v"(wb.c1), "+v"(wb.s), "+v"(wb.b));
+
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int n = blockIdx.x * kWideN + wn + 32 * j + fr;
+    if (n >= a.nstart[a.nseg]) continue;
+    int sg = 0;
+#pragma unroll
+    for (int q = 1; q < 4; ++q)
+      if (q < a.nseg && n >= a.nstart[q]) sg = q;
+    uint16_t* y = sg == 0 ? a.y[0] : sg == 1 ? a.y[1] : sg == 2 ? a.y[2] : a.y[3];
+    const int ld = a.nstart[sg + 1] - a.nstart[sg], col = n - a.nstart[sg];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int row = m0 + wm + 32 * i + 8 * (r >> 2) + 4 * fh + (r & 3);
+        if (row < m) y[(size_t)row * ld + col] = (uint16_t)f2bf(acc[i][j][r]);
+      }
+  }
 }
 
 // ---- row kernels: the decode operators' arithmetic, one row per token ----
@@ -617,10 +867,6 @@ __global__ __launch_bounds__(256) void k_attn_gate_rows(const uint16_t* o, const
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 constexpr int kFaQ = 32, kFaStages = 4, kFaKs = 264, kFaVs = 272;
 constexpr int kFaStageHalves = 32 * kFaKs + 32 * kFaVs;
-template <int N>
-__device__ __forceinline__ void wait_vmcnt() {
-  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
-}
 // eight transposing reads at a + 32*i bytes (i = 0..7: eight 16-dim tiles),
 // then their wait
 __device__ __forceinline__ void lds_read_tr16_x8(uint32_t a, uint2 (&r)[8]) {
@@ -811,10 +1057,53 @@ __global__ __launch_bounds__(512, 1) void k_attn_prefill(const uint16_t* qr, con
 
 }  // namespace
 
+// The wide kernel takes a GEMM whose total N fills at least eight of its
+// 256-column tiles; narrower ones (N = 1024 and below, with the residual add)
+// keep the 128 x 128 tiles, which give 256 or more blocks.
+static bool wide_ok(int n_total, int k) { return n_total >= 8 * kWideN && k % (2 * kWideK) == 0; }
+
+static hipError_t launch_wide(const WideGemmArgs& a, hipStream_t s) {
+  const dim3 grid((a.nstart[a.nseg] + kWideN - 1) / kWideN, (a.m + kWideM - 1) / kWideM);
+  hipLaunchKernelGGL(k_q4_gemm_wide, grid, dim3(256), 0, s, a);
+  return hipGetLastError();
+}
+
+hipError_t launch_q4_gemm_stacked(const Q4* w, uint16_t* const* y, int nseg, const uint16_t* x, int m,
+                                  hipStream_t s) {
+  if (!w || !y || nseg < 1 || nseg > 4 || !x || m < 1) return hipErrorInvalidValue;
+  WideGemmArgs a{};
+  int n = 0;
+  for (int i = 0; i < nseg; ++i) {
+    if (!w[i].w || !w[i].s || !w[i].b || !y[i] || w[i].n < 1 || w[i].k != w[0].k || w[i].k < kGemmBK ||
+        w[i].k % kGemmBK != 0)
+      return hipErrorInvalidValue;
+    a.w[i] = w[i];
+    a.y[i] = y[i];
+    a.nstart[i] = n;
+    n += w[i].n;
+  }
+  for (int i = nseg; i < 4; ++i) {
+    a.w[i] = w[0];
+    a.y[i] = y[0];
+  }
+  a.nstart[nseg] = n;
+  for (int i = nseg + 1; i < 5; ++i) a.nstart[i] = n;
+  a.nseg = nseg;
+  a.x = x;
+  a.m = m;
+  if (wide_ok(n, w[0].k)) return launch_wide(a, s);
+  for (int i = 0; i < nseg; ++i) {
+    const dim3 grid((w[i].n + kGemmBN - 1) / kGemmBN, (m + kGemmBM - 1) / kGemmBM);
+    hipLaunchKernelGGL(k_q4_gemm<false>, grid, dim3(256), 0, s, w[i], w[i], x, m, nullptr, y[i]);
+  }
+  return hipGetLastError();
+}
+
 hipError_t launch_q4_gemm(const Q4& w, const uint16_t* x, int m, const uint16_t* residual, uint16_t* y,
                           hipStream_t s) {
   if (!w.w || !w.s || !w.b || w.n < 1 || w.k < kGemmBK || w.k % kGemmBK != 0 || !x || !y || m < 1)
     return hipErrorInvalidValue;
+  if (!residual && wide_ok(w.n, w.k)) return launch_q4_gemm_stacked(&w, &y, 1, x, m, s);
   const dim3 grid((w.n + kGemmBN - 1) / kGemmBN, (m + kGemmBM - 1) / kGemmBM);
   hipLaunchKernelGGL(k_q4_gemm<false>, grid, dim3(256), 0, s, w, w, x, m, residual, y);
   return hipGetLastError();

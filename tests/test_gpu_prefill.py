@@ -12,8 +12,10 @@ from helpers import assert_bf16_close, bf16, f32, random_q4, rng
 
 pytestmark = pytest.mark.gpu
 
+# N >= 2048 (K a multiple of 128) takes the 256 x 256 tiles, the rest the 128 x 128 tiles
 GEMM_SHAPES = [(1, 16, 1024), (17, 1024, 1024), (128, 128, 64), (300, 6144, 1024), (257, 1024, 3584),
-               (2048, 512, 1024), (64, 1000, 2048), (130, 16, 1024)]
+               (2048, 512, 1024), (64, 1000, 2048), (130, 16, 1024), (1, 2048, 1024), (513, 2304, 1024),
+               (257, 2048, 3584), (600, 4096, 2048)]
 
 
 @pytest.mark.parametrize("m,n,k", GEMM_SHAPES)
@@ -56,6 +58,31 @@ def test_q4_gemm_residual_in_place(k):
     d = np.abs(f32(got).astype(np.float64) - sum_)
     assert np.all(d <= ulp(y) + ulp(sum_)), f"gemm add k={k}: max excess {np.max(d - ulp(y) - ulp(sum_))}"
     assert np.mean(got != want) <= 0.01
+
+
+@pytest.mark.parametrize("m,k", [(1, 1024), (300, 1024), (513, 3584)])
+def test_wide_gemm_equals_narrow_tiles(m, k):
+    """An N = 2048 GEMM (256 x 256 tiles) and its two 1024-row halves as
+    separate GEMMs (128 x 128 tiles) give the same bits: every output element
+    is the same chain of MFMAs over K in both."""
+    print(f"case wide vs narrow m={m} k={k}", flush=True)
+    r = rng(7000 + m + k)
+    n = 2048
+    codes, scales, biases = random_q4(r, n, k)
+    x = bf16(r.normal(0, 1, (m, k)))
+    W = E.DeviceQ4(codes, scales, biases)
+    halves = [E.DeviceQ4(codes[h * 1024:(h + 1) * 1024], scales[h * 1024:(h + 1) * 1024],
+                         biases[h * 1024:(h + 1) * 1024]) for h in range(2)]
+    dx = E.DeviceBuffer.from_numpy(x)
+    dy = E.DeviceBuffer(m * n * 2)
+    dh = [E.DeviceBuffer(m * 1024 * 2) for _ in range(2)]
+    E.check(E.lib().es_q4_gemm(W.struct, dx.ptr, m, None, dy.ptr, None))
+    for h in range(2):
+        E.check(E.lib().es_q4_gemm(halves[h].struct, dx.ptr, m, None, dh[h].ptr, None))
+    E.synchronize()
+    full = dy.numpy(np.uint16).reshape(m, n)
+    for h in range(2):
+        assert np.array_equal(full[:, h * 1024:(h + 1) * 1024], dh[h].numpy(np.uint16).reshape(m, 1024))
 
 
 def test_q4_gemm_rejects_bad_arguments():
