@@ -867,31 +867,51 @@ __global__ __launch_bounds__(256) void k_attn_gate_rows(const uint16_t* o, const
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 constexpr int kFaQ = 32, kFaStages = 4, kFaKs = 264, kFaVs = 272;
 constexpr int kFaStageHalves = 32 * kFaKs + 32 * kFaVs;
-// eight transposing reads at a + 32*i bytes (i = 0..7: eight 16-dim tiles),
-// then their wait
-__device__ __forceinline__ void lds_read_tr16_x8(uint32_t a, uint2 (&r)[8]) {
-  uint64_t x0, x1, x2, x3, x4, x5, x6, x7;
+// sixteen transposing reads: eight at a + 32*i and eight at b + 32*i. At most
+// 15 LDS operations are in flight (the width of lgkmcnt): the last read of b
+// is issued once the eight reads of a have landed. Every read completes
+// before the statement ends.
+__device__ __forceinline__ void lds_read_tr16_x16(uint32_t a, uint32_t b, uint2 (&ra)[8], uint2 (&rb)[8]) {
+  uint64_t x0, x1, x2, x3, x4, x5, x6, x7, y0, y1, y2, y3, y4, y5, y6, y7;
   asm volatile(
-      "ds_read_b64_tr_b16 %0, %8\n\t"
-      "ds_read_b64_tr_b16 %1, %8 offset:32\n\t"
-      "ds_read_b64_tr_b16 %2, %8 offset:64\n\t"
-      "ds_read_b64_tr_b16 %3, %8 offset:96\n\t"
-      "ds_read_b64_tr_b16 %4, %8 offset:128\n\t"
-      "ds_read_b64_tr_b16 %5, %8 offset:160\n\t"
-      "ds_read_b64_tr_b16 %6, %8 offset:192\n\t"
-      "ds_read_b64_tr_b16 %7, %8 offset:224\n\t"
+      "ds_read_b64_tr_b16 %0, %16\n\t"
+      "ds_read_b64_tr_b16 %1, %16 offset:32\n\t"
+      "ds_read_b64_tr_b16 %2, %16 offset:64\n\t"
+      "ds_read_b64_tr_b16 %3, %16 offset:96\n\t"
+      "ds_read_b64_tr_b16 %4, %16 offset:128\n\t"
+      "ds_read_b64_tr_b16 %5, %16 offset:160\n\t"
+      "ds_read_b64_tr_b16 %6, %16 offset:192\n\t"
+      "ds_read_b64_tr_b16 %7, %16 offset:224\n\t"
+      "ds_read_b64_tr_b16 %8, %17\n\t"
+      "ds_read_b64_tr_b16 %9, %17 offset:32\n\t"
+      "ds_read_b64_tr_b16 %10, %17 offset:64\n\t"
+      "ds_read_b64_tr_b16 %11, %17 offset:96\n\t"
+      "ds_read_b64_tr_b16 %12, %17 offset:128\n\t"
+      "ds_read_b64_tr_b16 %13, %17 offset:160\n\t"
+      "ds_read_b64_tr_b16 %14, %17 offset:192\n\t"
+      "s_waitcnt lgkmcnt(7)\n\t"
+      "ds_read_b64_tr_b16 %15, %17 offset:224\n\t"
       "s_waitcnt lgkmcnt(0)"
-      : "=&v"(x0), "=&v"(x1), "=&v"(x2), "=&v"(x3), "=&v"(x4), "=&v"(x5), "=&v"(x6), "=&v"(x7)
-      : "v"(a)
+      : "=&v"(x0), "=&v"(x1), "=&v"(x2), "=&v"(x3), "=&v"(x4), "=&v"(x5), "=&v"(x6), "=&v"(x7),
+        "=&v"(y0), "=&v"(y1), "=&v"(y2), "=&v"(y3), "=&v"(y4), "=&v"(y5), "=&v"(y6), "=&v"(y7)
+      : "v"(a), "v"(b)
       : "memory");
-  r[0] = __builtin_bit_cast(uint2, x0);
-  r[1] = __builtin_bit_cast(uint2, x1);
-  r[2] = __builtin_bit_cast(uint2, x2);
-  r[3] = __builtin_bit_cast(uint2, x3);
-  r[4] = __builtin_bit_cast(uint2, x4);
-  r[5] = __builtin_bit_cast(uint2, x5);
-  r[6] = __builtin_bit_cast(uint2, x6);
-  r[7] = __builtin_bit_cast(uint2, x7);
+  ra[0] = __builtin_bit_cast(uint2, x0);
+  ra[1] = __builtin_bit_cast(uint2, x1);
+  ra[2] = __builtin_bit_cast(uint2, x2);
+  ra[3] = __builtin_bit_cast(uint2, x3);
+  ra[4] = __builtin_bit_cast(uint2, x4);
+  ra[5] = __builtin_bit_cast(uint2, x5);
+  ra[6] = __builtin_bit_cast(uint2, x6);
+  ra[7] = __builtin_bit_cast(uint2, x7);
+  rb[0] = __builtin_bit_cast(uint2, y0);
+  rb[1] = __builtin_bit_cast(uint2, y1);
+  rb[2] = __builtin_bit_cast(uint2, y2);
+  rb[3] = __builtin_bit_cast(uint2, y3);
+  rb[4] = __builtin_bit_cast(uint2, y4);
+  rb[5] = __builtin_bit_cast(uint2, y5);
+  rb[6] = __builtin_bit_cast(uint2, y6);
+  rb[7] = __builtin_bit_cast(uint2, y7);
 }
 __global__ __launch_bounds__(512, 1) void k_attn_prefill(const uint16_t* qr, const uint16_t* kcache,
                                                          const uint16_t* vcache, int pos0, int m,
@@ -970,15 +990,31 @@ __global__ __launch_bounds__(512, 1) void k_attn_prefill(const uint16_t* qr, con
     const uint16_t* ks = kv[kb % kFaStages];
     const uint32_t vs_addr = kv_base + (uint32_t)(2 * kFaStageHalves * (kb % kFaStages)) + v_lane;
     // scores S^T[key][q] for the two 16-key tiles of this block
+    // The K fragments of k-steps s2 .. s2 + 3 are in flight while step s2's
+    // two products run (fences keep the order), so each pair of products
+    // waits for its own reads only.
     f32x4 st[2];
+    {
+      bf16x8 kf[2][8];
+      auto read_k = [&](int s2) {
 #pragma unroll
-    for (int kt = 0; kt < 2; ++kt) {
+        for (int kt = 0; kt < 2; ++kt)
+          kf[kt][s2] = *reinterpret_cast<const bf16x8*>(ks + (16 * kt + qi) * kFaKs + 32 * s2 + 8 * g);
+      };
 #pragma unroll
-      for (int r = 0; r < 4; ++r) st[kt][r] = 0.0f;
+      for (int s2 = 0; s2 < 4; ++s2) read_k(s2);
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) st[kt][r] = 0.0f;
 #pragma unroll
       for (int s2 = 0; s2 < 8; ++s2) {
-        const bf16x8 kf = *reinterpret_cast<const bf16x8*>(ks + (16 * kt + qi) * kFaKs + 32 * s2 + 8 * g);
-        st[kt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf, qf[s2], st[kt], 0, 0, 0);
+#pragma unroll
+        for (int kt = 0; kt < 2; ++kt)
+          st[kt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf[kt][s2], qf[s2], st[kt], 0, 0, 0);
+        if (s2 + 4 < 8) read_k(s2 + 4);
+        __builtin_amdgcn_sched_barrier(0);
       }
     }
     float x[8];
@@ -1036,8 +1072,7 @@ __global__ __launch_bounds__(512, 1) void k_attn_prefill(const uint16_t* qr, con
 #pragma unroll
     for (int d8 = 0; d8 < 2; ++d8) {
       uint2 lo[8], hi[8];
-      lds_read_tr16_x8(a_lo + 256 * d8, lo);
-      lds_read_tr16_x8(a_hi + 256 * d8, hi);
+      lds_read_tr16_x16(a_lo + 256 * d8, a_hi + 256 * d8, lo, hi);
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
         const int dt = 8 * d8 + i;
