@@ -986,7 +986,6 @@ __global__ __launch_bounds__(512, 1) void k_attn_prefill(const uint16_t* qr, con
     else
       wait_vmcnt<0>();
     __syncthreads();  // block kb visible; every wave is past block kb-1
-    if (kb + kFaStages - 1 < nkb) issue(kb + kFaStages - 1);
     const uint16_t* ks = kv[kb % kFaStages];
     const uint32_t vs_addr = kv_base + (uint32_t)(2 * kFaStageHalves * (kb % kFaStages)) + v_lane;
     // scores S^T[key][q] for the two 16-key tiles of this block
@@ -1003,6 +1002,9 @@ __global__ __launch_bounds__(512, 1) void k_attn_prefill(const uint16_t* qr, con
       };
 #pragma unroll
       for (int s2 = 0; s2 < 4; ++s2) read_k(s2);
+      // block kb + 3 goes to the stage every wave finished before the barrier;
+      // its DMA is issued while the first K reads are in flight
+      if (kb + kFaStages - 1 < nkb) issue(kb + kFaStages - 1);
       __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
       for (int kt = 0; kt < 2; ++kt)
