@@ -37,9 +37,8 @@ struct GemmStage {
   uint32_t s, b; // that row's scale and bias (bf16)
 };
 
-__device__ __forceinline__ uint32_t pack2(float lo, float hi) {
-  return (uint32_t)f2bf(lo) | ((uint32_t)f2bf(hi) << 16);
-}
+// Two values -> packed bf16 pair (lo in bits 0..15), one v_cvt_pk_bf16_f32.
+__device__ __forceinline__ uint32_t pack2(float lo, float hi) { return pack_bf2(lo, hi); }
 
 // GATEUP: w is the gate matrix and w2 the up matrix of the MLP; the block's
 // 128 staged W rows are gate rows n0 + 0..31, up rows n0 + 0..31, gate rows
@@ -867,34 +866,37 @@ __global__ __launch_bounds__(256) void k_attn_gate_rows(const uint16_t* o, const
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 constexpr int kFaQ = 32, kFaStages = 4, kFaKs = 264, kFaVs = 272;
 constexpr int kFaStageHalves = 32 * kFaKs + 32 * kFaVs;
-// sixteen transposing reads: eight at a + 32*i and eight at b + 32*i. At most
-// 15 LDS operations are in flight (the width of lgkmcnt): the last read of b
-// is issued once the eight reads of a have landed. Every read completes
-// before the statement ends.
-__device__ __forceinline__ void lds_read_tr16_x16(uint32_t a, uint32_t b, uint2 (&ra)[8], uint2 (&rb)[8]) {
+// sixteen transposing reads from one base: eight at OFF + 32*i (keys 4g..)
+// and eight at kFaHi + OFF + 32*i (keys 16 + 4g..). At most 15 LDS operations
+// are in flight (the width of lgkmcnt): the last read of the second set is
+// issued once the first eight have landed. Every read completes before the
+// statement ends.
+constexpr int kFaHi = 2 * 16 * kFaVs;  // bytes from key row 4g to key row 16 + 4g
+template <int OFF>
+__device__ __forceinline__ void lds_read_tr16_x16(uint32_t a, uint2 (&ra)[8], uint2 (&rb)[8]) {
   uint64_t x0, x1, x2, x3, x4, x5, x6, x7, y0, y1, y2, y3, y4, y5, y6, y7;
   asm volatile(
-      "ds_read_b64_tr_b16 %0, %16\n\t"
-      "ds_read_b64_tr_b16 %1, %16 offset:32\n\t"
-      "ds_read_b64_tr_b16 %2, %16 offset:64\n\t"
-      "ds_read_b64_tr_b16 %3, %16 offset:96\n\t"
-      "ds_read_b64_tr_b16 %4, %16 offset:128\n\t"
-      "ds_read_b64_tr_b16 %5, %16 offset:160\n\t"
-      "ds_read_b64_tr_b16 %6, %16 offset:192\n\t"
-      "ds_read_b64_tr_b16 %7, %16 offset:224\n\t"
-      "ds_read_b64_tr_b16 %8, %17\n\t"
-      "ds_read_b64_tr_b16 %9, %17 offset:32\n\t"
-      "ds_read_b64_tr_b16 %10, %17 offset:64\n\t"
-      "ds_read_b64_tr_b16 %11, %17 offset:96\n\t"
-      "ds_read_b64_tr_b16 %12, %17 offset:128\n\t"
-      "ds_read_b64_tr_b16 %13, %17 offset:160\n\t"
-      "ds_read_b64_tr_b16 %14, %17 offset:192\n\t"
+      "ds_read_b64_tr_b16 %0, %16 offset:%17\n\t"
+      "ds_read_b64_tr_b16 %1, %16 offset:%17+32\n\t"
+      "ds_read_b64_tr_b16 %2, %16 offset:%17+64\n\t"
+      "ds_read_b64_tr_b16 %3, %16 offset:%17+96\n\t"
+      "ds_read_b64_tr_b16 %4, %16 offset:%17+128\n\t"
+      "ds_read_b64_tr_b16 %5, %16 offset:%17+160\n\t"
+      "ds_read_b64_tr_b16 %6, %16 offset:%17+192\n\t"
+      "ds_read_b64_tr_b16 %7, %16 offset:%17+224\n\t"
+      "ds_read_b64_tr_b16 %8, %16 offset:%18\n\t"
+      "ds_read_b64_tr_b16 %9, %16 offset:%18+32\n\t"
+      "ds_read_b64_tr_b16 %10, %16 offset:%18+64\n\t"
+      "ds_read_b64_tr_b16 %11, %16 offset:%18+96\n\t"
+      "ds_read_b64_tr_b16 %12, %16 offset:%18+128\n\t"
+      "ds_read_b64_tr_b16 %13, %16 offset:%18+160\n\t"
+      "ds_read_b64_tr_b16 %14, %16 offset:%18+192\n\t"
       "s_waitcnt lgkmcnt(7)\n\t"
-      "ds_read_b64_tr_b16 %15, %17 offset:224\n\t"
+      "ds_read_b64_tr_b16 %15, %16 offset:%18+224\n\t"
       "s_waitcnt lgkmcnt(0)"
       : "=&v"(x0), "=&v"(x1), "=&v"(x2), "=&v"(x3), "=&v"(x4), "=&v"(x5), "=&v"(x6), "=&v"(x7),
         "=&v"(y0), "=&v"(y1), "=&v"(y2), "=&v"(y3), "=&v"(y4), "=&v"(y5), "=&v"(y6), "=&v"(y7)
-      : "v"(a), "v"(b)
+      : "v"(a), "n"(OFF), "n"(kFaHi + OFF)
       : "memory");
   ra[0] = __builtin_bit_cast(uint2, x0);
   ra[1] = __builtin_bit_cast(uint2, x1);
@@ -912,6 +914,13 @@ __device__ __forceinline__ void lds_read_tr16_x16(uint32_t a, uint32_t b, uint2 
   rb[5] = __builtin_bit_cast(uint2, y5);
   rb[6] = __builtin_bit_cast(uint2, y6);
   rb[7] = __builtin_bit_cast(uint2, y7);
+}
+// max of two scores by v_max_f32 alone: scores are never NaN, so the operand
+// canonicalisation that fmaxf adds changes nothing and is left out
+__device__ __forceinline__ float max_raw(float a, float b) {
+  float r;
+  asm("v_max_f32 %0, %1, %2" : "=v"(r) : "v"(a), "v"(b));
+  return r;
 }
 __global__ __launch_bounds__(512, 1) void k_attn_prefill(const uint16_t* qr, const uint16_t* kcache,
                                                          const uint16_t* vcache, int pos0, int m,
@@ -1038,22 +1047,22 @@ __global__ __launch_bounds__(512, 1) void k_attn_prefill(const uint16_t* qr, con
 #pragma unroll
     for (int e = 1; e < 8; ++e) mloc = fmaxf(mloc, x[e]);
     const float2 m16 = rows_xor16(mloc);
-    const float2 m32 = rows_xor32(fmaxf(m16.x, m16.y));
+    const float2 m32 = rows_xor32(max_raw(m16.x, m16.y));
     // The exponent's reference value moves only when the block's maximum
     // exceeds it by more than 8 (probabilities stay below 2^8; the output is
     // normalised by a sum taken against the same reference, so the softmax is
     // unchanged). The choice is per row, so a row's result depends on its own
     // scores only.
-    const float mblk = fmaxf(m32.x, m32.y) * c;
+    const float mblk = max_raw(m32.x, m32.y) * c;
     const float mnew = mblk > mrun + 8.0f ? mblk : mrun;
     const float factor = __builtin_amdgcn_exp2f(mrun - mnew);
-    float psum = 0.0f;
     float pv[8];
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      pv[e] = __builtin_amdgcn_exp2f(fmaf(x[e], c, -mnew));
-      psum += pv[e];
-    }
+    for (int e = 0; e < 8; ++e) pv[e] = __builtin_amdgcn_exp2f(fmaf(x[e], c, -mnew));
+    // ((p0 + p1) + p2) + ...: the same sum as from 0, since p0 >= +0
+    float psum = pv[0];
+#pragma unroll
+    for (int e = 1; e < 8; ++e) psum += pv[e];
     const float2 s16 = rows_xor16(psum);
     const float2 s32 = rows_xor32(s16.x + s16.y);
     lrun = lrun * factor + (s32.x + s32.y);
@@ -1070,11 +1079,13 @@ __global__ __launch_bounds__(512, 1) void k_attn_prefill(const uint16_t* qr, con
     // O^T += V^T . P^T: one 32-key step per 16-dim tile
     const u32x4 pb = u32x4{pack2(pv[0], pv[1]), pack2(pv[2], pv[3]), pack2(pv[4], pv[5]), pack2(pv[6], pv[7])};
     const bf16x8 pf = __builtin_bit_cast(bf16x8, pb);
-    const uint32_t a_lo = vs_addr, a_hi = vs_addr + 2 * 16 * kFaVs;  // keys 4g.. and 16 + 4g..
 #pragma unroll
     for (int d8 = 0; d8 < 2; ++d8) {
       uint2 lo[8], hi[8];
-      lds_read_tr16_x16(a_lo + 256 * d8, a_hi + 256 * d8, lo, hi);
+      if (d8 == 0)
+        lds_read_tr16_x16<0>(vs_addr, lo, hi);
+      else
+        lds_read_tr16_x16<256>(vs_addr, lo, hi);
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
         const int dt = 8 * d8 + i;
