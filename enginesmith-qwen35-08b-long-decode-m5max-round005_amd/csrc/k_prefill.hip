@@ -40,6 +40,26 @@ struct GemmStage {
 // Two values -> packed bf16 pair (lo in bits 0..15), one v_cvt_pk_bf16_f32.
 __device__ __forceinline__ uint32_t pack2(float lo, float hi) { return pack_bf2(lo, hi); }
 
+// The 8 nibbles of one code word (element j = bits 4j..4j+3) as
+// fma(scale, q, bias), packed to four bf16 pairs. The even nibbles are the
+// bytes of word & 0x0F0F0F0F and the odd ones the bytes of
+// (word >> 4) & 0x0F0F0F0F, so each converts with one v_cvt_f32_ubyteN (the
+// masked words are hidden from known-bits analysis, which would otherwise
+// extract every nibble separately).
+__device__ __forceinline__ u32x4 dequant8(uint32_t word, float sc, float bi) {
+  uint32_t lo = word & 0x0F0F0F0Fu;
+  uint32_t hi = (word >> 4) & 0x0F0F0F0Fu;
+  asm("" : "+v"(lo));
+  asm("" : "+v"(hi));
+  float v[8];
+#pragma unroll
+  for (int b = 0; b < 4; ++b) {
+    v[2 * b] = fmaf(sc, (float)((lo >> (8 * b)) & 0xffu), bi);
+    v[2 * b + 1] = fmaf(sc, (float)((hi >> (8 * b)) & 0xffu), bi);
+  }
+  return u32x4{pack2(v[0], v[1]), pack2(v[2], v[3]), pack2(v[4], v[5]), pack2(v[6], v[7])};
+}
+
 // GATEUP: w is the gate matrix and w2 the up matrix of the MLP; the block's
 // 128 staged W rows are gate rows n0 + 0..31, up rows n0 + 0..31, gate rows
 // n0 + 32..63, up rows n0 + 32..63, so each wave holds a gate and an up
@@ -82,11 +102,7 @@ __global__ __launch_bounds__(256) void k_q4_gemm(Q4 w, Q4 w2, const uint16_t* __
     u32x4 o[4];
 #pragma unroll
     for (int wd = 0; wd < 4; ++wd) {
-      const uint32_t c = g.c[wd];
-      float v[8];
-#pragma unroll
-      for (int j = 0; j < 8; ++j) v[j] = fmaf(sc, (float)((c >> (4 * j)) & 15u), bi);
-      o[wd] = u32x4{pack2(v[0], v[1]), pack2(v[2], v[3]), pack2(v[4], v[5]), pack2(v[6], v[7])};
+      o[wd] = dequant8(g.c[wd], sc, bi);
     }
     u32x4* wd4 = reinterpret_cast<u32x4*>(&ws[buf][lr][lh * 32]);
 #pragma unroll
@@ -320,11 +336,7 @@ __global__ __launch_bounds__(256, 1) void k_q4_gemm_wide(WideGemmArgs a) {
     const float sc = wok ? bf2f(r.s) : 0.0f, bi = wok ? bf2f(r.b) : 0.0f;
 #pragma unroll
     for (int c = 0; c < 8; ++c) {
-      const uint32_t word = c < 4 ? r.c0[c] : r.c1[c - 4];
-      float v[8];
-#pragma unroll
-      for (int j = 0; j < 8; ++j) v[j] = fmaf(sc, (float)((word >> (4 * j)) & 15u), bi);
-      const u32x4 o{pack2(v[0], v[1]), pack2(v[2], v[3]), pack2(v[4], v[5]), pack2(v[6], v[7])};
+      const u32x4 o = dequant8(c < 4 ? r.c0[c] : r.c1[c - 4], sc, bi);
       asm volatile("ds_write_b128 %0, %1" ::"v"(wt + (uint32_t)(wide_slot(t, c) * 2)), "v"(o));
     }
   };
