@@ -966,6 +966,15 @@ __global__ __launch_bounds__(512, 1) void k_attn_prefill(const uint16_t* qr, con
   }
   // DMA of one block of 32 keys: wave w moves rows 4w .. 4w+3 of K and V,
   // one row per instruction, lane L < 32 the row's 16-byte chunk L
+  // Buffer resources over this KV head's rows of both caches: the row's byte
+  // offset is a scalar operand and the lane's 16-byte chunk a fixed vector
+  // offset, so a DMA takes no per-lane address arithmetic. Rows are clamped
+  // to the capacity below, which the launcher keeps at most 2^22 (byte
+  // offsets up to 2^31), so the resources set no range of their own.
+  const size_t head_off = (size_t)kvh * capacity * 256;
+  const __amdgpu_buffer_rsrc_t krs = __builtin_amdgcn_make_buffer_rsrc((void*)(kcache + head_off), 0, -1, 0x00020000);
+  const __amdgpu_buffer_rsrc_t vrs = __builtin_amdgcn_make_buffer_rsrc((void*)(vcache + head_off), 0, -1, 0x00020000);
+  const uint32_t lane_off = (uint32_t)lane * 16u;
   auto issue = [&](int kb) {
     uint16_t* stage = kv[kb % kFaStages];
     if (lane < 32) {
@@ -973,12 +982,11 @@ __global__ __launch_bounds__(512, 1) void k_attn_prefill(const uint16_t* qr, con
       for (int i = 0; i < 4; ++i) {
         const int r = 4 * wave + i;
         const int key = min(kb * 32 + r, capacity - 1);
-        const size_t row = ((size_t)kvh * capacity + key) * 256;  // uniform
-        __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)(kcache + row + lane * 8),
-                                         (__attribute__((address_space(3))) void*)(stage + r * kFaKs), 16, 0, 0);
-        __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)(vcache + row + lane * 8),
-                                         (__attribute__((address_space(3))) void*)(stage + 32 * kFaKs + r * kFaVs),
-                                         16, 0, 0);
+        const uint32_t row = (uint32_t)key * 512u;  // uniform byte offset
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(krs, (__attribute__((address_space(3))) void*)(stage + r * kFaKs), 16,
+                                             lane_off, row, 0, 0);
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(vrs, (__attribute__((address_space(3))) void*)(stage + 32 * kFaKs + r * kFaVs),
+                                             16, lane_off, row, 0, 0);
       }
     }
   };
@@ -1272,7 +1280,10 @@ hipError_t launch_attn_prep_rows(const AttnPrepRowsArgs& a, hipStream_t s) {
 
 hipError_t launch_attn_prefill(const uint16_t* qr, const uint16_t* kcache, const uint16_t* vcache, int pos0,
                                int m, int capacity, uint16_t* o, hipStream_t s) {
-  if (!qr || !kcache || !vcache || !o || m < 1 || pos0 < 0 || pos0 + m > capacity) return hipErrorInvalidValue;
+  // capacity <= 2^22 (the engine's limit) keeps every byte offset within a KV
+  // head's rows below 2^31
+  if (!qr || !kcache || !vcache || !o || m < 1 || pos0 < 0 || pos0 + m > capacity || capacity > (1 << 22))
+    return hipErrorInvalidValue;
   const int tiles = (m + kFaQ - 1) / kFaQ;
   hipLaunchKernelGGL(k_attn_prefill, dim3(8 * ((tiles + 3) / 4)), dim3(512), 0, s, qr, kcache, vcache, pos0, m,
                      capacity, o);

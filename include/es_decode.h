@@ -211,7 +211,8 @@ int es_attn_prepare_rows(const uint16_t* q_proj, const uint16_t* k_proj, const u
 /* attn_prefill (attention_prefill.metal:2256; model.rs:337-343): causal GQA
  * attention, row r attends to cache positions 0 .. position+r; out
  * [rows, 8, 256] = bf16(softmax(q.K^T / 16) V), fp32 softmax, products on
- * bf16 operands (the probabilities rounded to bf16) with fp32 accumulation. */
+ * bf16 operands (the probabilities rounded to bf16) with fp32 accumulation.
+ * capacity is at most 2^22 rows. */
 int es_attn_prefill(const uint16_t* query, const uint16_t* kcache, const uint16_t* vcache, int position, int rows,
                     int capacity, uint16_t* out, void* stream);
 

@@ -245,6 +245,8 @@ def test_row_ops_reject_bad_arguments():
     assert L.es_rmsnorm_rows(b.ptr, b.ptr, 0, b.ptr, None) != E.ES_OK
     assert L.es_attn_prefill(b.ptr, b.ptr, b.ptr, 10, 8, 16, b.ptr, None) != E.ES_OK
     assert L.es_attn_prefill(b.ptr, b.ptr, b.ptr, -1, 1, 16, b.ptr, None) != E.ES_OK
+    # a KV head's rows are addressed by 32-bit byte offsets: capacity at most 2^22
+    assert L.es_attn_prefill(b.ptr, b.ptr, b.ptr, 0, 1, (1 << 22) + 1, b.ptr, None) != E.ES_OK
     assert L.es_attn_prepare_rows(b.ptr, b.ptr, b.ptr, b.ptr, b.ptr, b.ptr, 9, 8, b.ptr, b.ptr, b.ptr, 16,
                                   None) != E.ES_OK
     assert L.es_gdn_recur_rows(b.ptr, b.ptr, b.ptr, b.ptr, b.ptr, 0, b.ptr, b.ptr, None) != E.ES_OK
