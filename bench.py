@@ -160,7 +160,8 @@ def main():
     ap.add_argument("--steps", type=int, default=64)
     ap.add_argument("--warmup", type=int, default=8)
     ap.add_argument("--contexts", default="32768,65536,131072")
-    ap.add_argument("--cpu-steps", type=int, default=4)
+    ap.add_argument("--cpu-steps", type=int, default=16,
+                    help="oracle steps per context (timed, and judged for token agreement)")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--attn-reps", type=int, default=20)
     ap.add_argument("--copy-calibration", action="store_true",
@@ -203,7 +204,7 @@ def main():
             # host cores (the GPU is idle meanwhile); at the headline context
             # one more step on a single thread
             head = ctx == max(contexts)
-            n_cpu = args.cpu_steps if head else max(1, args.cpu_steps // 2)
+            n_cpu = args.cpu_steps
             orc = oracle_from_gpu_state(eng, blob, eng.position, n_cpu + 4)
             stream = eng.generate([], n_cpu + (1 if head else 0), reset=False)
             sec, mism = cpu_decode_sample(orc, first, stream[:n_cpu], threads)
@@ -255,8 +256,8 @@ def main():
         iso = cpu_isolated(E.tensor_views(blob, N_LAYERS, VOCAB), contexts)
         cpu = dict(value=cpu_ctx[head_ctx], unit="tok/s", cores=threads, kind="port",
                    sample=f"oracle decode steps of the 24-layer model from the GPU's post-prefill state "
-                          f"({args.cpu_steps} at {head_ctx}, {max(1, args.cpu_steps // 2)} at each other "
-                          f"context), {threads} OpenMP threads; isolated pieces median of 3",
+                          f"({args.cpu_steps} at each context, replaying the GPU's greedy tokens), "
+                          f"{threads} OpenMP threads; isolated pieces median of 3",
                    threads=threads, host_cores=host_cores, per_context={str(k): v for k, v in cpu_ctx.items()},
                    single_thread=single, isolated=iso)
 

@@ -87,14 +87,15 @@ int es_copy_d2d(void* dst, const void* src, size_t bytes, void* stream) {
   return hip_status(es::launch_copy16(dst, src, bytes, S(stream)), "es_copy_d2d");
 }
 int es_time_read(const void* src, size_t bytes, void* out, size_t out_bytes, int reps, double* ms_avg) {
-  if (!ms_avg || !src || !out || reps <= 0 || bytes == 0 || bytes % 16 != 0 || out_bytes < es::read16_out_bytes())
+  if (!ms_avg || !src || !out || reps <= 0 || bytes == 0 || bytes % es::read_granule() != 0 ||
+      out_bytes < es::read_out_bytes())
     return fail(ES_ERR_INVALID, "es_time_read: bad arguments");
   hipEvent_t e0, e1;
   if (int rc = hip_status(hipEventCreate(&e0), "hipEventCreate")) return rc;
   if (int rc = hip_status(hipEventCreate(&e1), "hipEventCreate")) return rc;
-  int rc = hip_status(es::launch_read16(src, bytes, out, nullptr), "read warmup");
+  int rc = hip_status(es::launch_read(src, bytes, out, nullptr), "read warmup");
   if (!rc) rc = hip_status(hipEventRecord(e0, nullptr), "hipEventRecord");
-  for (int i = 0; i < reps && !rc; ++i) rc = hip_status(es::launch_read16(src, bytes, out, nullptr), "read");
+  for (int i = 0; i < reps && !rc; ++i) rc = hip_status(es::launch_read(src, bytes, out, nullptr), "read");
   if (!rc) rc = hip_status(hipEventRecord(e1, nullptr), "hipEventRecord");
   if (!rc) rc = hip_status(hipEventSynchronize(e1), "hipEventSynchronize");
   float ms = 0.0f;
@@ -558,6 +559,12 @@ int es_engine_set_xcd_kernels(es_engine* e, int on) {
   if (!e || !e->impl) return fail(ES_ERR_INVALID, "null engine");
   std::string err;
   return engine_rc(e->impl->set_xcd_kernels(on != 0, &err), err);
+}
+
+int es_engine_inject_exchange_fault(es_engine* e, int mode) {
+  if (!e || !e->impl) return fail(ES_ERR_INVALID, "null engine");
+  std::string err;
+  return engine_rc(e->impl->inject_exchange_fault(mode, &err), err);
 }
 
 int es_engine_prompt_split(const es_engine* e, int* chunks, int* routed_rows, int* decode_rows) {

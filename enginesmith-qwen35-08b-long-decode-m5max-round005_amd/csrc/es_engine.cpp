@@ -190,15 +190,7 @@ int Engine::init(const void* blob, uint64_t bytes, std::string* err) {
       ES_HIP(hipMemsetAsync(L.vcache, 0, cache, stream_), "memset kv");
     }
   reset_state();
-  // Placement probe for the XCD-cooperative kernels: the blocks of a
-  // 256-block launch must be dealt to the 8 XCDs in turn (from any start),
-  // 32 to each (err_ doubles as the probe's output)
-  ES_HIP(launch_xcc_probe(err_, stream_), "placement probe");
-  uint32_t xcc[256];
-  ES_HIP(hipMemcpyAsync(xcc, err_, sizeof(xcc), hipMemcpyDeviceToHost, stream_), "placement probe");
-  ES_HIP(hipStreamSynchronize(stream_), "init sync");
-  xcd_ok_ = xcc[0] < 8;
-  for (int b = 0; b < 256; ++b) xcd_ok_ = xcd_ok_ && xcc[b] == (xcc[0] + (uint32_t)b) % 8;
+  if (int rc = probe_placement(&xcd_ok_, err)) return rc;
   fused_mlp_ = xcd_ok_;
   for (auto& L : layers_) {
     if (!L.attention) continue;
@@ -237,27 +229,80 @@ int Engine::init(const void* blob, uint64_t bytes, std::string* err) {
       ES_HIP(launch_pack_out_pairs(L.out.s, L.out.b, L.out_sb, stream_), "pack");
     }
   }
-  ES_HIP(hipMemsetAsync(err_, 0, 256 * sizeof(uint32_t), stream_), "memset");
-  ES_HIP(hipMemsetAsync(xflags_, 0, 8 * 32 * sizeof(uint32_t), stream_), "memset");
-  // tag 0 on every exchange word: the first tag a launch waits for is 1
-  ES_HIP(hipMemsetAsync(xact_, 0, 8 * 512 * 4, stream_), "memset");
-  ES_HIP(hipMemsetAsync(xgdn_, 0, 8 * 2 * 648 * 4, stream_), "memset");
-  ES_HIP(hipStreamSynchronize(stream_), "init sync");
+  return clear_exchanges(err);
+}
+
+// Placement probe for the XCD-cooperative kernels: the blocks of a 256-block
+// launch must be dealt to the 8 XCDs in turn (from any start), 32 to each
+// (err_ doubles as the probe's output; clear_exchanges clears it after).
+int Engine::probe_placement(bool* ok, std::string* err) {
+  ES_HIP(launch_xcc_probe(err_, stream_), "placement probe");
+  uint32_t xcc[256];
+  ES_HIP(hipMemcpyAsync(xcc, err_, sizeof(xcc), hipMemcpyDeviceToHost, stream_), "placement probe");
+  ES_HIP(hipStreamSynchronize(stream_), "placement probe");
+  bool good = xcc[0] < 8;
+  for (int b = 0; b < 256; ++b) good = good && xcc[b] == (xcc[0] + (uint32_t)b) % 8;
+  *ok = good;
   return 0;
 }
 
-// The cooperative kernels report an exhausted exchange wait in err_; the
-// step's results are then not to be trusted.
+// The error word, the per-block exchange counts and every exchange word back
+// to zero (tag 0 on every word: the first tag a launch waits for is 1).
+int Engine::clear_exchanges(std::string* err) {
+  ES_HIP(hipMemsetAsync(err_, 0, 256 * sizeof(uint32_t), stream_), "memset");
+  ES_HIP(hipMemsetAsync(xflags_, 0, 8 * 32 * sizeof(uint32_t), stream_), "memset");
+  ES_HIP(hipMemsetAsync(xact_, 0, 8 * 512 * 4, stream_), "memset");
+  ES_HIP(hipMemsetAsync(xgdn_, 0, 8 * 2 * 648 * 4, stream_), "memset");
+  ES_HIP(hipStreamSynchronize(stream_), "exchange clear");
+  return 0;
+}
+
+// The cooperative kernels report an exhausted exchange wait in err_ (every
+// later wait then gives up at once); the batch's results are not to be
+// trusted. The exchange state is cleared so the next request starts afresh,
+// and the placement probe runs again: if the blocks are no longer dealt to
+// the XCDs in turn, later steps run on one launch per dependency.
 int Engine::check_device_error(std::string* err) {
   if (!fused_mlp_) return 0;
   uint32_t e = 0;
   ES_HIP(hipMemcpyAsync(&e, err_, sizeof(e), hipMemcpyDeviceToHost, stream_), "error word");
   ES_HIP(hipStreamSynchronize(stream_), "error word");
   if (e == 0) return 0;
-  ES_HIP(hipMemsetAsync(err_, 0, sizeof(uint32_t), stream_), "error word");
-  ES_HIP(hipStreamSynchronize(stream_), "error word");
+  bool ok = false;
+  if (int rc = probe_placement(&ok, err)) return rc;
+  if (int rc = clear_exchanges(err)) return rc;
+  if (!ok) {
+    std::string ignored;
+    (void)set_xcd_kernels(false, &ignored);
+    xcd_ok_ = false;
+  }
   if (err) *err = "decode kernels: an XCD exchange wait timed out";
   return 2;
+}
+
+// Test hook: mode 1 sets the error word (every wait of the next launches
+// gives up at once); mode 2 moves block 0's exchange count away from its
+// XCD's, so the waits on its words run to their spin limit.
+int Engine::inject_exchange_fault(int mode, std::string* err) {
+  if (!fused_mlp_) {
+    if (err) *err = "the XCD-cooperative kernels are off";
+    return 1;
+  }
+  if (mode == 1) {
+    const uint32_t v = 2u;
+    ES_HIP(hipMemcpyAsync(err_, &v, sizeof(v), hipMemcpyHostToDevice, stream_), "fault");
+  } else if (mode == 2) {
+    uint32_t c = 0;
+    ES_HIP(hipMemcpyAsync(&c, xflags_, sizeof(c), hipMemcpyDeviceToHost, stream_), "fault");
+    ES_HIP(hipStreamSynchronize(stream_), "fault");
+    c += 0x8000u;
+    ES_HIP(hipMemcpyAsync(xflags_, &c, sizeof(c), hipMemcpyHostToDevice, stream_), "fault");
+  } else {
+    if (err) *err = "fault mode must be 1 or 2";
+    return 1;
+  }
+  ES_HIP(hipStreamSynchronize(stream_), "fault");
+  return 0;
 }
 
 // model.rs:93-96: position 0, no pending token, zeroed GDN history and state.

@@ -101,6 +101,9 @@ class Engine {
   // Decode steps on the XCD-cooperative kernels (on, when the start-up probe
   // allowed them) or on one launch per dependency; both give the same bits.
   int set_xcd_kernels(bool on, std::string* err);
+  // Test hook for the exchange failure path (1: set the error word; 2: move
+  // one block's exchange count so waits on its words run out).
+  int inject_exchange_fault(int mode, std::string* err);
   int n_layers() const { return shape_.n_layers; }
   int vocab() const { return shape_.vocab; }
   int capacity() const { return capacity_; }
@@ -171,6 +174,8 @@ class Engine {
   uint32_t* xflags_ = nullptr;    // [8, 32] per-block exchange counts
   uint32_t* err_ = nullptr;       // device error word of the cooperative kernels
   int check_device_error(std::string* err);
+  int probe_placement(bool* ok, std::string* err);
+  int clear_exchanges(std::string* err);
   float* inv_freq_ = nullptr;
   StepState* st_ = nullptr;
   uint32_t* prompt_ = nullptr;  // [capacity]

@@ -323,9 +323,11 @@ hipError_t launch_fill_normal_bf16(uint16_t* dst, size_t n, float sigma, uint64_
                                    hipStream_t s);
 // Device-to-device copy of `bytes` (a multiple of 16) by a plain kernel.
 hipError_t launch_copy16(void* dst, const void* src, size_t bytes, hipStream_t s);
-// Streaming read of `bytes` (multiple of 16); out: read16_out_bytes() scratch.
-size_t read16_out_bytes();
-hipError_t launch_read16(const void* src, size_t bytes, void* out, hipStream_t s);
+// Streaming read of `bytes` (a multiple of read_granule()) by global->LDS DMA;
+// out: read_out_bytes() of device scratch.
+size_t read_out_bytes();
+size_t read_granule();
+hipError_t launch_read(const void* src, size_t bytes, void* out, hipStream_t s);
 hipError_t launch_fill_normal_f32(float* dst, size_t n, float sigma, uint64_t seed,
                                   hipStream_t s);
 

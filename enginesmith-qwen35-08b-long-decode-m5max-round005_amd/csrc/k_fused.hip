@@ -7,10 +7,14 @@
 // from b >> 3. The 32 blocks of an XCD share its L2 and exchange data through
 // it (tagged words, below) at the cost of one store and one load, where any
 // exchange between XCDs costs a kernel boundary. The engine uses these kernels only
-// after a start-up probe has seen that dealing. Waits are bounded: a wait that
-// exceeds its spin limit (as it would if two blocks of one XCD shared a rank)
-// sets an error word, which the engine checks after each batch of steps, and
-// the block goes on.
+// after a start-up probe has seen that dealing. Waits are bounded and fail
+// fast: a wait that exceeds kSpinLimit polls (as it would if two blocks of one
+// XCD shared a rank) sets an error word; every 64th poll of any wait reads
+// that word and gives up once it is set, and a launch that starts with the
+// word set makes no wait at all. The kernels index nothing by exchanged
+// values, so a wait that gave up leaves wrong numbers but no stray access; the
+// engine checks the word after each batch of steps, reports the error, and
+// clears the word, the exchange counts and the exchange words.
 //
 // k_mlp_xcd: the MLP of a layer in one launch. It replaces the post-mixer
 // residual + post RMSNorm + gate/up + SwiGLU launch and the down-projection
@@ -28,12 +32,25 @@ namespace es {
 namespace {
 
 constexpr int kGroupBlocks = 32;          // blocks per XCD in a 256-block launch
-constexpr int kSpinLimit = 1 << 22;       // polls before a wait gives up
+constexpr int kSpinLimit = 1 << 16;       // polls before a wait gives up (tens of ms)
 
 __device__ __forceinline__ uint32_t xcc_id() {
   uint32_t v;
   asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(v));
   return v & 15u;
+}
+
+// After a failed poll n of a wait: true when the wait is to stop. Every 64th
+// poll checks the limit (setting the error word when it has run out) and reads
+// the error word that another wait may have set (an agent-scope load: the
+// word is set by atomics from any XCD).
+__device__ __forceinline__ bool wait_gives_up(int n, uint32_t* err) {
+  if ((n & 63) != 63) return false;
+  if (n >= kSpinLimit) {
+    atomicOr(err, 2u);
+    return true;
+  }
+  return __hip_atomic_load(err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0u;
 }
 
 // Exchanges within an XCD are tagged words: each published word holds a bf16
@@ -54,7 +71,7 @@ __device__ __forceinline__ uint32_t xcc_id() {
 // carries `tag`, and writes their values to lds (slice k of 32 at lds[36k ..]);
 // the block then syncs.
 __device__ __forceinline__ void xcd_gather(const uint32_t* words, int count, uint32_t tag, float* lds,
-                                           uint32_t* err) {
+                                           uint32_t* err, bool failed) {
   if (threadIdx.x < 64) {
     const int lane = threadIdx.x;
     const bool live = lane * 8 < count;
@@ -71,11 +88,7 @@ __device__ __forceinline__ void xcd_gather(const uint32_t* words, int count, uin
       bool ok = true;
 #pragma unroll
       for (int i = 0; i < 4; ++i) ok = ok && (w0[i] >> 16) == tag && (w1[i] >> 16) == tag;
-      if (__all(ok || !live)) break;
-      if (n >= kSpinLimit) {
-        if (lane == 0) atomicOr(err, 2u);
-        break;
-      }
+      if (__all(ok || !live) || failed || wait_gives_up(n, err)) break;
     }
     if (live) {
       float4* d = reinterpret_cast<float4*>(lds + (lane >> 2) * 36 + (lane & 3) * 8);
@@ -118,8 +131,10 @@ __global__ __launch_bounds__(256) void k_mlp_xcd(MlpXcdArgs a) {
   float4 pv[NPART];
 #pragma unroll
   for (int k = 0; k < NPART; ++k) pv[k] = reinterpret_cast<const float4*>(a.part + k * kHidden)[t];
-  // this block's exchange count as it left the previous launch
+  // this block's exchange count as it left the previous launch; the error
+  // word (set: make no wait)
   const uint32_t own = flags[rank];
+  const bool failed = *a.err != 0u;
   issue_fence();
   u32x4 cg[2], cu[2];
   uint32_t gsb[2], usb[2];
@@ -209,7 +224,7 @@ __global__ __launch_bounds__(256) void k_mlp_xcd(MlpXcdArgs a) {
   // ---- exchange the XCD's activation elements (hs is free again: the
   // norm's barrier followed its last read)
   if (t == 0) flags[rank] = own + 1u;
-  xcd_gather(xact, wide ? 512 : 256, tag, hs, a.err);
+  xcd_gather(xact, wide ? 512 : 256, tag, hs, a.err, failed);
 
   // ---- phase 2: octet x of every down row of this block
   // lane L's slice: elements 32L .. 32L+31 of the exchange
@@ -237,7 +252,7 @@ __global__ __launch_bounds__(256) void k_mlp_xcd(MlpXcdArgs a) {
 // XCD's L2 until the first carries tag0 and the second tag1; returns their
 // bf16 values.
 __device__ __forceinline__ uint2 xcd_poll2(const uint32_t* p0, uint32_t tag0, const uint32_t* p1, uint32_t tag1,
-                                           uint32_t* err) {
+                                           uint32_t* err, bool failed) {
   uint32_t a, b;
   for (int n = 0;; ++n) {
     asm volatile(
@@ -247,18 +262,14 @@ __device__ __forceinline__ uint2 xcd_poll2(const uint32_t* p0, uint32_t tag0, co
         : "=&v"(a), "=&v"(b)
         : "v"(p0), "v"(p1)
         : "memory");
-    if (__all((a >> 16) == tag0 && (b >> 16) == tag1)) break;
-    if (n >= kSpinLimit) {
-      atomicOr(err, 2u);
-      break;
-    }
+    if (__all((a >> 16) == tag0 && (b >> 16) == tag1) || failed || wait_gives_up(n, err)) break;
   }
   return make_uint2(a & 0xffffu, b & 0xffffu);
 }
 
 // The same for three words with one tag.
 __device__ __forceinline__ uint3 xcd_poll3(const uint32_t* p0, const uint32_t* p1, const uint32_t* p2, uint32_t tag,
-                                           uint32_t* err) {
+                                           uint32_t* err, bool failed) {
   uint32_t a, b, c;
   for (int n = 0;; ++n) {
     asm volatile(
@@ -269,11 +280,8 @@ __device__ __forceinline__ uint3 xcd_poll3(const uint32_t* p0, const uint32_t* p
         : "=&v"(a), "=&v"(b), "=&v"(c)
         : "v"(p0), "v"(p1), "v"(p2)
         : "memory");
-    if (__all((a >> 16) == tag && (b >> 16) == tag && (c >> 16) == tag)) break;
-    if (n >= kSpinLimit) {
-      atomicOr(err, 2u);
+    if (__all((a >> 16) == tag && (b >> 16) == tag && (c >> 16) == tag) || failed || wait_gives_up(n, err))
       break;
-    }
   }
   return make_uint3(a & 0xffffu, b & 0xffffu, c & 0xffffu);
 }
@@ -337,6 +345,7 @@ __global__ __launch_bounds__(256) void k_gdn_xcd(GdnXcdArgs a) {
   asm volatile("v_mov_b32 %0, 0" : "=v"(zero));
   const int pos = (&a.st->pos)[zero];
   const uint32_t own = flags[rank];
+  const bool failed = *a.err != 0u;  // set: make no wait
   issue_fence();
   // pass p: matrix p (q, k, v rows of in_proj_qkv, then z), channel 8j + hw
   u32x4 c[5];
@@ -475,7 +484,7 @@ __global__ __launch_bounds__(256) void k_gdn_xcd(GdnXcdArgs a) {
     // q/k word twice
     const uint32_t* qk_word = xb + (t < 128 ? kXq + t : kXk + (t - 128));
     const uint3 qkr = xcd_poll3(qk_word, xb + kXv + 8 * j + (t & 7), t == 8 || t == 9 ? xb + kXab + (t - 8) : qk_word,
-                                tag1, a.err);
+                                tag1, a.err, failed);
     const float v = bf2f(qkr.x);
     const float ss = tree64(v * v);
     if (lane == 0) red[wave] = ss;
@@ -527,7 +536,7 @@ __global__ __launch_bounds__(256) void k_gdn_xcd(GdnXcdArgs a) {
   const int hl = t >> 7, dl = t & 127;
   {
     const uint32_t* xh = a.xbuf + (size_t)(x * 2 + hl) * kHx;
-    const uint2 yz = xcd_poll2(xh + kXy + dl, tag2, xh + kXz + dl, tag1, a.err);
+    const uint2 yz = xcd_poll2(xh + kXy + dl, tag2, xh + kXz + dl, tag1, a.err, failed);
     yv[t] = bf2f(yz.x);
     xg[t + (t >> 5)] = bf2f(yz.y);  // z, replaced by the gated value below
   }

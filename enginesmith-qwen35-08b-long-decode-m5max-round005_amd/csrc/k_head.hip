@@ -303,21 +303,28 @@ __global__ __launch_bounds__(256) void k_copy16(u32x4* __restrict__ dst,
     dst[i] = __builtin_nontemporal_load(src + i);
 }
 
-// Plain streaming read: non-temporal 16-byte loads, four in flight per
-// thread, xor-folded; one 4-byte store per thread (out holds gridDim x 256
-// words). The measured read-only ceiling beside the nameplate HBM figure.
-__global__ __launch_bounds__(256) void k_read16(const u32x4* __restrict__ src, size_t n16, uint32_t* out) {
-  const size_t stride = (size_t)gridDim.x * blockDim.x;
-  size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
-  u32x4 acc = {0u, 0u, 0u, 0u};
-  for (; i + 3 * stride < n16; i += 4 * stride) {
-    const u32x4 a = __builtin_nontemporal_load(src + i), b = __builtin_nontemporal_load(src + i + stride);
-    const u32x4 c = __builtin_nontemporal_load(src + i + 2 * stride);
-    const u32x4 d = __builtin_nontemporal_load(src + i + 3 * stride);
-    acc ^= a ^ b ^ c ^ d;
+// Plain streaming read by global->LDS DMA, the fastest read pattern measured
+// on this part and so the read-only ceiling beside the nameplate HBM figure:
+// kReadBlocks blocks, each reading one contiguous chunk in 4 KB steps (wave w
+// takes the step's kilobyte w, one 16-byte DMA per lane), at most 12 DMAs in
+// flight per wave, into an LDS ring that nothing reads. One word per block is
+// stored so the launch has an output.
+constexpr int kReadBlocks = 256;
+typedef __attribute__((address_space(3))) void* read_lds_t;
+
+__global__ __launch_bounds__(256) void k_read_lds(const uint8_t* __restrict__ src, size_t chunk, uint32_t* out) {
+  __shared__ __attribute__((aligned(16))) uint32_t ring[4][16][256];
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const uint8_t* p = src + (size_t)blockIdx.x * chunk + (size_t)wave * 1024 + (size_t)lane * 16;
+  const size_t steps = chunk / 4096;
+  for (size_t i = 0; i < steps; ++i) {
+    __builtin_amdgcn_global_load_lds(p + i * 4096, (read_lds_t)&ring[wave][i & 15][0], 16, 0, kLoadNonTemporal);
+    // vmcnt(12): at most 12 of this wave's DMAs in flight
+    __builtin_amdgcn_s_waitcnt((12 & 15) | (7 << 4) | (15 << 8) | ((12 >> 4) << 14));
   }
-  for (; i < n16; i += stride) acc ^= __builtin_nontemporal_load(src + i);
-  out[(size_t)blockIdx.x * blockDim.x + threadIdx.x] = acc[0] ^ acc[1] ^ acc[2] ^ acc[3];
+  __builtin_amdgcn_s_waitcnt((7 << 4) | (15 << 8));  // vmcnt(0)
+  __syncthreads();
+  if (threadIdx.x == 0) out[blockIdx.x] = ring[0][0][0];
 }
 
 // Block partials of launch_head_noalloc, for callers that cannot allocate:
@@ -379,12 +386,13 @@ hipError_t launch_greedy(const uint16_t* logits, int count, float* part, uint32_
   return hipGetLastError();
 }
 
-size_t read16_out_bytes() { return (size_t)8192 * 256 * 4; }
+size_t read_out_bytes() { return (size_t)kReadBlocks * 4; }
+size_t read_granule() { return (size_t)kReadBlocks * 4096; }
 
-hipError_t launch_read16(const void* src, size_t bytes, void* out, hipStream_t s) {
-  if (!src || !out || bytes % 16 != 0 || bytes == 0) return hipErrorInvalidValue;
-  hipLaunchKernelGGL(k_read16, dim3(8192), dim3(256), 0, s, static_cast<const u32x4*>(src), bytes / 16,
-                     static_cast<uint32_t*>(out));
+hipError_t launch_read(const void* src, size_t bytes, void* out, hipStream_t s) {
+  if (!src || !out || bytes == 0 || bytes % read_granule() != 0) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(k_read_lds, dim3(kReadBlocks), dim3(256), 0, s, static_cast<const uint8_t*>(src),
+                     bytes / kReadBlocks, static_cast<uint32_t*>(out));
   return hipGetLastError();
 }
 

@@ -105,6 +105,7 @@ _SIGNATURES = {
     "es_engine_prompt_split": (c_int, [c_void_p, POINTER(c_int), POINTER(c_int), POINTER(c_int)]),
     "es_engine_xcd_kernels": (c_int, [c_void_p]),
     "es_engine_set_xcd_kernels": (c_int, [c_void_p, c_int]),
+    "es_engine_inject_exchange_fault": (c_int, [c_void_p, c_int]),
     "es_engine_cancel": (None, [c_void_p]),
     "es_engine_clear_cancel": (None, [c_void_p]),
     "es_engine_position": (c_int, [c_void_p]),
@@ -343,6 +344,12 @@ class Engine:
         per dependency (False); both give the same bits."""
         check(lib().es_engine_set_xcd_kernels(self.h, 1 if on else 0))
 
+    def inject_exchange_fault(self, mode: int) -> None:
+        """Test hook: 1 sets the device error word of the XCD-cooperative
+        kernels, 2 moves one block's exchange count so the waits on its words
+        run out; the next request then fails and the engine recovers."""
+        check(lib().es_engine_inject_exchange_fault(self.h, int(mode)))
+
     def prompt_split(self):
         """(batched chunks, routed rows, decode rows) of the last reset request."""
         c, r, d = c_int(), c_int(), c_int()
@@ -413,7 +420,8 @@ def splits_for(length: int) -> int:
 
 
 def time_read(nbytes: int, reps: int = 10) -> float:
-    """Average ms of the plain streaming-read kernel over nbytes."""
+    """Average ms of the streaming-read kernel (256 blocks, contiguous chunks
+    by global->LDS DMA) over nbytes, a multiple of 1 MiB."""
     src, out = DeviceBuffer(nbytes), DeviceBuffer(8 << 20)
     ms = c_double()
     try:

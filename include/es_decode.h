@@ -68,9 +68,11 @@ int es_copy_d2d(void* dst, const void* src, size_t bytes, void* stream);
  * the measured streaming-copy peak beside the nameplate HBM figure. */
 int es_time_copy_d2d(void* dst, const void* src, size_t bytes, int reps, double* ms_avg);
 /* Average ms of `reps` launches of a plain streaming-read kernel over `bytes`
- * (a multiple of 16) at src; out is device scratch of at least 8 MiB. No
- * reference counterpart: the measured read-only ceiling beside the nameplate
- * HBM figure, for kernels that only read. */
+ * (a multiple of 1 MiB) at src: 256 blocks, each reading a contiguous chunk
+ * by 16-byte global->LDS DMA, the fastest read pattern measured on MI355X;
+ * out is device scratch of at least 1 KiB. No reference counterpart: the
+ * measured read-only ceiling beside the nameplate HBM figure, for kernels
+ * that only read. */
 int es_time_read(const void* src, size_t bytes, void* out, size_t out_bytes, int reps, double* ms_avg);
 int es_synchronize(void);
 int es_stream_create(void** stream);
@@ -400,6 +402,17 @@ int es_engine_xcd_kernels(const es_engine* e);
  * reference counterpart: lets tests hold the two kernel sets to the same
  * bits. */
 int es_engine_set_xcd_kernels(es_engine* e, int on);
+/* Test hook for the failure path of the XCD-cooperative kernels' exchange
+ * waits, forced from the host so every kernel still exits normally. mode 1
+ * sets the device error word: every wait of the following launches gives up
+ * at once. mode 2 moves one block's exchange count away from its XCD's, so
+ * the waits on that block's words run to their spin limit (tens of
+ * milliseconds) and then every other wait gives up. The next request fails
+ * with ES_ERR_DEVICE ("decode kernels: an XCD exchange wait timed out"),
+ * after which the engine has cleared the error word, the counts and the
+ * exchange words, and the request after it runs normally. ES_ERR_INVALID
+ * when the XCD-cooperative kernels are off. No reference counterpart. */
+int es_engine_inject_exchange_fault(es_engine* e, int mode);
 
 /* How the last reset request consumed its prompt: batched chunks of
  * full-forward rows, rows of the routed last forward (0 or 2 .. 32), and

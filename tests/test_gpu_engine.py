@@ -152,6 +152,35 @@ def test_xcd_kernels_equal_per_dependency_launches(small):
             assert np.array_equal(a, b), n
 
 
+@pytest.mark.parametrize("mode", [1, 2])
+def test_exchange_fault_fails_fast_and_recovers(small, mode):
+    """The failure path of the XCD-cooperative kernels' exchange waits,
+    forced from the host (every kernel still exits normally). Mode 1 sets the
+    device error word, so every wait gives up at once; mode 2 moves one
+    block's exchange count, so the waits on its words run to their spin limit
+    and then every other wait gives up. Either way the request fails within a
+    second with the exchange error, and the next request returns the normal
+    tokens bit for bit on the XCD kernels."""
+    import time
+    eng, _, _ = small
+    assert eng.xcd_kernels()
+    r = rng(48 + mode)
+    prompt = r.integers(0, SMALL["vocab"], 24).tolist()
+    want = eng.generate(prompt, 40, reset=True)   # 2 batches of 16 + 8
+    print(f"case exchange fault mode {mode}", flush=True)
+    eng.inject_exchange_fault(mode)
+    t0 = time.perf_counter()
+    with pytest.raises(E.EsError) as ei:
+        eng.generate(prompt, 40, reset=True)
+    took = time.perf_counter() - t0
+    assert ei.value.code == E.ES_ERR_DEVICE
+    assert "XCD exchange wait timed out" in str(ei.value)
+    assert took < 1.0, f"the failed request took {took:.2f} s"
+    assert eng.xcd_kernels()
+    assert eng.generate(prompt, 40, reset=True) == want
+    assert eng.generate(prompt, 40, reset=True) == want
+
+
 def test_reset_isolation(small):
     eng, _, _ = small
     r = rng(44)

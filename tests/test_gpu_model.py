@@ -77,13 +77,13 @@ def test_full_model_teacher_forced_agreement(full):
 
 
 @pytest.mark.timeout(900)
-@pytest.mark.parametrize("ctx,steps", [(32768, 257), (65536, 64), (131072, 64)])
+@pytest.mark.parametrize("ctx,steps", [(32768, 257), (65536, 257), (131072, 257)])
 def test_long_context_agreement_after_batched_prefill(ctx, steps):
-    """Full model (the 257-token decode at 32K, 64 steps at 64K and 128K): a
-    prompt of `ctx` uniform-random ids consumed by the batched prefill, then
-    greedy tokens; the post-prefill state is handed to the oracle and the
-    stream judged teacher-forced: at most 1% of the steps mismatch (the >= 99%
-    agreement bar), every mismatch a near tie, and the harness's gates hold."""
+    """Full model, the 257-token decode at every context: a prompt of `ctx`
+    uniform-random ids consumed by the batched prefill, then greedy tokens;
+    the post-prefill state is handed to the oracle and the stream judged
+    teacher-forced: at most 1% of the steps mismatch (the >= 99% agreement
+    bar, 2 of 257), every mismatch a near tie, and the harness's gates hold."""
     from judge import gates
     print(f"case long context {ctx}", flush=True)
     blob = E.random_weights(N_LAYERS, VOCAB, seed=20260101, threads=16)
