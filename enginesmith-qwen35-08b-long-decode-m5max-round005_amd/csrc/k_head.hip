@@ -305,22 +305,22 @@ __global__ __launch_bounds__(256) void k_copy16(u32x4* __restrict__ dst,
 
 // Plain streaming read by global->LDS DMA, the fastest read pattern measured
 // on this part and so the read-only ceiling beside the nameplate HBM figure:
-// kReadBlocks blocks, each reading one contiguous chunk in 4 KB steps (wave w
-// takes the step's kilobyte w, one 16-byte DMA per lane), at most 12 DMAs in
-// flight per wave, into an LDS ring that nothing reads. One word per block is
-// stored so the launch has an output.
+// kReadBlocks blocks of 8 waves, each block reading one contiguous chunk in
+// 8 KB steps (wave w takes the step's kilobyte w, one 16-byte DMA per lane),
+// waiting after every fourth DMA of a wave until at most three are in
+// flight, into an LDS ring that nothing reads. One word per block is stored
+// so the launch has an output.
 constexpr int kReadBlocks = 256;
 typedef __attribute__((address_space(3))) void* read_lds_t;
 
-__global__ __launch_bounds__(256) void k_read_lds(const uint8_t* __restrict__ src, size_t chunk, uint32_t* out) {
-  __shared__ __attribute__((aligned(16))) uint32_t ring[4][16][256];
+__global__ __launch_bounds__(512) void k_read_lds(const uint8_t* __restrict__ src, size_t chunk, uint32_t* out) {
+  __shared__ __attribute__((aligned(16))) uint32_t ring[8][4][256];
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const uint8_t* p = src + (size_t)blockIdx.x * chunk + (size_t)wave * 1024 + (size_t)lane * 16;
-  const size_t steps = chunk / 4096;
+  const size_t steps = chunk / 8192;
   for (size_t i = 0; i < steps; ++i) {
-    __builtin_amdgcn_global_load_lds(p + i * 4096, (read_lds_t)&ring[wave][i & 15][0], 16, 0, kLoadNonTemporal);
-    // vmcnt(12): at most 12 of this wave's DMAs in flight
-    __builtin_amdgcn_s_waitcnt((12 & 15) | (7 << 4) | (15 << 8) | ((12 >> 4) << 14));
+    __builtin_amdgcn_global_load_lds(p + i * 8192, (read_lds_t)&ring[wave][i & 3][0], 16, 0, kLoadNonTemporal);
+    if ((i & 3) == 3) __builtin_amdgcn_s_waitcnt(3 | (7 << 4) | (15 << 8));  // vmcnt(3)
   }
   __builtin_amdgcn_s_waitcnt((7 << 4) | (15 << 8));  // vmcnt(0)
   __syncthreads();
@@ -387,11 +387,11 @@ hipError_t launch_greedy(const uint16_t* logits, int count, float* part, uint32_
 }
 
 size_t read_out_bytes() { return (size_t)kReadBlocks * 4; }
-size_t read_granule() { return (size_t)kReadBlocks * 4096; }
+size_t read_granule() { return (size_t)kReadBlocks * 8192; }
 
 hipError_t launch_read(const void* src, size_t bytes, void* out, hipStream_t s) {
   if (!src || !out || bytes == 0 || bytes % read_granule() != 0) return hipErrorInvalidValue;
-  hipLaunchKernelGGL(k_read_lds, dim3(kReadBlocks), dim3(256), 0, s, static_cast<const uint8_t*>(src),
+  hipLaunchKernelGGL(k_read_lds, dim3(kReadBlocks), dim3(512), 0, s, static_cast<const uint8_t*>(src),
                      bytes / kReadBlocks, static_cast<uint32_t*>(out));
   return hipGetLastError();
 }

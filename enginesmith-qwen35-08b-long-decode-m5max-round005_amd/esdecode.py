@@ -421,7 +421,7 @@ def splits_for(length: int) -> int:
 
 def time_read(nbytes: int, reps: int = 10) -> float:
     """Average ms of the streaming-read kernel (256 blocks, contiguous chunks
-    by global->LDS DMA) over nbytes, a multiple of 1 MiB."""
+    by global->LDS DMA) over nbytes, a multiple of 2 MiB."""
     src, out = DeviceBuffer(nbytes), DeviceBuffer(8 << 20)
     ms = c_double()
     try:

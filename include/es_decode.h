@@ -68,7 +68,7 @@ int es_copy_d2d(void* dst, const void* src, size_t bytes, void* stream);
  * the measured streaming-copy peak beside the nameplate HBM figure. */
 int es_time_copy_d2d(void* dst, const void* src, size_t bytes, int reps, double* ms_avg);
 /* Average ms of `reps` launches of a plain streaming-read kernel over `bytes`
- * (a multiple of 1 MiB) at src: 256 blocks, each reading a contiguous chunk
+ * (a multiple of 2 MiB) at src: 256 blocks, each reading a contiguous chunk
  * by 16-byte global->LDS DMA, the fastest read pattern measured on MI355X;
  * out is device scratch of at least 1 KiB. No reference counterpart: the
  * measured read-only ceiling beside the nameplate HBM figure, for kernels

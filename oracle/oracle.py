@@ -12,6 +12,7 @@ import subprocess
 from ctypes import POINTER, c_float, c_int, c_uint16, c_uint32, c_void_p
 
 import numpy as np
+import xxhash
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libesoracle.so")
@@ -173,11 +174,18 @@ _DEQUANT_CACHE: dict = {}
 _DEQUANT_CACHE_BYTES = 1 << 30
 
 
+def _fingerprint(a):
+    """64-bit hash of an array's bytes (a weight changed in place gets a new key)."""
+    return xxhash.xxh3_64_intdigest(memoryview(np.ascontiguousarray(a)).cast("B"))
+
+
 def _dequant_cached(codes, scales, biases):
     """q4_dequant_bf16 of a weight as fp64, kept (the codes array with it, so
-    its address stays unique) until the cache passes 1 GiB, oldest first."""
+    its address stays unique) until the cache passes 1 GiB, oldest first. The
+    key holds the arrays' addresses and a hash of their contents, so a weight
+    modified in place after its first use is dequantised again."""
     key = (codes.__array_interface__["data"][0], codes.shape, scales.__array_interface__["data"][0],
-           biases.__array_interface__["data"][0])
+           biases.__array_interface__["data"][0], _fingerprint(codes), _fingerprint(scales), _fingerprint(biases))
     hit = _DEQUANT_CACHE.get(key)
     if hit is not None:
         return hit[0]

@@ -168,3 +168,20 @@ def test_q4_gemm_dequant_rounding_and_rows():
     res = bf16(r.normal(0, 1, (m, n)))
     ya = O.q4_gemm(codes, scales, biases, x, residual=res)
     assert np.array_equal(ya, bf16(f32(res) + f32(y)))
+
+
+def test_q4_gemm_sees_weights_changed_in_place():
+    """The oracle's cache of dequantised GEMM weights is keyed by content as
+    well as address: rows planted into a weight after its first use (as the
+    head tests plant rows) change the result."""
+    r = rng(90)
+    codes, scales, biases = random_q4(r, 64, 1024)
+    x = bf16(r.normal(0, 1, (3, 1024)))
+    before = O.q4_gemm(codes, scales, biases, x)
+    codes[5] ^= np.uint32(0xFFFFFFFF)
+    scales[7] = bf16(np.full(16, 0.5))
+    after = O.q4_gemm(codes, scales, biases, x)
+    fresh = O.q4_gemm(codes.copy(), scales.copy(), biases.copy(), x)
+    assert np.array_equal(after, fresh)
+    assert not np.array_equal(after[:, 5], before[:, 5])
+    assert not np.array_equal(after[:, 7], before[:, 7])
