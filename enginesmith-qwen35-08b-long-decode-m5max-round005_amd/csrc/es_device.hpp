@@ -354,15 +354,18 @@ struct Q4 {
 // table: the lane's 32 elements sl*32 .. +31 of row tok. The table is taken
 // by value: a reference into the kernel-argument struct made the compiler copy
 // the whole struct to per-thread scratch memory.
-__device__ __forceinline__ void embed_slice(Q4 e, uint32_t tok, int sl, float* xv) {
-  if (tok >= (uint32_t)e.n) tok = 0;  // ids come from validated prompts or the head's argmax
-  const u32x4 c = *reinterpret_cast<const u32x4*>(e.w + (size_t)tok * 128 + sl * 4);
-  const float sc = bf2f(e.s[(size_t)tok * 16 + sl / 2]);
-  const float bi = bf2f(e.b[(size_t)tok * 16 + sl / 2]);
+// The same from a slice's loaded code word and raw bf16 scale and bias.
+__device__ __forceinline__ void embed_convert(const u32x4 c, uint32_t scale, uint32_t bias, float* xv) {
+  const float sc = bf2f(scale), bi = bf2f(bias);
 #pragma unroll
   for (int w = 0; w < 4; ++w)
 #pragma unroll
     for (int j = 0; j < 8; ++j) xv[8 * w + j] = rbf(fmaf(sc, (float)((c[w] >> (4 * j)) & 15u), bi));
+}
+__device__ __forceinline__ void embed_slice(Q4 e, uint32_t tok, int sl, float* xv) {
+  if (tok >= (uint32_t)e.n) tok = 0;  // ids come from validated prompts or the head's argmax
+  const u32x4 c = *reinterpret_cast<const u32x4*>(e.w + (size_t)tok * 128 + sl * 4);
+  embed_convert(c, e.s[(size_t)tok * 16 + sl / 2], e.b[(size_t)tok * 16 + sl / 2], xv);
 }
 
 // Device-resident decode cursor shared by every kernel of a step.

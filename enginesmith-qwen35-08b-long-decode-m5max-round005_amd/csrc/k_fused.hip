@@ -132,9 +132,9 @@ __global__ __launch_bounds__(256) void k_mlp_xcd(MlpXcdArgs a) {
 #pragma unroll
   for (int k = 0; k < NPART; ++k) pv[k] = reinterpret_cast<const float4*>(a.part + k * kHidden)[t];
   // this block's exchange count as it left the previous launch; the error
-  // word (set: make no wait)
+  // word (set: make no wait), first used at the exchange
   const uint32_t own = flags[rank];
-  const bool failed = *a.err != 0u;
+  uint32_t err_raw = *a.err;
   issue_fence();
   u32x4 cg[2], cu[2];
   uint32_t gsb[2], usb[2];
@@ -224,7 +224,11 @@ __global__ __launch_bounds__(256) void k_mlp_xcd(MlpXcdArgs a) {
   // ---- exchange the XCD's activation elements (hs is free again: the
   // norm's barrier followed its last read)
   if (t == 0) flags[rank] = own + 1u;
-  xcd_gather(xact, wide ? 512 : 256, tag, hs, a.err, failed);
+  // the error word is read here, not at entry: a uniform value formed from a
+  // load right after it would wait for every input load before the weights
+  // are issued
+  asm volatile("" : "+v"(err_raw));
+  xcd_gather(xact, wide ? 512 : 256, tag, hs, a.err, err_raw != 0u);
 
   // ---- phase 2: octet x of every down row of this block
   // lane L's slice: elements 32L .. 32L+31 of the exchange
@@ -345,7 +349,20 @@ __global__ __launch_bounds__(256) void k_gdn_xcd(GdnXcdArgs a) {
   asm volatile("v_mov_b32 %0, 0" : "=v"(zero));
   const int pos = (&a.st->pos)[zero];
   const uint32_t own = flags[rank];
-  const bool failed = *a.err != 0u;  // set: make no wait
+  uint32_t err_raw = *a.err;  // set: make no wait (first used at the first exchange)
+  // layer 0: the input is the token's embedding row. Its loads go before the
+  // weights (loads complete in issue order, so the norm would otherwise wait
+  // for every weight load), at the cost of a wait here for the token and the
+  // few loads issued before it.
+  u32x4 emb_c = {0u, 0u, 0u, 0u};
+  uint32_t emb_s = 0u, emb_b = 0u;
+  if (EMBED) {
+    uint32_t tok = __builtin_amdgcn_readfirstlane((&a.st->token)[zero]);
+    if (tok >= (uint32_t)a.embed.n) tok = 0;  // ids come from validated prompts or the head's argmax
+    emb_c = *reinterpret_cast<const u32x4*>(a.embed.w + (size_t)tok * 128 + sl * 4);
+    emb_s = a.embed.s[(size_t)tok * 16 + sl / 2];
+    emb_b = a.embed.b[(size_t)tok * 16 + sl / 2];
+  }
   issue_fence();
   // pass p: matrix p (q, k, v rows of in_proj_qkv, then z), channel 8j + hw
   u32x4 c[5];
@@ -410,8 +427,7 @@ __global__ __launch_bounds__(256) void k_gdn_xcd(GdnXcdArgs a) {
   // ---- phase 1: input, RMSNorm, projection rows, ring, convolution
   float xv[32];
   if (EMBED) {
-    const uint32_t tok = a.st->token;
-    embed_slice(a.embed, tok, sl, xv);
+    embed_convert(emb_c, emb_s, emb_b, xv);
     if (blockIdx.x == 0 && t < 32) store_bf16x32(a.h_out + sl * 32, xv);
   } else {
     const float hf[4] = {bf_lo(x4.x), bf_hi(x4.x), bf_lo(x4.y), bf_hi(x4.y)};
@@ -479,6 +495,11 @@ __global__ __launch_bounds__(256) void k_gdn_xcd(GdnXcdArgs a) {
   if (t == 0) flags[rank] = own + 2u;  // this launch's two exchanges
 
   // ---- phase 2: q/k L2 norms (k_gdn_recur_out's order), gates, delta rule
+  // (the error word is used from here on, not at entry: a uniform value
+  // formed from a load right after it would wait for every input load before
+  // the weights are issued)
+  asm volatile("" : "+v"(err_raw));
+  const bool failed = err_raw != 0u;
   {
     // lanes 8 and 9 also read a and b (the same exchange), the others their
     // q/k word twice
