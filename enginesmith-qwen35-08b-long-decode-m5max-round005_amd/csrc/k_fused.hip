@@ -546,9 +546,6 @@ __global__ __launch_bounds__(256) void k_gdn_xcd(GdnXcdArgs a) {
       out = fmaf(S[i], qq[i], out);
     }
     out = tree16(out);
-    f32x4* sp = reinterpret_cast<f32x4*>(a.state + ((size_t)(h * 128 + srow)) * 128 + 8 * sj);
-    __builtin_nontemporal_store(f32x4{S[0], S[1], S[2], S[3]}, sp);
-    __builtin_nontemporal_store(f32x4{S[4], S[5], S[6], S[7]}, sp + 1);
     if (sj == 0) xb[kXy + srow] = f2bf(out) | tag2 << 16;
   }
 
@@ -560,6 +557,13 @@ __global__ __launch_bounds__(256) void k_gdn_xcd(GdnXcdArgs a) {
     const uint2 yz = xcd_poll2(xh + kXy + dl, tag2, xh + kXz + dl, tag1, a.err, failed);
     yv[t] = bf2f(yz.x);
     xg[t + (t >> 5)] = bf2f(yz.y);  // z, replaced by the gated value below
+  }
+  // the updated state rows, stored after the exchange's poll: a store issued
+  // before it would hold the poll's wait until the store is acknowledged
+  if (t < 128) {
+    f32x4* sp = reinterpret_cast<f32x4*>(a.state + ((size_t)(h * 128 + srow)) * 128 + 8 * sj);
+    __builtin_nontemporal_store(f32x4{S[0], S[1], S[2], S[3]}, sp);
+    __builtin_nontemporal_store(f32x4{S[4], S[5], S[6], S[7]}, sp + 1);
   }
   __syncthreads();
   if (dl < 16) {  // lanes 0-15 of waves 0 and 2
